@@ -1,0 +1,206 @@
+"""Qwen3 decode benchmark on one MI355X (BASELINE metric: decode tok/s + % HBM roofline,
+Qwen3-0.6B shape, batch 1; prefill tok/s).
+
+Workload: Qwen3-0.6B shape, fp32 weights, random init N(0, 0.02) from a
+seed (synthetic; no checkpoint), prompt of 128 uniform random token ids, greedy decode.  A
+"step" is one decode token.  The prompt (positions 0..127) and `--warmup` tokens run untimed;
+then exactly `--steps` tokens are timed with the tokens kept on the device (no host round
+trip inside the timed region).  Default: warmup 5 + 251 timed = the config's 256 decode tokens.
+
+Extra fields on the JSON line:
+  roofline      dominant kernel's achieved HBM GB/s, from HIP events bracketing every launch
+                of that kernel class on the model's stream over a probe pass of --probe-steps
+  cpu_baseline  the CPU oracle (reference semantics, fp32) on this host, over a bounded sample
+  prefill       prompt throughput through the same decode-step path (token by token)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes_per_token(cfg, pos):
+    """Bytes one decode step must move at position `pos` (weights once + KV read/write)."""
+    wb = 4 if cfg.weight_dtype == 0 else 2
+    layer_w = cfg.layer_weight_params() * wb
+    norms = (2 * cfg.dim + cfg.q_dim + cfg.kv_dim) * 4
+    head = cfg.vocab_size * cfg.dim * wb
+    kv = cfg.layer_count * 2 * cfg.kv_dim * 4 * (pos + 1)
+    return cfg.layer_count * (layer_w + norms) + head + cfg.dim * 4 + kv
+
+
+def kernel_bytes(cfg, which, batch=1):
+    from common_amd import qwen3 as q
+    wb = 4 if cfg.weight_dtype == 0 else 2
+    d, F, V = cfg.dim, cfg.hidden_dim, cfg.vocab_size
+    act = 4 * batch
+    if which == q.KT_LOGITS:
+        return V * d * wb + d * 4 + d * act
+    if which == q.KT_GATE_UP:
+        return 2 * F * d * wb + d * 4 + d * act + F * act
+    if which == q.KT_QKV:
+        n = cfg.q_dim + 2 * cfg.kv_dim
+        return n * d * wb + d * 4 + d * act + n * act
+    if which == q.KT_DOWN:
+        return d * F * wb + F * act + 2 * d * act
+    if which == q.KT_O:
+        return d * cfg.q_dim * wb + cfg.q_dim * act + 2 * d * act
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=251)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--probe-steps", type=int, default=16)
+    ap.add_argument("--cpu-steps", type=int, default=160, help="oracle steps timed for the CPU baseline (0: skip)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the path has no "
+              f"collectives. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    from common_amd import config as C
+    from common_amd import qwen3 as q
+    from common_amd import synthetic
+    from common_amd.qwen3 import Qwen3
+
+    cfg = C.C3_0_6B
+    n_prompt = C.C3_PROMPT
+    total = n_prompt + args.warmup + args.steps + args.probe_steps
+    if total > cfg.seq_len:
+        import dataclasses
+        cfg = dataclasses.replace(cfg, seq_len=total)
+    prompt = synthetic.prompt_ids(n_prompt, cfg.vocab_size, seed=args.seed)
+
+    t0 = time.time()
+    model = Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed))
+    info = model.ctx.info()
+    log(f"[bench] weights generated + uploaded in {time.time() - t0:.1f}s on {info}")
+    am = model.model
+    am.use_graph(not args.no_graph)
+    am.reset()
+    am.set_prompt(prompt)
+
+    # prompt through the decode path (token by token, as AutoregressiveModel feeds it)
+    model.ctx.synchronize()
+    tp = time.perf_counter()
+    fed_prompt = am.run(n_prompt)
+    prefill_s = time.perf_counter() - tp
+    warm = am.run(args.warmup) if args.warmup else np.zeros((1, 0), np.int32)
+
+    # ---- timed region ----------------------------------------------------------------
+    model.ctx.synchronize()
+    t1 = time.perf_counter()
+    toks = am.run(args.steps)  # enqueues K steps, synchronises once at the end
+    t2 = time.perf_counter()
+    elapsed = t2 - t1
+    tok_s = args.steps / elapsed
+    ms = 1000.0 * elapsed / args.steps
+    pos0 = n_prompt + args.warmup
+    mean_bytes = float(np.mean([algorithmic_bytes_per_token(cfg, p) for p in range(pos0, pos0 + args.steps)]))
+    e2e_gbs = mean_bytes * tok_s / 1e9
+    log(f"[bench] decode {args.steps} tokens: {ms:.3f} ms/token, {tok_s:.1f} tok/s, "
+        f"{e2e_gbs:.0f} GB/s algorithmic ({100 * e2e_gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+
+    # ---- per-kernel probe: HIP events around each launch of one kernel class ----------
+    kernels = {}
+    names = {q.KT_LOGITS: "logits_gemv_argmax", q.KT_GATE_UP: "gate_up_gemv_swiglu", q.KT_QKV: "qkv_gemv_rmsnorm",
+             q.KT_DOWN: "down_gemv_residual", q.KT_O: "o_gemv_residual", q.KT_ATTENTION: "attention_decode"}
+    probe_left = cfg.seq_len - (pos0 + args.steps)
+    per_class = max(1, min(args.probe_steps, probe_left // len(names))) if probe_left >= len(names) else 0
+    for which, name in names.items():
+        if per_class == 0:
+            break
+        am.kernel_timing(which)
+        am.run(per_class)
+        ms_k, n_k = am.kernel_time()
+        am.kernel_timing(q.KT_NONE)
+        avg_us = 1000.0 * ms_k / max(n_k, 1)
+        per_tok_us = 1000.0 * ms_k / per_class
+        b = kernel_bytes(cfg, which)
+        kernels[name] = {"avg_us": round(avg_us, 3), "launches": n_k, "us_per_token": round(per_tok_us, 2),
+                         "bytes_per_launch": b, "GBs": round(b / avg_us / 1e3, 1) if b else None}
+        log(f"[bench] {name}: {avg_us:.2f} us/launch x {n_k // per_class}/token"
+            + (f" = {b / avg_us / 1e3:.0f} GB/s" if b else ""))
+    dom = max((k for k in kernels if kernels[k]["GBs"]), key=lambda k: kernels[k]["us_per_token"], default=None)
+    roofline = None
+    if dom:
+        kd = kernels[dom]
+        roofline = {"bound": "hbm", "kernel": dom, "achieved": kd["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                    "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": kd["avg_us"]}
+    model.close()
+
+    # ---- CPU baseline: the oracle (reference semantics, fp32) on this host -------------
+    cpu = None
+    parity = None
+    if args.cpu_steps > 0:
+        import oracle
+        nproc = os.cpu_count() or 1
+        threads = oracle.set_threads(max(2, nproc // 2))
+        ref = oracle.OracleQwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed), precision="fp32")
+        n = min(args.cpu_steps, n_prompt + args.warmup + args.steps)
+        gpu_fed = np.concatenate([fed_prompt[0], warm[0], toks[0]])
+        tc = time.perf_counter()
+        fed, _ = ref.generate(prompt[:min(n, n_prompt)], max(0, n - n_prompt), want_logits=False)
+        cpu_s = time.perf_counter() - tc
+        ref.close()
+        steps_done = n
+        cpu = {"value": round(steps_done / cpu_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"first {steps_done} steps of the workload (prompt tokens 0..{min(n, n_prompt) - 1} fed one "
+                         f"per step as the reference does, then {max(0, n - n_prompt)} greedy tokens), oracle fp32, "
+                         f"{threads} OpenMP threads of {nproc} ({platform.processor() or platform.machine()})"}
+        if n > n_prompt:
+            match = int(np.sum(fed[:n] == gpu_fed[:n]))
+            parity = {"steps_compared": n, "tokens_equal": match, "all_equal": bool(match == n)}
+        log(f"[bench] cpu oracle: {cpu['value']} tok/s over {steps_done} steps ({cpu_s:.1f}s), parity {parity}")
+
+    out = {
+        "metric": "decode tok/s (Qwen3-0.6B shape, b=1)",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
+        "config": {"workload": "C3: Qwen3-0.6B shape fp32 (d1024, 28L, 16Q/8KV, hd128, F3072, V151936), "
+                               "batch 1, prompt 128, greedy decode",
+                   "decode_positions": f"{pos0}..{pos0 + args.steps - 1}", "graph": not args.no_graph},
+        "hbm": {"algorithmic_bytes_per_token": round(mean_bytes), "achieved_GBs": round(e2e_gbs, 1),
+                "frac_of_peak": round(e2e_gbs / HBM_PEAK_GBS, 4)},
+        "prefill": {"tok_s": round(n_prompt / prefill_s, 1), "tokens": n_prompt,
+                    "path": "token-by-token through the decode step (reference AutoregressiveModel semantics)"},
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

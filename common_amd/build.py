@@ -1,0 +1,74 @@
+"""Builds the native libraries in-tree (common_amd/lib/), for gfx950 only.
+
+  libar_hip.so    HIP kernels + C-ABI (hipcc, --offload-arch=gfx950)
+  libar_synth.so  seeded synthetic-input generator (gcc, host only)
+
+Every HIP translation unit is compiled with packed-FP32 instructions disabled.
+Run: python -m common_amd.build
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "lib")
+OBJ = os.path.join(HERE, "lib", "obj")
+ARCH = "gfx950"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics",
+]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("build step failed:\n  " + " ".join(cmd) + "\n" + r.stdout)
+    return r.stdout
+
+
+def build_synth():
+    src = os.path.join(CSRC, "synth", "ar_synth.c")
+    out = os.path.join(LIB, "libar_synth.so")
+    _run(["gcc", "-O2", "-fopenmp", "-fPIC", "-shared", "-std=c11", "-o", out + ".tmp", src, "-lm"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_hip(jobs: int = 8):
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    os.makedirs(OBJ, exist_ok=True)
+
+    def compile_one(src):
+        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+        _run([HIPCC, *HIP_FLAGS, "-I", os.path.join(HERE, "..", "include"), "-c", src, "-o", obj])
+        return obj
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, srcs))
+    out = os.path.join(LIB, "libar_hip.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", *objs])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build(jobs: int = 8):
+    os.makedirs(LIB, exist_ok=True)
+    if shutil.which("gcc") is None:
+        raise RuntimeError("gcc not found")
+    paths = [build_synth(), build_hip(jobs)]
+    return paths
+
+
+if __name__ == "__main__":
+    for p in build(int(sys.argv[1]) if len(sys.argv) > 1 else 8):
+        print("built", p)

@@ -1,0 +1,142 @@
+// Internal declarations shared by the HIP backend translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/ar_hip.h"
+
+// ---- error channel ---------------------------------------------------------------
+// Every C-ABI entry point returns an AR_HIP_* code; the message for the calling thread
+// is kept here and returned by ar_hip_last_error().
+void ar_set_error(const char* fmt, ...);
+void ar_clear_error();
+
+#define AR_CHECK_ARG(cond, ...)                  \
+    do {                                         \
+        if (!(cond)) {                           \
+            ar_set_error(__VA_ARGS__);           \
+            return AR_HIP_ERR_INVALID;           \
+        }                                        \
+    } while (0)
+
+#define AR_HIP_TRY(expr)                                                                   \
+    do {                                                                                   \
+        hipError_t _e = (expr);                                                            \
+        if (_e != hipSuccess) {                                                            \
+            ar_set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, \
+                         __LINE__);                                                        \
+            return AR_HIP_ERR_HIP;                                                         \
+        }                                                                                  \
+    } while (0)
+
+#define AR_TRY(expr)                 \
+    do {                             \
+        int _rc = (expr);            \
+        if (_rc != AR_HIP_OK) return _rc; \
+    } while (0)
+
+#define AR_LAUNCH_CHECK()                                                                 \
+    do {                                                                                  \
+        hipError_t _e = hipGetLastError();                                                \
+        if (_e != hipSuccess) {                                                           \
+            ar_set_error("kernel launch failed: %s (%s:%d)", hipGetErrorString(_e),       \
+                         __FILE__, __LINE__);                                             \
+            return AR_HIP_ERR_HIP;                                                        \
+        }                                                                                 \
+    } while (0)
+
+// ---- data / compute context ------------------------------------------------------
+struct ar_hip_ctx {
+    int device = 0;
+    int num_cus = 0;
+    size_t hbm_bytes = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    std::unordered_map<void*, size_t> device_allocs;  // memory-provider bookkeeping
+    std::unordered_map<void*, size_t> host_allocs;
+    size_t device_bytes = 0;
+};
+
+// Device allocation owned by the context's memory provider.
+int ar_ctx_alloc(ar_hip_ctx* ctx, size_t bytes, void** out);
+int ar_ctx_free(ar_hip_ctx* ctx, void* p);
+
+// ---- kernel launchers (device pointers, enqueue on `stream`) ----------------------
+struct GemvLaunch {
+    const void* w = nullptr;       // rows x cols, row-major, weight dtype
+    const void* w2 = nullptr;      // second matrix (SwiGLU up projection), same shape
+    int wdtype = AR_DTYPE_F32;
+    int rows = 0, cols = 0, batch = 1;
+    const float* x = nullptr;      // [batch][x_stride]
+    int x_stride = 0;
+    const float* norm_w = nullptr; // RMSNorm gain over cols (prologue), or null
+    float eps = 1e-6f;
+    const float* bias = nullptr;   // [rows] or null
+    float* y = nullptr;            // [batch][y_stride]
+    int y_stride = 0;
+    int epilogue = 0;              // GEMV_EPI_*
+    // argmax epilogue
+    float* part_val = nullptr;     // [grid][batch]
+    int* part_idx = nullptr;
+    unsigned* counter = nullptr;   // zero before first use; the last block resets it
+    int* tokens = nullptr;         // [batch][token_stride]
+    int token_stride = 0;
+    int* state = nullptr;          // device {position, prompt length}: tokens[pos+1] is written only
+                                   // when pos+1 >= prompt length; advance=1 increments position
+    int advance = 0;
+};
+
+enum {
+    GEMV_EPI_STORE = 0,     // y = W x (+ b)
+    GEMV_EPI_RESIDUAL = 1,  // y += W x
+    GEMV_EPI_SWIGLU = 2,    // y = (W2 x) * silu(W x)
+    GEMV_EPI_ARGMAX = 3,    // optional y = W x; greedy token; optional position advance
+};
+
+int launch_gemv(const GemvLaunch& a, hipStream_t stream);
+int gemv_argmax_partials(int rows, int batch);  // partial slots the argmax epilogue needs
+
+struct AttnLaunch {
+    const float* qkv = nullptr;   // [batch][qkv_stride]: q | k | v raw projections
+    int qkv_stride = 0;
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+    float qk_eps = 1e-6f;
+    int per_head_norm = 0;
+    float* kcache = nullptr;      // [batch][kv_heads][max_seq][hd]
+    float* vcache = nullptr;
+    int max_seq = 0;
+    const int* pos = nullptr;     // device position (same for every sequence)
+    int heads = 0, kv_heads = 0, head_dim = 0;
+    double rope_theta = 1e6;
+    int tile = 64;                // positions per split
+    int max_splits = 0;           // grid.x (splits past the live context exit at once)
+    float* part_o = nullptr;      // [batch][heads][max_splits][hd]
+    float* part_ml = nullptr;     // [batch][heads][max_splits][2]
+    unsigned* counters = nullptr; // [batch][kv_heads], zero before first use
+    float* out = nullptr;         // [batch][out_stride]
+    int out_stride = 0;
+    int batch = 1;
+};
+
+int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
+size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);
+
+int launch_embed(const void* table, int wdtype, int dim, const int* tokens, int token_stride,
+                 const int* pos, int batch, float* x, int x_stride, hipStream_t stream);
+int launch_rmsnorm(const float* x, const float* w, float* y, int rows, int n, float eps,
+                   hipStream_t stream);
+int launch_rope(float* x, int heads, int hd, int pos, double theta, int rows, int row_stride,
+                hipStream_t stream);
+int launch_index_of_max(const float* x, int rows, int n, int* out, hipStream_t stream);
+int launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream);
+int launch_fill_i32(int* dst, int value, size_t n, hipStream_t stream);
+
+void ar_ops_release(ar_hip_ctx* ctx);

@@ -1,0 +1,371 @@
+// Decode-step grouped-query attention with the QK-norm / RoPE / KV-cache-write prologue fused in.
+//
+// One launch covers what the reference builds as a chain of graph ops per layer
+// (engine/ml/.../AttentionFeatures.java:785-929):
+//   QK-norm        rmsnorm over the whole q / k vector (:840-845, :886-891) or per head
+//   split-half RoPE reshapeToSplitHalfRope + ropeRotation + reshapeFromSplitHalfRope
+//                  (:195-237; RotationFeatures.java:124-208), angles pos * exp(f * -2 ln(theta)/hd)
+//                  evaluated in double
+//   cache write    k, v at row pos (:858-864, :871-877; CollectionReceptor.java:95-105)
+//   scores         q . K[t] / sqrt(hd) (attentionKeysStandard :531-559)
+//   causal mask    rows t > pos are never visited; the reference adds -10000 there (:906-917),
+//                  whose exp underflows to exactly 0, so skipping them is identical
+//   softmax        max-subtracted (ActivationFeatures.java:135-143), computed online per split
+//   values         sum_t a[t] V[t] (attentionValuesStandard :572-616)
+//
+// Layout: caches are compact and head-major, (batch, kv_heads, max_seq, hd) fp32; query head h
+// reads KV head h / (heads / kv_heads), which holds exactly what the reference's GQA-expanded
+// cache copy (:823-826) holds.
+//
+// Grid (splits, kv_heads, batch), 256 threads.  Block (s, g, b) handles context rows
+// [s*tile, min((s+1)*tile, pos+1)) for the heads/kv_heads query heads sharing KV head g:
+//   phase 1: 16-lane groups compute one row's scores for all heads of the group (K row read once)
+//   phase 2: each wavefront accumulates a[t] * V[t] for every fourth row (V row read once)
+// and writes unnormalised partials (o, max, sum).  The last block of a (b, g) to finish, found
+// with an atomic counter, merges the splits and writes the normalised output; it also resets the
+// counter, so no memset is needed between launches.
+#include "ar_hip_internal.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxTile = 256;
+
+struct AttnParams {
+    const float* qkv;
+    int qkv_stride;
+    const float* q_norm;
+    const float* k_norm;
+    float qk_eps;
+    int per_head_norm;
+    float* kcache;
+    float* vcache;
+    int max_seq;
+    const int* pos;
+    int heads, kv_heads;
+    double rope_c;  // -2 ln(theta) / hd
+    int tile, max_splits;
+    float* part_o;
+    float* part_ml;
+    unsigned* counters;
+    float* out;
+    int out_stride;
+};
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Block-wide sum of per-thread values; every thread gets the result.
+__device__ inline float block_sum(float v, float* scratch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; w++) t += scratch[w];
+    return t;
+}
+
+__device__ inline void rope_cs(int pos, int f, double c, float* cs, float* sn) {
+    const double invf = exp((double)f * c);
+    const double ang = (double)pos * invf;
+    *cs = (float)cos(ang);
+    *sn = (float)sin(ang);
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
+    constexpr int FD = HD / 2;
+    constexpr int EPL = HD / 16;     // elements per lane in a 16-lane row group
+    constexpr int VPL = HD / 64;     // value columns per lane in phase 2
+    __shared__ __attribute__((aligned(16))) float q_s[G][HD];
+    __shared__ float s_s[G][kMaxTile];
+    __shared__ __attribute__((aligned(16))) float red_s[kThreads / 64][G][HD];
+    __shared__ float m_s[G], l_s[G];
+    __shared__ float scratch[kThreads / 64];
+    __shared__ float rq_s[G], rk_s;
+    __shared__ int last_s;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
+    const int pos = *p.pos;
+    if (pos < 0 || pos >= p.max_seq) return;
+    const int n = pos + 1;
+    const int nsplit = (n + p.tile - 1) / p.tile;
+    if (split >= nsplit) return;
+    const int t0 = split * p.tile;
+    const int t1 = min(t0 + p.tile, n);
+    const int heads = p.heads, kvH = p.kv_heads;
+    const int q_dim = heads * HD, kv_dim = kvH * HD;
+    const float* q_raw = p.qkv + (size_t)b * p.qkv_stride;
+    const float* k_raw = q_raw + q_dim;
+    const float* v_raw = k_raw + kv_dim;
+    const size_t head_base = ((size_t)b * kvH + kvh) * (size_t)p.max_seq * HD;
+    float* kc = p.kcache + head_base;
+    float* vc = p.vcache + head_base;
+
+    // ---- QK-norm factors ----------------------------------------------------------
+    if (p.q_norm || p.k_norm) {
+        if (!p.per_head_norm) {
+            float sq = 0.f, sk = 0.f;
+            for (int i = tid; i < q_dim; i += kThreads) sq += q_raw[i] * q_raw[i];
+            for (int i = tid; i < kv_dim; i += kThreads) sk += k_raw[i] * k_raw[i];
+            sq = block_sum(sq, scratch);
+            sk = block_sum(sk, scratch);
+            if (tid == 0) {
+                const float rq = 1.0f / sqrtf(sq / (float)q_dim + p.qk_eps);
+                for (int g = 0; g < G; g++) rq_s[g] = rq;
+                rk_s = 1.0f / sqrtf(sk / (float)kv_dim + p.qk_eps);
+            }
+        } else {
+            // wave w reduces heads w, w+4, ...; the k head goes to the last slot
+            for (int j = wave; j < G + 1; j += kThreads / 64) {
+                const float* src = (j < G) ? q_raw + (size_t)(kvh * G + j) * HD : k_raw + (size_t)kvh * HD;
+                float s = 0.f;
+                for (int i = lane; i < HD; i += 64) s += src[i] * src[i];
+                s = wave_sum(s);
+                if (lane == 0) {
+                    const float r = 1.0f / sqrtf(s / (float)HD + p.qk_eps);
+                    if (j < G) rq_s[j] = r; else rk_s = r;
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- normalised, rotated queries of this group -> LDS ---------------------------
+    for (int idx = tid; idx < G * FD; idx += kThreads) {
+        const int g = idx / FD, f = idx - g * FD;
+        const int h = kvh * G + g;
+        float x1 = q_raw[(size_t)h * HD + f], x2 = q_raw[(size_t)h * HD + f + FD];
+        if (p.q_norm) {
+            x1 = (p.q_norm[(size_t)h * HD + f] * x1) * rq_s[g];
+            x2 = (p.q_norm[(size_t)h * HD + f + FD] * x2) * rq_s[g];
+        }
+        float c, s;
+        rope_cs(pos, f, p.rope_c, &c, &s);
+        q_s[g][f] = x1 * c - x2 * s;
+        q_s[g][f + FD] = x2 * c + x1 * s;
+    }
+    // ---- the split holding `pos` writes this step's k and v rows ---------------------
+    if (pos >= t0 && pos < t1) {
+        for (int f = tid; f < FD; f += kThreads) {
+            float x1 = k_raw[(size_t)kvh * HD + f], x2 = k_raw[(size_t)kvh * HD + f + FD];
+            if (p.k_norm) {
+                x1 = (p.k_norm[(size_t)kvh * HD + f] * x1) * rk_s;
+                x2 = (p.k_norm[(size_t)kvh * HD + f + FD] * x2) * rk_s;
+            }
+            float c, s;
+            rope_cs(pos, f, p.rope_c, &c, &s);
+            kc[(size_t)pos * HD + f] = x1 * c - x2 * s;
+            kc[(size_t)pos * HD + f + FD] = x2 * c + x1 * s;
+        }
+        for (int i = tid; i < HD; i += kThreads) vc[(size_t)pos * HD + i] = v_raw[(size_t)kvh * HD + i];
+        __threadfence_block();
+    }
+    __syncthreads();
+
+    // ---- phase 1: scores -----------------------------------------------------------
+    {
+        const int grp = tid >> 4, gl = tid & 15;
+        float qr[G][EPL];
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int j = 0; j < EPL / 4; j++) {
+                float4 t = *reinterpret_cast<const float4*>(&q_s[g][j * 64 + gl * 4]);
+                qr[g][j * 4] = t.x; qr[g][j * 4 + 1] = t.y; qr[g][j * 4 + 2] = t.z; qr[g][j * 4 + 3] = t.w;
+            }
+        const float scale = sqrtf((float)HD);
+        for (int tb = t0 + grp; tb < t1; tb += 4 * 16) {
+            float kr[4][EPL];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = min(tb + u * 16, t1 - 1);
+#pragma unroll
+                for (int j = 0; j < EPL / 4; j++) {
+                    float4 v = *reinterpret_cast<const float4*>(kc + (size_t)t * HD + j * 64 + gl * 4);
+                    kr[u][j * 4] = v.x; kr[u][j * 4 + 1] = v.y; kr[u][j * 4 + 2] = v.z; kr[u][j * 4 + 3] = v.w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = tb + u * 16;
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    float d = 0.f;
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) d = fmaf(qr[g][e], kr[u][e], d);
+#pragma unroll
+                    for (int off = 8; off > 0; off >>= 1) d += __shfl_xor(d, off, 16);
+                    if (gl == 0 && t < t1) s_s[g][t - t0] = d / scale;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- split-local softmax statistics --------------------------------------------
+    const int len = t1 - t0;
+    for (int g = wave; g < G; g += kThreads / 64) {
+        float m = -INFINITY;
+        for (int i = lane; i < len; i += 64) m = fmaxf(m, s_s[g][i]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int i = lane; i < len; i += 64) {
+            const float e = expf(s_s[g][i] - m);
+            s_s[g][i] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { m_s[g] = m; l_s[g] = l; }
+    }
+    __syncthreads();
+
+    // ---- phase 2: values -------------------------------------------------------------
+    {
+        float acc[G][VPL];
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int j = 0; j < VPL; j++) acc[g][j] = 0.f;
+        for (int tb = t0 + wave; tb < t1; tb += 4 * 4) {
+            float vr[4][VPL];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = min(tb + u * 4, t1 - 1);
+                if constexpr (VPL == 2) {
+                    float2 v = *reinterpret_cast<const float2*>(vc + (size_t)t * HD + lane * 2);
+                    vr[u][0] = v.x; vr[u][1] = v.y;
+                } else {
+                    vr[u][0] = vc[(size_t)t * HD + lane];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = tb + u * 4;
+                if (t < t1) {
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const float a = s_s[g][t - t0];
+#pragma unroll
+                        for (int j = 0; j < VPL; j++) acc[g][j] = fmaf(a, vr[u][j], acc[g][j]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int j = 0; j < VPL; j++) red_s[wave][g][lane * VPL + j] = acc[g][j];
+    }
+    __syncthreads();
+
+    const int hbase = kvh * G;
+    if (nsplit == 1) {
+        for (int idx = tid; idx < G * HD; idx += kThreads) {
+            const int g = idx / HD, i = idx - g * HD;
+            float o = 0.f;
+#pragma unroll
+            for (int w = 0; w < kThreads / 64; w++) o += red_s[w][g][i];
+            p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = o / l_s[g];
+        }
+        return;
+    }
+
+    for (int idx = tid; idx < G * HD; idx += kThreads) {
+        const int g = idx / HD, i = idx - g * HD;
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; w++) o += red_s[w][g][i];
+        const size_t slot = ((size_t)b * heads + hbase + g) * p.max_splits + split;
+        p.part_o[slot * HD + i] = o;
+        if (i == 0) {
+            p.part_ml[slot * 2] = m_s[g];
+            p.part_ml[slot * 2 + 1] = l_s[g];
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    unsigned* ctr = p.counters + (size_t)b * kvH + kvh;
+    if (tid == 0) last_s = (atomicAdd(ctr, 1u) == (unsigned)(nsplit - 1));
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();
+    for (int idx = tid; idx < G * HD; idx += kThreads) {
+        const int g = idx / HD, i = idx - g * HD;
+        const size_t slot0 = ((size_t)b * heads + hbase + g) * p.max_splits;
+        float M = -INFINITY;
+        for (int s = 0; s < nsplit; s++) M = fmaxf(M, p.part_ml[(slot0 + s) * 2]);
+        float L = 0.f, O = 0.f;
+        for (int s = 0; s < nsplit; s++) {
+            const float w = expf(p.part_ml[(slot0 + s) * 2] - M);
+            L = fmaf(p.part_ml[(slot0 + s) * 2 + 1], w, L);
+            O = fmaf(p.part_o[(slot0 + s) * HD + i], w, O);
+        }
+        p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = O / L;
+    }
+    if (tid == 0) *ctr = 0u;
+}
+
+template <int HD, int G>
+int launch_t(const AttnLaunch& a, hipStream_t stream) {
+    AttnParams p;
+    p.qkv = a.qkv; p.qkv_stride = a.qkv_stride; p.q_norm = a.q_norm; p.k_norm = a.k_norm;
+    p.qk_eps = a.qk_eps; p.per_head_norm = a.per_head_norm; p.kcache = a.kcache; p.vcache = a.vcache;
+    p.max_seq = a.max_seq; p.pos = a.pos; p.heads = a.heads; p.kv_heads = a.kv_heads;
+    p.rope_c = -2.0 * log(a.rope_theta) / (double)HD;
+    p.tile = a.tile; p.max_splits = a.max_splits; p.part_o = a.part_o; p.part_ml = a.part_ml;
+    p.counters = a.counters; p.out = a.out; p.out_stride = a.out_stride;
+    hipLaunchKernelGGL((attn_decode_kernel<HD, G>), dim3(a.max_splits, a.kv_heads, a.batch), dim3(kThreads), 0,
+                       stream, p);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
+template <int HD>
+int pick_g(const AttnLaunch& a, hipStream_t s) {
+    switch (a.heads / a.kv_heads) {
+        case 1: return launch_t<HD, 1>(a, s);
+        case 2: return launch_t<HD, 2>(a, s);
+        case 4: return launch_t<HD, 4>(a, s);
+        case 8: return launch_t<HD, 8>(a, s);
+    }
+    ar_set_error("attention: heads/kv_heads = %d not in {1,2,4,8}", a.heads / a.kv_heads);
+    return AR_HIP_ERR_INVALID;
+}
+
+}  // namespace
+
+size_t attention_partial_floats(int batch, int heads, int max_splits, int hd) {
+    return (size_t)batch * heads * max_splits * (size_t)hd;
+}
+
+int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
+    AR_CHECK_ARG(a.qkv && a.kcache && a.vcache && a.pos && a.out, "attention: null pointer");
+    AR_CHECK_ARG(a.heads > 0 && a.kv_heads > 0 && a.heads % a.kv_heads == 0, "attention: bad head counts %d/%d",
+                 a.heads, a.kv_heads);
+    AR_CHECK_ARG(a.tile >= 16 && a.tile <= kMaxTile && a.tile % 16 == 0, "attention: tile %d outside 16..%d",
+                 a.tile, kMaxTile);
+    AR_CHECK_ARG(a.max_splits >= 1 && (long long)a.max_splits * a.tile >= a.max_seq,
+                 "attention: %d splits of %d do not cover %d rows", a.max_splits, a.tile, a.max_seq);
+    AR_CHECK_ARG(a.max_splits == 1 || (a.part_o && a.part_ml && a.counters), "attention: missing split buffers");
+    AR_CHECK_ARG(a.batch >= 1 && a.batch <= 65535, "attention: bad batch %d", a.batch);
+    AR_CHECK_ARG((reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.vcache) & 15) == 0,
+                 "attention: caches must be 16-byte aligned");
+    if (a.head_dim == 128) return pick_g<128>(a, stream);
+    if (a.head_dim == 64) return pick_g<64>(a, stream);
+    ar_set_error("attention: head_dim %d not supported (64, 128)", a.head_dim);
+    return AR_HIP_ERR_INVALID;
+}

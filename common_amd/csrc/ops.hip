@@ -1,0 +1,106 @@
+// Stand-alone operator entry points of the C-ABI (device pointers, context stream).
+// Each mirrors one reference layer feature; see include/ar_hip.h for the citations.
+#include <cmath>
+
+#include "ar_hip_internal.h"
+
+extern "C" int ar_hip_rmsnorm(ar_hip_ctx* ctx, const float* x, const float* w, float* y, int rows, int n, float eps) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    return launch_rmsnorm(x, w, y, rows, n, eps, ctx->stream);
+}
+
+extern "C" int ar_hip_dense(ar_hip_ctx* ctx, const void* W, int w_dtype, const float* bias, const float* x,
+                            const float* norm_w, float eps, float* y, int rows, int cols, int batch) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    GemvLaunch a;
+    a.w = W; a.wdtype = w_dtype; a.bias = bias; a.x = x; a.x_stride = cols; a.norm_w = norm_w; a.eps = eps;
+    a.y = y; a.y_stride = rows; a.rows = rows; a.cols = cols; a.batch = batch; a.epilogue = GEMV_EPI_STORE;
+    return launch_gemv(a, ctx->stream);
+}
+
+extern "C" int ar_hip_swiglu(ar_hip_ctx* ctx, const void* W_gate, const void* W_up, int w_dtype, const float* x,
+                             const float* norm_w, float eps, float* y, int rows, int cols, int batch) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    GemvLaunch a;
+    a.w = W_gate; a.w2 = W_up; a.wdtype = w_dtype; a.x = x; a.x_stride = cols; a.norm_w = norm_w; a.eps = eps;
+    a.y = y; a.y_stride = rows; a.rows = rows; a.cols = cols; a.batch = batch; a.epilogue = GEMV_EPI_SWIGLU;
+    return launch_gemv(a, ctx->stream);
+}
+
+extern "C" int ar_hip_rope(ar_hip_ctx* ctx, float* x, int heads, int head_dim, int pos, double theta, int rows) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    return launch_rope(x, heads, head_dim, pos, theta, rows, heads * head_dim, ctx->stream);
+}
+
+extern "C" int ar_hip_index_of_max(ar_hip_ctx* ctx, const float* x, int rows, int n, int32_t* out_device) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    return launch_index_of_max(x, rows, n, out_device, ctx->stream);
+}
+
+namespace {
+// Scratch the stand-alone attention op keeps between calls: packed q|k|v, the position, split
+// partials and counters.  Grown on demand; freed with the context's allocations.
+struct AttnScratch {
+    size_t qkv_floats = 0, part_floats = 0, ml_floats = 0, ctr_count = 0;
+    float* qkv = nullptr;
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    unsigned* counters = nullptr;
+    int* pos = nullptr;
+};
+std::mutex g_attn_mu;
+std::unordered_map<ar_hip_ctx*, AttnScratch> g_attn;
+
+int grow(ar_hip_ctx* ctx, void** p, size_t* have, size_t need, size_t elem) {
+    if (*have >= need && *p) return AR_HIP_OK;
+    if (*p) AR_TRY(ar_ctx_free(ctx, *p));
+    *p = nullptr;
+    *have = 0;
+    AR_TRY(ar_ctx_alloc(ctx, need * elem, p));
+    *have = need;
+    return AR_HIP_OK;
+}
+}  // namespace
+
+extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const float* k, const float* v,
+                                       const float* q_norm, const float* k_norm, float qk_eps, int qk_norm_mode,
+                                       float* k_cache, float* v_cache, int max_seq, int pos, int heads, int kv_heads,
+                                       int head_dim, double rope_theta, float* out) {
+    AR_CHECK_ARG(ctx && q && k && v && k_cache && v_cache && out, "attention: null pointer");
+    AR_CHECK_ARG(pos >= 0 && pos < max_seq, "attention: position %d outside cache of %d rows", pos, max_seq);
+    AR_CHECK_ARG(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "attention: bad head counts");
+    AR_CHECK_ARG(qk_norm_mode == AR_QK_NORM_WHOLE || qk_norm_mode == AR_QK_NORM_PER_HEAD, "attention: bad qk-norm mode");
+    std::lock_guard<std::mutex> lk(g_attn_mu);
+    AttnScratch& s = g_attn[ctx];
+    const int q_dim = heads * head_dim, kv_dim = kv_heads * head_dim;
+    const int tile = max_seq >= 1024 ? 64 : 32;
+    const int max_splits = (max_seq + tile - 1) / tile;
+    size_t dummy = 0;
+    AR_TRY(grow(ctx, (void**)&s.qkv, &s.qkv_floats, (size_t)q_dim + 2 * kv_dim, sizeof(float)));
+    AR_TRY(grow(ctx, (void**)&s.part_o, &s.part_floats, attention_partial_floats(1, heads, max_splits, head_dim),
+                sizeof(float)));
+    AR_TRY(grow(ctx, (void**)&s.part_ml, &s.ml_floats, (size_t)heads * max_splits * 2, sizeof(float)));
+    if (!s.counters) {
+        AR_TRY(grow(ctx, (void**)&s.counters, &s.ctr_count, 64, sizeof(unsigned)));
+        AR_HIP_TRY(hipMemsetAsync(s.counters, 0, 64 * sizeof(unsigned), ctx->stream));
+    }
+    AR_CHECK_ARG(kv_heads <= 64, "attention: more than 64 KV heads");
+    if (!s.pos) AR_TRY(grow(ctx, (void**)&s.pos, &dummy, 1, sizeof(int)));
+    AR_HIP_TRY(hipMemcpyAsync(s.qkv, q, sizeof(float) * q_dim, hipMemcpyDeviceToDevice, ctx->stream));
+    AR_HIP_TRY(hipMemcpyAsync(s.qkv + q_dim, k, sizeof(float) * kv_dim, hipMemcpyDeviceToDevice, ctx->stream));
+    AR_HIP_TRY(hipMemcpyAsync(s.qkv + q_dim + kv_dim, v, sizeof(float) * kv_dim, hipMemcpyDeviceToDevice, ctx->stream));
+    AR_TRY(launch_fill_i32(s.pos, pos, 1, ctx->stream));
+    AttnLaunch a;
+    a.qkv = s.qkv; a.qkv_stride = q_dim + 2 * kv_dim; a.q_norm = q_norm; a.k_norm = k_norm; a.qk_eps = qk_eps;
+    a.per_head_norm = qk_norm_mode == AR_QK_NORM_PER_HEAD; a.kcache = k_cache; a.vcache = v_cache;
+    a.max_seq = max_seq; a.pos = s.pos; a.heads = heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
+    a.rope_theta = rope_theta; a.tile = tile; a.max_splits = max_splits; a.part_o = s.part_o; a.part_ml = s.part_ml;
+    a.counters = s.counters; a.out = out; a.out_stride = q_dim; a.batch = 1;
+    return launch_attention_decode(a, ctx->stream);
+}
+
+// Called from ar_hip_destroy's owner before the context goes away.
+void ar_ops_release(ar_hip_ctx* ctx) {
+    std::lock_guard<std::mutex> lk(g_attn_mu);
+    g_attn.erase(ctx);  // the allocations themselves are freed with the context
+}

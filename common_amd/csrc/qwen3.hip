@@ -1,0 +1,588 @@
+// Qwen3 decode-step plan: device-resident weights, KV caches and token loop.
+//
+// Stands in for Qwen3.model + CompiledModel + AutoregressiveModel
+// (engine/ml/.../qwen3/Qwen3.java:334-415, domain/graph/.../model/CompiledModel.java:189-197,
+//  engine/ml/.../AutoregressiveModel.java:203-220,295-308,405-434).  The reference runs ~877
+// generated ops per layer with host-side cache writes; one step here is
+//   embed, then per layer [QKV GEMV (+RMSNorm) | attention (+QK-norm, RoPE, cache write) |
+//   O GEMV (+residual) | gate/up GEMV (+RMSNorm, SwiGLU) | down GEMV (+residual)],
+//   then logits GEMV (+final RMSNorm, argmax, position advance)
+// on one stream, optionally replayed from a captured HIP graph.  Tokens and the position stay
+// on the device, so many steps can be enqueued without a host round trip.
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ar_hip_internal.h"
+
+namespace {
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct Slot {
+    void* dst = nullptr;     // device destination
+    int64_t elems = 0;
+    bool matrix = false;     // stored in the model's weight dtype (else fp32)
+    bool required = true;
+    bool filled = false;
+};
+
+struct Layer {
+    void* wqkv = nullptr;    // rows: q (q_dim) | k (kv_dim) | v (kv_dim), cols dim
+    void* wo = nullptr;
+    void* w1 = nullptr;      // gate
+    void* w3 = nullptr;      // up
+    void* w2 = nullptr;      // down
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    float* q_norm = nullptr;
+    float* k_norm = nullptr;
+    float* bqkv = nullptr;
+};
+
+int attention_tile(int seq) {
+    int t = (seq + 15) / 16;
+    t = (t + 15) / 16 * 16;
+    if (t < 16) t = 16;
+    if (t > 128) t = 128;
+    return t;
+}
+
+}  // namespace
+
+struct ar_qwen3 {
+    ar_hip_ctx* ctx = nullptr;
+    ar_qwen3_cfg cfg{};
+    int q_dim = 0, kv_dim = 0, qkv_dim = 0, B = 1, S = 0;
+    size_t wbytes = 4;
+    char* arena = nullptr;
+    size_t arena_bytes = 0;
+    std::vector<Layer> layers;
+    void* embed = nullptr;
+    void* lm_head = nullptr;
+    float* final_norm = nullptr;
+    std::unordered_map<std::string, Slot> slots;
+    bool finalized = false;
+
+    // activations and state
+    float* x = nullptr;       // [B][dim] residual stream
+    float* qkv = nullptr;     // [B][qkv_dim]
+    float* attn = nullptr;    // [B][q_dim]
+    float* act = nullptr;     // [B][F]
+    float* logits = nullptr;  // [B][V]
+    float* kcache = nullptr;  // [L][B][KV][S][hd]
+    float* vcache = nullptr;
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    unsigned* attn_ctr = nullptr;
+    float* am_val = nullptr;
+    int* am_idx = nullptr;
+    unsigned* am_ctr = nullptr;
+    int* tokens = nullptr;    // [B][S+1]
+    int* state = nullptr;     // {position, prompt length}
+    float* staging = nullptr; // fp32 upload staging for dtype conversion
+    size_t staging_floats = 0;
+    int tile = 32, max_splits = 1;
+
+    int host_pos = 0;
+    int prompt_len = 0;
+    std::vector<int> prompt_set;
+
+    bool use_graph = true;
+    hipGraphExec_t graph[2] = {nullptr, nullptr};  // [store logits]
+
+    int timed = AR_KT_NONE;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+    size_t events_used = 0;
+};
+
+namespace {
+
+int alloc_zero(ar_qwen3* m, size_t bytes, void** p) {
+    AR_TRY(ar_ctx_alloc(m->ctx, bytes, p));
+    AR_HIP_TRY(hipMemsetAsync(*p, 0, bytes, m->ctx->stream));
+    return AR_HIP_OK;
+}
+
+void release(ar_qwen3* m) {
+    if (!m) return;
+    for (auto& g : m->graph)
+        if (g) hipGraphExecDestroy(g);
+    for (auto& e : m->events) {
+        hipEventDestroy(e.first);
+        hipEventDestroy(e.second);
+    }
+    void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
+                    m->part_ml, m->attn_ctr, m->am_val, m->am_idx, m->am_ctr, m->tokens, m->state, m->staging};
+    for (void* b : bufs)
+        if (b) ar_ctx_free(m->ctx, b);
+    delete m;
+}
+
+int add_slot(ar_qwen3* m, const std::string& key, void* dst, int64_t elems, bool matrix, bool required = true) {
+    Slot s;
+    s.dst = dst;
+    s.elems = elems;
+    s.matrix = matrix;
+    s.required = required;
+    m->slots[key] = s;
+    return AR_HIP_OK;
+}
+
+int invalidate_graphs(ar_qwen3* m) {
+    for (auto& g : m->graph) {
+        if (g) {
+            AR_HIP_TRY(hipGraphExecDestroy(g));
+            g = nullptr;
+        }
+    }
+    return AR_HIP_OK;
+}
+
+// One decode step on the model's stream.
+int enqueue_step(ar_qwen3* m, bool store_logits) {
+    const ar_qwen3_cfg& c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int B = m->B, dim = c.dim, F = c.hidden_dim;
+    auto timed_begin = [&](int which) -> int {
+        if (m->timed != which) return AR_HIP_OK;
+        if (m->events_used == m->events.size()) {
+            hipEvent_t a, b;
+            AR_HIP_TRY(hipEventCreate(&a));
+            AR_HIP_TRY(hipEventCreate(&b));
+            m->events.push_back({a, b});
+        }
+        AR_HIP_TRY(hipEventRecord(m->events[m->events_used].first, st));
+        return AR_HIP_OK;
+    };
+    auto timed_end = [&](int which) -> int {
+        if (m->timed != which) return AR_HIP_OK;
+        AR_HIP_TRY(hipEventRecord(m->events[m->events_used].second, st));
+        m->events_used++;
+        return AR_HIP_OK;
+    };
+
+    AR_TRY(launch_embed(m->embed, c.weight_dtype, dim, m->tokens, m->S + 1, m->state, B, m->x, dim, st));
+    const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
+    for (int l = 0; l < c.layer_count; l++) {
+        const Layer& L = m->layers[l];
+        GemvLaunch g;
+        g.wdtype = c.weight_dtype;
+        g.batch = B;
+        g.eps = (float)c.epsilon;
+        // QKV projection with the pre-attention RMSNorm fused in (AttentionFeatures.java:830-900)
+        g.w = L.wqkv; g.rows = m->qkv_dim; g.cols = dim; g.x = m->x; g.x_stride = dim; g.norm_w = L.attn_norm;
+        g.bias = L.bqkv; g.y = m->qkv; g.y_stride = m->qkv_dim; g.epilogue = GEMV_EPI_STORE;
+        AR_TRY(timed_begin(AR_KT_QKV));
+        AR_TRY(launch_gemv(g, st));
+        AR_TRY(timed_end(AR_KT_QKV));
+
+        AttnLaunch a;
+        a.qkv = m->qkv; a.qkv_stride = m->qkv_dim; a.q_norm = L.q_norm; a.k_norm = L.k_norm;
+        a.qk_eps = (float)c.epsilon; a.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
+        a.kcache = m->kcache + l * layer_cache; a.vcache = m->vcache + l * layer_cache; a.max_seq = m->S;
+        a.pos = m->state; a.heads = c.head_count; a.kv_heads = c.kv_head_count; a.head_dim = c.head_size;
+        a.rope_theta = c.rope_theta; a.tile = m->tile; a.max_splits = m->max_splits; a.part_o = m->part_o;
+        a.part_ml = m->part_ml; a.counters = m->attn_ctr; a.out = m->attn; a.out_stride = m->q_dim; a.batch = B;
+        AR_TRY(timed_begin(AR_KT_ATTENTION));
+        AR_TRY(launch_attention_decode(a, st));
+        AR_TRY(timed_end(AR_KT_ATTENTION));
+
+        // O projection + residual (AttentionFeatures.java:922, :1704)
+        GemvLaunch o;
+        o.wdtype = c.weight_dtype; o.batch = B; o.w = L.wo; o.rows = dim; o.cols = m->q_dim; o.x = m->attn;
+        o.x_stride = m->q_dim; o.y = m->x; o.y_stride = dim; o.epilogue = GEMV_EPI_RESIDUAL;
+        AR_TRY(timed_begin(AR_KT_O));
+        AR_TRY(launch_gemv(o, st));
+        AR_TRY(timed_end(AR_KT_O));
+
+        // gate/up with the pre-FFN RMSNorm and SwiGLU fused (FeedForwardFeatures.java:147-155)
+        GemvLaunch u;
+        u.wdtype = c.weight_dtype; u.batch = B; u.eps = (float)c.epsilon; u.w = L.w1; u.w2 = L.w3; u.rows = F;
+        u.cols = dim; u.x = m->x; u.x_stride = dim; u.norm_w = L.ffn_norm; u.y = m->act; u.y_stride = F;
+        u.epilogue = GEMV_EPI_SWIGLU;
+        AR_TRY(timed_begin(AR_KT_GATE_UP));
+        AR_TRY(launch_gemv(u, st));
+        AR_TRY(timed_end(AR_KT_GATE_UP));
+
+        // down projection + residual (FeedForwardFeatures.java:156; AttentionFeatures.java:1705)
+        GemvLaunch d;
+        d.wdtype = c.weight_dtype; d.batch = B; d.w = L.w2; d.rows = dim; d.cols = F; d.x = m->act; d.x_stride = F;
+        d.y = m->x; d.y_stride = dim; d.epilogue = GEMV_EPI_RESIDUAL;
+        AR_TRY(timed_begin(AR_KT_DOWN));
+        AR_TRY(launch_gemv(d, st));
+        AR_TRY(timed_end(AR_KT_DOWN));
+    }
+    // final RMSNorm + tied logits + greedy token + advance (Qwen3.java:401-405; AutoregressiveModel.java:412-421)
+    GemvLaunch h;
+    h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
+    h.cols = dim; h.x = m->x; h.x_stride = dim; h.norm_w = m->final_norm; h.y = store_logits ? m->logits : nullptr;
+    h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.part_val = m->am_val; h.part_idx = m->am_idx;
+    h.counter = m->am_ctr; h.tokens = m->tokens; h.token_stride = m->S + 1; h.state = m->state; h.advance = 1;
+    AR_TRY(timed_begin(AR_KT_LOGITS));
+    AR_TRY(launch_gemv(h, st));
+    AR_TRY(timed_end(AR_KT_LOGITS));
+    return AR_HIP_OK;
+}
+
+int run_step(ar_qwen3* m, bool store_logits) {
+    hipStream_t st = m->ctx->stream;
+    if (!m->use_graph || m->timed != AR_KT_NONE) return enqueue_step(m, store_logits);
+    hipGraphExec_t& ex = m->graph[store_logits ? 1 : 0];
+    if (!ex) {
+        hipGraph_t g = nullptr;
+        AR_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_step(m, store_logits);
+        hipError_t ce = hipStreamEndCapture(st, &g);
+        if (rc != AR_HIP_OK) {
+            if (g) hipGraphDestroy(g);
+            return rc;
+        }
+        if (ce != hipSuccess) {
+            ar_set_error("hipStreamEndCapture: %s", hipGetErrorString(ce));
+            return AR_HIP_ERR_HIP;
+        }
+        hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ie != hipSuccess) {
+            ex = nullptr;
+            ar_set_error("hipGraphInstantiate: %s", hipGetErrorString(ie));
+            return AR_HIP_ERR_HIP;
+        }
+    }
+    AR_HIP_TRY(hipGraphLaunch(ex, st));
+    return AR_HIP_OK;
+}
+
+int upload(ar_qwen3* m, Slot& s, const void* src, int src_dtype, int64_t n) {
+    hipStream_t st = m->ctx->stream;
+    const int dst_dtype = s.matrix ? m->cfg.weight_dtype : AR_DTYPE_F32;
+    if (src_dtype == dst_dtype) {
+        const size_t bytes = (size_t)n * (dst_dtype == AR_DTYPE_BF16 ? 2 : 4);
+        AR_HIP_TRY(hipMemcpyAsync(s.dst, src, bytes, hipMemcpyHostToDevice, st));
+        AR_HIP_TRY(hipStreamSynchronize(st));
+        return AR_HIP_OK;
+    }
+    if (src_dtype == AR_DTYPE_F32 && dst_dtype == AR_DTYPE_BF16) {
+        // fp32 host values -> device staging -> bf16 (round to nearest even) in place
+        const int64_t chunk = (int64_t)m->staging_floats;
+        for (int64_t off = 0; off < n; off += chunk) {
+            const int64_t len = std::min(chunk, n - off);
+            AR_HIP_TRY(hipMemcpyAsync(m->staging, (const float*)src + off, (size_t)len * 4, hipMemcpyHostToDevice, st));
+            AR_TRY(launch_f32_to_bf16(m->staging, (uint16_t*)s.dst + off, (size_t)len, st));
+            AR_HIP_TRY(hipStreamSynchronize(st));
+        }
+        return AR_HIP_OK;
+    }
+    ar_set_error("weight upload from dtype %d into dtype %d is not supported", src_dtype, dst_dtype);
+    return AR_HIP_ERR_INVALID;
+}
+
+}  // namespace
+
+extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_qwen3** out) {
+    AR_CHECK_ARG(ctx && cfg && out, "null argument");
+    *out = nullptr;
+    const ar_qwen3_cfg& c = *cfg;
+    AR_CHECK_ARG(c.dim > 0 && c.hidden_dim > 0 && c.layer_count > 0 && c.vocab_size > 0 && c.seq_len > 0,
+                 "Qwen3: sizes must be positive");
+    AR_CHECK_ARG(c.head_count > 0 && c.kv_head_count > 0 && c.head_count % c.kv_head_count == 0,
+                 "headCount (%d) must be divisible by kvHeadCount (%d)", c.head_count, c.kv_head_count);
+    const int G = c.head_count / c.kv_head_count;
+    AR_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 8, "Qwen3: heads per KV head %d not in {1,2,4,8}", G);
+    AR_CHECK_ARG(c.head_size == 64 || c.head_size == 128, "Qwen3: head size %d not in {64,128}", c.head_size);
+    AR_CHECK_ARG(c.max_batch >= 1 && c.max_batch <= 8, "Qwen3: batch %d outside 1..8", c.max_batch);
+    AR_CHECK_ARG(c.weight_dtype == AR_DTYPE_F32 || c.weight_dtype == AR_DTYPE_BF16, "Qwen3: bad weight dtype");
+    AR_CHECK_ARG(c.qk_norm_mode == AR_QK_NORM_WHOLE || c.qk_norm_mode == AR_QK_NORM_PER_HEAD, "Qwen3: bad qk-norm mode");
+    AR_CHECK_ARG(c.dim % 8 == 0 && c.hidden_dim % 8 == 0, "Qwen3: dim and hidden dim must be multiples of 8");
+    auto* m = new ar_qwen3();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->q_dim = c.head_count * c.head_size;
+    m->kv_dim = c.kv_head_count * c.head_size;
+    m->qkv_dim = m->q_dim + 2 * m->kv_dim;
+    m->B = c.max_batch;
+    m->S = c.seq_len;
+    m->wbytes = c.weight_dtype == AR_DTYPE_BF16 ? 2 : 4;
+    m->layers.resize(c.layer_count);
+    m->prompt_set.assign(m->B, 0);
+    m->tile = attention_tile(m->S);
+    m->max_splits = (m->S + m->tile - 1) / m->tile;
+
+    // ---- weight arena: every tensor 256-byte aligned --------------------------------
+    const size_t d = c.dim, F = c.hidden_dim, V = c.vocab_size, wb = m->wbytes;
+    struct Pending { std::string key; size_t off; int64_t elems; bool matrix; bool required; };
+    std::vector<Pending> plan;
+    size_t off = 0;
+    auto place = [&](const std::string& key, int64_t elems, bool matrix, bool required = true) {
+        plan.push_back({key, off, elems, matrix, required});
+        off = align_up(off + (size_t)elems * (matrix ? wb : 4), 256);
+        return plan.back().off;
+    };
+    const size_t emb_off = place("model.embed_tokens.weight", (int64_t)(V * d), true);
+    const size_t head_off = c.shared_weights ? emb_off : place("lm_head.weight", (int64_t)(V * d), true);
+    const size_t fnorm_off = place("model.norm.weight", (int64_t)d, false);
+    std::vector<size_t> lo(c.layer_count * 12);
+    for (int l = 0; l < c.layer_count; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        size_t* o = &lo[l * 12];
+        o[0] = place(p + "self_attn.qkv", (int64_t)m->qkv_dim * d, true);  // q|k|v rows, filled by 3 keys
+        o[1] = place(p + "self_attn.o_proj.weight", (int64_t)d * m->q_dim, true);
+        o[2] = place(p + "mlp.gate_proj.weight", (int64_t)F * d, true);
+        o[3] = place(p + "mlp.up_proj.weight", (int64_t)F * d, true);
+        o[4] = place(p + "mlp.down_proj.weight", (int64_t)d * F, true);
+        o[5] = place(p + "input_layernorm.weight", (int64_t)d, false);
+        o[6] = place(p + "post_attention_layernorm.weight", (int64_t)d, false);
+        o[7] = place(p + "self_attn.q_norm.weight", m->q_dim, false, false);
+        o[8] = place(p + "self_attn.k_norm.weight", m->kv_dim, false, false);
+        o[9] = c.qkv_bias ? place(p + "self_attn.qkv_bias", m->qkv_dim, false) : (size_t)-1;
+    }
+    m->arena_bytes = off;
+    int rc = ar_ctx_alloc(ctx, m->arena_bytes, (void**)&m->arena);
+    if (rc != AR_HIP_OK) {
+        delete m;
+        return rc;
+    }
+    char* A = m->arena;
+    m->embed = A + emb_off;
+    m->lm_head = A + head_off;
+    m->final_norm = (float*)(A + fnorm_off);
+    for (auto& pd : plan) {
+        if (pd.key.find(".self_attn.qkv") != std::string::npos) continue;  // split into q/k/v slots below
+        add_slot(m, pd.key, A + pd.off, pd.elems, pd.matrix, pd.required);
+    }
+    if (c.shared_weights) add_slot(m, "lm_head.weight", nullptr, (int64_t)(V * d), true, false);
+    for (int l = 0; l < c.layer_count; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        size_t* o = &lo[l * 12];
+        Layer& L = m->layers[l];
+        L.wqkv = A + o[0];
+        L.wo = A + o[1];
+        L.w1 = A + o[2];
+        L.w3 = A + o[3];
+        L.w2 = A + o[4];
+        L.attn_norm = (float*)(A + o[5]);
+        L.ffn_norm = (float*)(A + o[6]);
+        L.q_norm = (float*)(A + o[7]);
+        L.k_norm = (float*)(A + o[8]);
+        char* qkv = (char*)L.wqkv;
+        add_slot(m, p + "self_attn.q_proj.weight", qkv, (int64_t)m->q_dim * d, true);
+        add_slot(m, p + "self_attn.k_proj.weight", qkv + (size_t)m->q_dim * d * wb, (int64_t)m->kv_dim * d, true);
+        add_slot(m, p + "self_attn.v_proj.weight", qkv + (size_t)(m->q_dim + m->kv_dim) * d * wb,
+                 (int64_t)m->kv_dim * d, true);
+        if (c.qkv_bias) {
+            L.bqkv = (float*)(A + o[9]);
+            add_slot(m, p + "self_attn.q_proj.bias", L.bqkv, m->q_dim, false);
+            add_slot(m, p + "self_attn.k_proj.bias", L.bqkv + m->q_dim, m->kv_dim, false);
+            add_slot(m, p + "self_attn.v_proj.bias", L.bqkv + m->q_dim + m->kv_dim, m->kv_dim, false);
+        }
+    }
+
+    // ---- activations, caches, loop state -------------------------------------------
+    const size_t B = m->B;
+    const size_t cache = (size_t)c.layer_count * B * c.kv_head_count * m->S * c.head_size;
+    const int am_parts = gemv_argmax_partials(c.vocab_size, m->B);
+    m->staging_floats = 16u << 20;
+#define ALLOC(ptr, bytes)                                          \
+    do {                                                           \
+        int _r = alloc_zero(m, (bytes), (void**)&m->ptr);          \
+        if (_r != AR_HIP_OK) { release(m); return _r; }            \
+    } while (0)
+    ALLOC(x, B * d * 4);
+    ALLOC(qkv, B * m->qkv_dim * 4);
+    ALLOC(attn, B * m->q_dim * 4);
+    ALLOC(act, B * F * 4);
+    ALLOC(logits, B * V * 4);
+    ALLOC(kcache, cache * 4);
+    ALLOC(vcache, cache * 4);
+    ALLOC(part_o, attention_partial_floats(m->B, c.head_count, m->max_splits, c.head_size) * 4);
+    ALLOC(part_ml, B * c.head_count * m->max_splits * 2 * 4);
+    ALLOC(attn_ctr, B * c.kv_head_count * 4);
+    ALLOC(am_val, (size_t)am_parts * 4);
+    ALLOC(am_idx, (size_t)am_parts * 4);
+    ALLOC(am_ctr, 64);
+    ALLOC(tokens, B * (m->S + 1) * 4);
+    ALLOC(state, 64);
+    ALLOC(staging, m->staging_floats * 4);
+#undef ALLOC
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        release(m);
+        ar_set_error("stream synchronize after allocation failed");
+        return AR_HIP_ERR_HIP;
+    }
+    *out = m;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_destroy(ar_qwen3* m) {
+    if (!m) return AR_HIP_OK;
+    hipStreamSynchronize(m->ctx->stream);
+    release(m);
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_set_weight(ar_qwen3* m, const char* key, const void* src, int src_dtype, int64_t n) {
+    AR_CHECK_ARG(m && key && src, "null argument");
+    auto it = m->slots.find(key);
+    if (it == m->slots.end()) {
+        ar_set_error("unknown weight key '%s'", key);
+        return AR_HIP_ERR_NOT_FOUND;
+    }
+    Slot& s = it->second;
+    if (!s.dst) return AR_HIP_OK;  // lm_head.weight with tied embeddings: the embedding is the head
+    AR_CHECK_ARG(n == s.elems, "weight '%s': %lld elements given, %lld expected", key, (long long)n,
+                 (long long)s.elems);
+    AR_TRY(upload(m, s, src, src_dtype, n));
+    s.filled = true;
+    m->finalized = false;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
+    AR_CHECK_ARG(m, "null model");
+    for (auto& kv : m->slots) {
+        if (kv.second.dst && kv.second.required && !kv.second.filled) {
+            ar_set_error("weight '%s' was never set", kv.first.c_str());
+            return AR_HIP_ERR_STATE;
+        }
+    }
+    // QK-norm gains are optional (Qwen3.java:378-379, AttentionFeatures.java:839,885): a gain that
+    // was never set means that norm is skipped.
+    for (int l = 0; l < m->cfg.layer_count; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        Layer& L = m->layers[l];
+        const Slot& qs = m->slots[p + "self_attn.q_norm.weight"];
+        const Slot& ks = m->slots[p + "self_attn.k_norm.weight"];
+        L.q_norm = qs.filled ? (float*)qs.dst : nullptr;
+        L.k_norm = ks.filled ? (float*)ks.dst : nullptr;
+    }
+    AR_TRY(invalidate_graphs(m));
+    m->finalized = true;
+    return ar_hip_qwen3_reset(m);
+}
+
+extern "C" int ar_hip_qwen3_reset(ar_qwen3* m) {
+    AR_CHECK_ARG(m, "null model");
+    m->host_pos = 0;
+    int st[2] = {0, m->prompt_len};
+    AR_HIP_TRY(hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, m->ctx->stream));
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_set_prompt(ar_qwen3* m, int seq, const int32_t* ids, int n) {
+    AR_CHECK_ARG(m && (ids || n == 0), "null argument");
+    AR_CHECK_ARG(seq >= 0 && seq < m->B, "sequence %d outside batch of %d", seq, m->B);
+    AR_CHECK_ARG(n >= 0 && n <= m->S, "prompt of %d tokens exceeds the %d-position cache", n, m->S);
+    for (int i = 0; i < n; i++)
+        AR_CHECK_ARG(ids[i] >= 0 && ids[i] < m->cfg.vocab_size, "prompt token %d at %d outside vocab", ids[i], i);
+    for (int b = 0; b < m->B; b++)
+        if (b != seq && m->prompt_set[b])
+            AR_CHECK_ARG(n == m->prompt_len, "all sequences of a batch share one prompt length (%d != %d)", n,
+                         m->prompt_len);
+    if (n > 0)
+        AR_HIP_TRY(hipMemcpyAsync(m->tokens + (size_t)seq * (m->S + 1), ids, (size_t)n * 4, hipMemcpyHostToDevice,
+                                  m->ctx->stream));
+    m->prompt_len = n;
+    m->prompt_set[seq] = 1;
+    int st[2] = {m->host_pos, m->prompt_len};
+    AR_HIP_TRY(hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, m->ctx->stream));
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return AR_HIP_OK;
+}
+
+static int check_ready(ar_qwen3* m, int steps) {
+    AR_CHECK_ARG(m, "null model");
+    if (!m->finalized) {
+        ar_set_error("model not finalized (call ar_hip_qwen3_finalize after setting weights)");
+        return AR_HIP_ERR_STATE;
+    }
+    if (m->prompt_len < 1) {
+        ar_set_error("no prompt: set at least one prompt token before stepping");
+        return AR_HIP_ERR_STATE;
+    }
+    for (int b = 0; b < m->B; b++)
+        if (!m->prompt_set[b]) {
+            ar_set_error("sequence %d has no prompt", b);
+            return AR_HIP_ERR_STATE;
+        }
+    if (m->host_pos + steps > m->S) {
+        ar_set_error("position %d + %d steps exceeds the %d-position KV cache", m->host_pos, steps, m->S);
+        return AR_HIP_ERR_STATE;
+    }
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_next(ar_qwen3* m, int32_t* tokens_out, float* logits_out) {
+    AR_TRY(check_ready(m, 1));
+    hipStream_t st = m->ctx->stream;
+    AR_TRY(run_step(m, logits_out != nullptr));
+    if (tokens_out)
+        for (int b = 0; b < m->B; b++)
+            AR_HIP_TRY(hipMemcpyAsync(tokens_out + b, m->tokens + (size_t)b * (m->S + 1) + m->host_pos, 4,
+                                      hipMemcpyDeviceToHost, st));
+    if (logits_out)
+        AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)m->B * m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
+                                  st));
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    m->host_pos++;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_run(ar_qwen3* m, int steps, int32_t* tokens_out) {
+    AR_CHECK_ARG(steps >= 0, "negative step count");
+    AR_TRY(check_ready(m, steps));
+    hipStream_t st = m->ctx->stream;
+    const int start = m->host_pos;
+    for (int i = 0; i < steps; i++) AR_TRY(run_step(m, false));
+    if (tokens_out && steps > 0)
+        for (int b = 0; b < m->B; b++)
+            AR_HIP_TRY(hipMemcpyAsync(tokens_out + (size_t)b * steps, m->tokens + (size_t)b * (m->S + 1) + start,
+                                      (size_t)steps * 4, hipMemcpyDeviceToHost, st));
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    m->host_pos += steps;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_position(ar_qwen3* m, int* pos) {
+    AR_CHECK_ARG(m && pos, "null argument");
+    *pos = m->host_pos;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_hidden(ar_qwen3* m, float* out) {
+    AR_CHECK_ARG(m && out, "null argument");
+    AR_HIP_TRY(hipMemcpyAsync(out, m->x, (size_t)m->B * m->cfg.dim * 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_kernel_timing(ar_qwen3* m, int which) {
+    AR_CHECK_ARG(m, "null model");
+    AR_CHECK_ARG(which >= AR_KT_NONE && which <= AR_KT_O, "unknown kernel class %d", which);
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    m->timed = which;
+    m->events_used = 0;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_kernel_time(ar_qwen3* m, double* ms, int* launches) {
+    AR_CHECK_ARG(m && ms && launches, "null argument");
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    double t = 0.0;
+    for (size_t i = 0; i < m->events_used; i++) {
+        float e = 0.f;
+        AR_HIP_TRY(hipEventElapsedTime(&e, m->events[i].first, m->events[i].second));
+        t += e;
+    }
+    *ms = t;
+    *launches = (int)m->events_used;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_use_graph(ar_qwen3* m, int enable) {
+    AR_CHECK_ARG(m, "null model");
+    m->use_graph = enable != 0;
+    return AR_HIP_OK;
+}

@@ -1,0 +1,203 @@
+// HIP data/compute context and memory provider behind the C-ABI.
+//
+// Plays the role of the reference's DataContext / ComputeContext / MemoryProvider trio
+// (base/code/src/main/java/io/almostrealism/code/DataContext.java:81-88,
+//  ComputeContext.java:89,133, MemoryProvider.java:60-188) for one GPU.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "ar_hip_internal.h"
+
+namespace {
+thread_local char g_last_error[1024] = "";
+}
+
+void ar_set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+}
+
+void ar_clear_error() { g_last_error[0] = '\0'; }
+
+extern "C" const char* ar_hip_last_error(void) { return g_last_error; }
+
+extern "C" const char* ar_hip_version(void) { return "ar-hip 0.1 gfx950"; }
+
+extern "C" int ar_hip_device_count(int* count) {
+    AR_CHECK_ARG(count, "count is null");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        *count = 0;
+        ar_set_error("hipGetDeviceCount: %s", hipGetErrorString(e));
+        return AR_HIP_ERR_NO_DEVICE;
+    }
+    *count = n;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_init(int device, ar_hip_ctx** out) {
+    AR_CHECK_ARG(out, "out is null");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+        ar_set_error("no HIP device available (%s)", e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+        return AR_HIP_ERR_NO_DEVICE;
+    }
+    AR_CHECK_ARG(device >= 0 && device < n, "device %d out of range [0,%d)", device, n);
+    AR_HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    AR_HIP_TRY(hipGetDeviceProperties(&prop, device));
+    auto* ctx = new ar_hip_ctx();
+    ctx->device = device;
+    ctx->num_cus = prop.multiProcessorCount;
+    ctx->hbm_bytes = prop.totalGlobalMem;
+    // Default-priority, non-blocking stream: all work of this context is ordered on it.
+    hipError_t se = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (se != hipSuccess) {
+        ar_set_error("hipStreamCreateWithFlags: %s", hipGetErrorString(se));
+        delete ctx;
+        return AR_HIP_ERR_HIP;
+    }
+    *out = ctx;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_destroy(ar_hip_ctx* ctx) {
+    if (!ctx) return AR_HIP_OK;
+    ar_ops_release(ctx);
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->device_allocs) hipFree(kv.first);
+    for (auto& kv : ctx->host_allocs) hipHostFree(kv.first);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_synchronize(ar_hip_ctx* ctx) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    AR_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_device_info(ar_hip_ctx* ctx, int* num_cus, size_t* hbm_bytes, char* name, int name_len) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    if (num_cus) *num_cus = ctx->num_cus;
+    if (hbm_bytes) *hbm_bytes = ctx->hbm_bytes;
+    if (name && name_len > 0) {
+        hipDeviceProp_t prop;
+        AR_HIP_TRY(hipGetDeviceProperties(&prop, ctx->device));
+        snprintf(name, (size_t)name_len, "%s", prop.gcnArchName);
+    }
+    return AR_HIP_OK;
+}
+
+int ar_ctx_alloc(ar_hip_ctx* ctx, size_t bytes, void** out) {
+    AR_CHECK_ARG(ctx && out, "null argument");
+    AR_CHECK_ARG(bytes > 0, "allocation of 0 bytes");
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        ar_set_error("hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+        return AR_HIP_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->device_allocs[p] = bytes;
+    ctx->device_bytes += bytes;
+    *out = p;
+    return AR_HIP_OK;
+}
+
+int ar_ctx_free(ar_hip_ctx* ctx, void* p) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    if (!p) return AR_HIP_OK;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        auto it = ctx->device_allocs.find(p);
+        if (it == ctx->device_allocs.end()) {
+            ar_set_error("pointer %p is not owned by this memory provider", p);
+            return AR_HIP_ERR_NOT_FOUND;
+        }
+        ctx->device_bytes -= it->second;
+        ctx->device_allocs.erase(it);
+    }
+    AR_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    AR_HIP_TRY(hipFree(p));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_alloc(ar_hip_ctx* ctx, size_t bytes, void** device_ptr) {
+    return ar_ctx_alloc(ctx, bytes, device_ptr);
+}
+
+extern "C" int ar_hip_free(ar_hip_ctx* ctx, void* device_ptr) { return ar_ctx_free(ctx, device_ptr); }
+
+extern "C" int ar_hip_host_alloc(ar_hip_ctx* ctx, size_t bytes, void** pinned_ptr) {
+    AR_CHECK_ARG(ctx && pinned_ptr, "null argument");
+    AR_CHECK_ARG(bytes > 0, "allocation of 0 bytes");
+    void* p = nullptr;
+    AR_HIP_TRY(hipHostMalloc(&p, bytes, hipHostMallocDefault));
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->host_allocs[p] = bytes;
+    *pinned_ptr = p;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_host_free(ar_hip_ctx* ctx, void* pinned_ptr) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    if (!pinned_ptr) return AR_HIP_OK;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        auto it = ctx->host_allocs.find(pinned_ptr);
+        if (it == ctx->host_allocs.end()) {
+            ar_set_error("pinned pointer %p is not owned by this memory provider", pinned_ptr);
+            return AR_HIP_ERR_NOT_FOUND;
+        }
+        ctx->host_allocs.erase(it);
+    }
+    AR_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    AR_HIP_TRY(hipHostFree(pinned_ptr));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_memcpy_h2d(ar_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    AR_CHECK_ARG(ctx && (bytes == 0 || (dst && src)), "null argument");
+    if (!bytes) return AR_HIP_OK;
+    AR_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    AR_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_memcpy_d2h(ar_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    AR_CHECK_ARG(ctx && (bytes == 0 || (dst && src)), "null argument");
+    if (!bytes) return AR_HIP_OK;
+    AR_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    AR_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_memcpy_d2d(ar_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    AR_CHECK_ARG(ctx && (bytes == 0 || (dst && src)), "null argument");
+    if (!bytes) return AR_HIP_OK;
+    AR_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_memset(ar_hip_ctx* ctx, void* dst, int value, size_t bytes) {
+    AR_CHECK_ARG(ctx && (bytes == 0 || dst), "null argument");
+    if (!bytes) return AR_HIP_OK;
+    AR_HIP_TRY(hipMemsetAsync(dst, value, bytes, ctx->stream));
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_allocated_bytes(ar_hip_ctx* ctx, size_t* bytes) {
+    AR_CHECK_ARG(ctx && bytes, "null argument");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    *bytes = ctx->device_bytes;
+    return AR_HIP_OK;
+}

@@ -1,0 +1,227 @@
+"""ctypes binding of the HIP backend's context, memory provider and operators.
+
+Python stand-ins for the reference's backend SPI objects
+(base/code/src/main/java/io/almostrealism/code/DataContext.java:81-88,
+ComputeContext.java:89,133, MemoryProvider.java:60-188), written as a JNI bridge would
+bind the same C-ABI (include/ar_hip.h).  Every call goes to the native library: there
+is no Python or CPU fallback, and a missing library raises ``NativeLibraryMissing``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+
+from . import _native
+
+AR_HIP_OK = 0
+AR_HIP_ERR_INVALID = 1
+AR_HIP_ERR_HIP = 2
+AR_HIP_ERR_NO_DEVICE = 3
+AR_HIP_ERR_STATE = 4
+AR_HIP_ERR_NOT_FOUND = 5
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+_c_void_pp = ctypes.POINTER(ctypes.c_void_p)
+_c_int_p = ctypes.POINTER(ctypes.c_int)
+_c_float_p = ctypes.c_void_p
+_SIGS = {
+    "ar_hip_last_error": (ctypes.c_char_p, []),
+    "ar_hip_version": (ctypes.c_char_p, []),
+    "ar_hip_device_count": (ctypes.c_int, [_c_int_p]),
+    "ar_hip_init": (ctypes.c_int, [ctypes.c_int, _c_void_pp]),
+    "ar_hip_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_device_info": (ctypes.c_int, [ctypes.c_void_p, _c_int_p, ctypes.POINTER(ctypes.c_size_t),
+                                          ctypes.c_char_p, ctypes.c_int]),
+    "ar_hip_alloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, _c_void_pp]),
+    "ar_hip_free": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_host_alloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, _c_void_pp]),
+    "ar_hip_host_free": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_memcpy_h2d": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    "ar_hip_memcpy_d2h": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    "ar_hip_memcpy_d2d": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    "ar_hip_memset": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]),
+    "ar_hip_allocated_bytes": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]),
+    "ar_hip_rmsnorm": (ctypes.c_int, [ctypes.c_void_p, _c_float_p, _c_float_p, _c_float_p, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_float]),
+    "ar_hip_dense": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _c_float_p, _c_float_p,
+                                    _c_float_p, ctypes.c_float, _c_float_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int]),
+    "ar_hip_swiglu": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _c_float_p,
+                                     _c_float_p, ctypes.c_float, _c_float_p, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int]),
+    "ar_hip_rope": (ctypes.c_int, [ctypes.c_void_p, _c_float_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_double, ctypes.c_int]),
+    "ar_hip_index_of_max": (ctypes.c_int, [ctypes.c_void_p, _c_float_p, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_void_p]),
+    "ar_hip_attention_decode": (ctypes.c_int, [ctypes.c_void_p, _c_float_p, _c_float_p, _c_float_p, _c_float_p,
+                                               _c_float_p, ctypes.c_float, ctypes.c_int, _c_float_p, _c_float_p,
+                                               ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int, ctypes.c_double, _c_float_p]),
+    "ar_hip_qwen3_create": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _c_void_pp]),
+    "ar_hip_qwen3_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_qwen3_set_weight": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int,
+                                               ctypes.c_int64]),
+    "ar_hip_qwen3_finalize": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_qwen3_reset": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_qwen3_set_prompt": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int]),
+    "ar_hip_qwen3_next": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_qwen3_run": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
+    "ar_hip_qwen3_position": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
+    "ar_hip_qwen3_hidden": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_qwen3_kernel_timing": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "ar_hip_qwen3_kernel_time": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), _c_int_p]),
+    "ar_hip_qwen3_use_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+}
+
+
+class HardwareException(RuntimeError):
+    """Raised for a non-zero C-ABI status (the reference's HardwareException)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[ar_hip error {code}] {message}")
+        self.code = code
+
+
+def lib():
+    L = _native.load_hip()
+    if not getattr(L, "_ar_typed", False):
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        L._ar_typed = True
+    return L
+
+
+def check(code: int):
+    if code != AR_HIP_OK:
+        raise HardwareException(code, lib().ar_hip_last_error().decode(errors="replace"))
+
+
+def declared_symbols(header: str | None = None) -> list[str]:
+    """Names of every function include/ar_hip.h declares."""
+    if header is None:
+        header = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "ar_hip.h")
+    text = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ar_hip_\w+)\s*\(", text, flags=re.M)))
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    rc = lib().ar_hip_device_count(ctypes.byref(n))
+    return n.value if rc == AR_HIP_OK else 0
+
+
+class DeviceBuffer:
+    """A device allocation owned by a HipMemoryProvider (HipMemory in the JNI mapping)."""
+
+    def __init__(self, ctx: "HipContext", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib().ar_hip_alloc(ctx.handle, self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, ctx: "HipContext", a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(ctx, max(a.nbytes, 16))
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(a)
+        if offset + a.nbytes > self.nbytes:
+            raise ValueError("upload past the end of the buffer")
+        check(lib().ar_hip_memcpy_h2d(self.ctx.handle, self.ptr + offset, a.ctypes.data, a.nbytes))
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download past the end of the buffer")
+        check(lib().ar_hip_memcpy_d2h(self.ctx.handle, out.ctypes.data, self.ptr + offset, out.nbytes))
+        return out
+
+    def zero(self):
+        check(lib().ar_hip_memset(self.ctx.handle, self.ptr, 0, self.nbytes))
+
+    def free(self):
+        if self.ptr is not None:
+            check(lib().ar_hip_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+
+class HipContext:
+    """One GPU: data context + compute context (one in-order stream) + memory provider."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        check(lib().ar_hip_init(device, ctypes.byref(h)))
+        self.handle = h.value
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            check(lib().ar_hip_destroy(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def synchronize(self):
+        check(lib().ar_hip_synchronize(self.handle))
+
+    def info(self):
+        cus = ctypes.c_int()
+        hbm = ctypes.c_size_t()
+        name = ctypes.create_string_buffer(64)
+        check(lib().ar_hip_device_info(self.handle, ctypes.byref(cus), ctypes.byref(hbm), name, 64))
+        return {"num_cus": cus.value, "hbm_bytes": hbm.value, "arch": name.value.decode()}
+
+    def allocated_bytes(self) -> int:
+        v = ctypes.c_size_t()
+        check(lib().ar_hip_allocated_bytes(self.handle, ctypes.byref(v)))
+        return v.value
+
+    # memory provider --------------------------------------------------------------
+    def allocate(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, a: np.ndarray) -> DeviceBuffer:
+        return DeviceBuffer.from_array(self, a)
+
+    # operators (see include/ar_hip.h for the reference each mirrors) ----------------
+    def rmsnorm(self, x: DeviceBuffer, w: DeviceBuffer, y: DeviceBuffer, rows: int, n: int, eps: float):
+        check(lib().ar_hip_rmsnorm(self.handle, x.ptr, w.ptr, y.ptr, rows, n, eps))
+
+    def dense(self, W: DeviceBuffer, w_dtype: int, x: DeviceBuffer, y: DeviceBuffer, rows: int, cols: int,
+              batch: int = 1, bias: DeviceBuffer | None = None, norm_w: DeviceBuffer | None = None,
+              eps: float = 1e-6):
+        check(lib().ar_hip_dense(self.handle, W.ptr, w_dtype, bias.ptr if bias else None, x.ptr,
+                                 norm_w.ptr if norm_w else None, eps, y.ptr, rows, cols, batch))
+
+    def swiglu(self, Wg: DeviceBuffer, Wu: DeviceBuffer, w_dtype: int, x: DeviceBuffer, y: DeviceBuffer,
+               rows: int, cols: int, batch: int = 1, norm_w: DeviceBuffer | None = None, eps: float = 1e-6):
+        check(lib().ar_hip_swiglu(self.handle, Wg.ptr, Wu.ptr, w_dtype, x.ptr, norm_w.ptr if norm_w else None,
+                                  eps, y.ptr, rows, cols, batch))
+
+    def rope(self, x: DeviceBuffer, heads: int, head_dim: int, pos: int, theta: float, rows: int = 1):
+        check(lib().ar_hip_rope(self.handle, x.ptr, heads, head_dim, pos, theta, rows))
+
+    def index_of_max(self, x: DeviceBuffer, rows: int, n: int, out: DeviceBuffer):
+        check(lib().ar_hip_index_of_max(self.handle, x.ptr, rows, n, out.ptr))
+
+    def attention_decode(self, q, k, v, q_norm, k_norm, qk_eps, qk_norm_mode, k_cache, v_cache, max_seq, pos,
+                         heads, kv_heads, head_dim, theta, out):
+        check(lib().ar_hip_attention_decode(
+            self.handle, q.ptr, k.ptr, v.ptr, q_norm.ptr if q_norm else None, k_norm.ptr if k_norm else None,
+            qk_eps, qk_norm_mode, k_cache.ptr, v_cache.ptr, max_seq, pos, heads, kv_heads, head_dim, theta, out.ptr))

@@ -1,0 +1,127 @@
+"""Qwen3 model runtime on the HIP backend, mirroring the reference's model API.
+
+``Qwen3(config, state_dict)`` builds the device model from HF-named tensors as
+``Qwen3.model`` does (engine/ml/src/main/java/org/almostrealism/ml/qwen3/Qwen3.java:334-415),
+and ``Qwen3.model`` returns an ``AutoregressiveModel`` with the reference's
+``reset`` / ``set_prompt`` / ``next`` token loop
+(engine/ml/src/main/java/org/almostrealism/ml/AutoregressiveModel.java:203-220,295-308).
+All work happens in the native library (include/ar_hip.h).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import hardware as hw
+from .config import DTYPE_BF16, Qwen3Config
+
+KT_NONE, KT_LOGITS, KT_GATE_UP, KT_QKV, KT_ATTENTION, KT_DOWN, KT_O = range(7)
+
+
+class _Cfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "dim", "hidden_dim", "layer_count", "head_count", "kv_head_count", "head_size", "vocab_size", "seq_len",
+        "max_batch", "weight_dtype", "qk_norm_mode", "shared_weights", "qkv_bias", "reserved")] + [
+        ("rope_theta", ctypes.c_double), ("epsilon", ctypes.c_double)]
+
+
+def native_cfg(c: Qwen3Config) -> _Cfg:
+    return _Cfg(c.dim, c.hidden_dim, c.layer_count, c.head_count, c.kv_head_count, c.head_size, c.vocab_size,
+                c.seq_len, c.max_batch, c.weight_dtype, c.qk_norm_mode, int(c.shared_weights), int(c.qkv_bias), 0,
+                c.rope_theta, c.epsilon)
+
+
+class AutoregressiveModel:
+    """Token loop over the device model: prompt tokens are fed one per step, then the greedy
+    choice from the previous step's logits (AutoregressiveModel.next, :295-308)."""
+
+    def __init__(self, qwen: "Qwen3"):
+        self.qwen = qwen
+        self.batch = qwen.config.max_batch
+
+    @property
+    def handle(self):
+        return self.qwen.handle
+
+    def reset(self):
+        hw.check(hw.lib().ar_hip_qwen3_reset(self.handle))
+
+    def set_prompt(self, ids, seq: int = 0):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        hw.check(hw.lib().ar_hip_qwen3_set_prompt(self.handle, seq, ids.ctypes.data, ids.size))
+
+    def next(self, return_logits: bool = False):
+        toks = np.empty(self.batch, dtype=np.int32)
+        logits = np.empty((self.batch, self.qwen.config.vocab_size), dtype=np.float32) if return_logits else None
+        hw.check(hw.lib().ar_hip_qwen3_next(self.handle, toks.ctypes.data,
+                                            logits.ctypes.data if return_logits else None))
+        return (toks, logits) if return_logits else toks
+
+    def run(self, steps: int) -> np.ndarray:
+        """``steps`` calls of next() without host synchronisation; returns (batch, steps) tokens."""
+        out = np.empty((self.batch, steps), dtype=np.int32)
+        hw.check(hw.lib().ar_hip_qwen3_run(self.handle, steps, out.ctypes.data))
+        return out
+
+    def get_current_step(self) -> int:
+        v = ctypes.c_int()
+        hw.check(hw.lib().ar_hip_qwen3_position(self.handle, ctypes.byref(v)))
+        return v.value
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty((self.batch, self.qwen.config.dim), dtype=np.float32)
+        hw.check(hw.lib().ar_hip_qwen3_hidden(self.handle, out.ctypes.data))
+        return out
+
+    def use_graph(self, enable: bool):
+        hw.check(hw.lib().ar_hip_qwen3_use_graph(self.handle, int(enable)))
+
+    def kernel_timing(self, which: int):
+        hw.check(hw.lib().ar_hip_qwen3_kernel_timing(self.handle, which))
+
+    def kernel_time(self):
+        ms = ctypes.c_double()
+        n = ctypes.c_int()
+        hw.check(hw.lib().ar_hip_qwen3_kernel_time(self.handle, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+
+class Qwen3:
+    """Device-resident Qwen3 built from an HF-keyed state dict (or an iterator of (key, tensor))."""
+
+    def __init__(self, config: Qwen3Config, state_dict, ctx: hw.HipContext | None = None):
+        self.config = config
+        self.ctx = ctx or hw.HipContext(0)
+        self._own_ctx = ctx is None
+        h = ctypes.c_void_p()
+        cfg = native_cfg(config)
+        hw.check(hw.lib().ar_hip_qwen3_create(self.ctx.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        self.handle = h.value
+        items = state_dict.items() if isinstance(state_dict, dict) else state_dict
+        for key, t in items:
+            self.set_weight(key, t)
+        hw.check(hw.lib().ar_hip_qwen3_finalize(self.handle))
+        self.model = AutoregressiveModel(self)
+
+    def set_weight(self, key: str, t: np.ndarray):
+        t = np.ascontiguousarray(t, dtype=np.float32)
+        hw.check(hw.lib().ar_hip_qwen3_set_weight(self.handle, key.encode(), t.ctypes.data, hw.DTYPE_F32, t.size))
+
+    def close(self):
+        if self.handle:
+            hw.check(hw.lib().ar_hip_qwen3_destroy(self.handle))
+            self.handle = None
+        if self._own_ctx and self.ctx:
+            self.ctx.close()
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def weight_bytes(self) -> int:
+        return 2 if self.config.weight_dtype == DTYPE_BF16 else 4

@@ -1,0 +1,187 @@
+/*
+ * ar_hip.h -- C-ABI of the MI355X (gfx950) HIP backend for the Qwen3 decode/prefill path.
+ *
+ * Plain C: opaque handles, POD structs, raw pointers and sizes.  Every function returns
+ * AR_HIP_OK (0) or an error code; ar_hip_last_error() gives the calling thread's message.
+ * A JNI bridge maps `long` handles to these pointers and turns a non-zero code into
+ * HardwareException.
+ *
+ * Reference interfaces each group replaces are cited as path:line under
+ * almostrealism/common.
+ */
+#ifndef AR_HIP_H
+#define AR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ----------------------------------------------------------------- */
+#define AR_HIP_OK 0
+#define AR_HIP_ERR_INVALID 1   /* bad argument (IllegalArgumentException in the reference) */
+#define AR_HIP_ERR_HIP 2       /* HIP runtime error (HardwareException) */
+#define AR_HIP_ERR_NO_DEVICE 3 /* no usable GPU: driver init fails (Hardware.java:771-777) */
+#define AR_HIP_ERR_STATE 4     /* call out of order (missing weight, position past capacity) */
+#define AR_HIP_ERR_NOT_FOUND 5 /* unknown weight key / allocation not owned by this provider */
+
+/* ---- element types ---------------------------------------------------------------- */
+#define AR_DTYPE_F32 0
+#define AR_DTYPE_BF16 1
+
+/* ---- QK-norm grouping ------------------------------------------------------------- */
+#define AR_QK_NORM_WHOLE 0    /* one RMS over the whole q / k vector (AttentionFeatures.java:840-845, :886-891) */
+#define AR_QK_NORM_PER_HEAD 1 /* one RMS per head (HF Qwen3) */
+
+typedef struct ar_hip_ctx ar_hip_ctx;
+typedef struct ar_qwen3 ar_qwen3;
+
+/* Thread-local message for the last failing call on this thread ("" if none). */
+const char *ar_hip_last_error(void);
+/* Library version string. */
+const char *ar_hip_version(void);
+
+/* ---- data context / compute context ------------------------------------------------
+ * Replaces DataContext.init/destroy/getComputeContexts
+ * (base/code/src/main/java/io/almostrealism/code/DataContext.java:81-88) and
+ * ComputeContext (base/code/src/main/java/io/almostrealism/code/ComputeContext.java:89,133)
+ * for the HIP driver: one context per GPU, one in-order HIP stream per context. */
+int ar_hip_device_count(int *count);
+int ar_hip_init(int device, ar_hip_ctx **out);
+int ar_hip_destroy(ar_hip_ctx *ctx);
+int ar_hip_synchronize(ar_hip_ctx *ctx);
+/* Number of compute units and HBM bytes of the context's device. */
+int ar_hip_device_info(ar_hip_ctx *ctx, int *num_cus, size_t *hbm_bytes, char *name, int name_len);
+
+/* ---- memory provider -----------------------------------------------------------------
+ * Replaces MemoryProvider.allocate / deallocate / setMem / getMem
+ * (base/code/src/main/java/io/almostrealism/code/MemoryProvider.java:60,70,158,188) and the
+ * JNI provider's malloc/free (base/hardware/src/main/java/org/almostrealism/nio/NativeMemoryProvider.java).
+ * Sizes are bytes; copies are ordered on the context's stream and complete on return. */
+int ar_hip_alloc(ar_hip_ctx *ctx, size_t bytes, void **device_ptr);
+int ar_hip_free(ar_hip_ctx *ctx, void *device_ptr);
+int ar_hip_host_alloc(ar_hip_ctx *ctx, size_t bytes, void **pinned_ptr); /* pinned staging */
+int ar_hip_host_free(ar_hip_ctx *ctx, void *pinned_ptr);
+int ar_hip_memcpy_h2d(ar_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int ar_hip_memcpy_d2h(ar_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int ar_hip_memcpy_d2d(ar_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int ar_hip_memset(ar_hip_ctx *ctx, void *dst, int value, size_t bytes);
+/* Bytes currently held by the provider. */
+int ar_hip_allocated_bytes(ar_hip_ctx *ctx, size_t *bytes);
+
+/* ---- operators (device pointers, fp32 activations) --------------------------------
+ * Each runs on the context's stream and returns after enqueueing; call
+ * ar_hip_synchronize before reading results on the host. */
+
+/* rmsnorm over the last axis: y = (w * x) / sqrt(mean(x^2) + eps), `rows` vectors of n.
+ * NormalizationLayerFeatures.rmsnorm (domain/graph/.../layers/NormalizationLayerFeatures.java:574-604). */
+int ar_hip_rmsnorm(ar_hip_ctx *ctx, const float *x, const float *w, float *y, int rows, int n, float eps);
+
+/* dense: y[b] = W x[b] (+ bias) for W (rows x cols) row-major, fp32 or bf16, batch <= 8.
+ * If norm_w is non-null the input is first RMS-normalised with that gain (fused prologue).
+ * LayerFeatures.dense (domain/graph/.../layers/LayerFeatures.java:785-830) ->
+ * MatrixFeatures.matmul (compute/algebra/.../MatrixFeatures.java:182-337). */
+int ar_hip_dense(ar_hip_ctx *ctx, const void *W, int w_dtype, const float *bias, const float *x,
+                 const float *norm_w, float eps, float *y, int rows, int cols, int batch);
+
+/* SwiGLU feed-forward hidden: y[b] = (Wup h) * silu(Wgate h), h = rmsnorm(x[b]; norm_w) when
+ * norm_w is non-null.  FeedForwardFeatures.feedForward (engine/ml/.../FeedForwardFeatures.java:140-157),
+ * silu (domain/graph/.../ActivationFeatures.java:263-265). */
+int ar_hip_swiglu(ar_hip_ctx *ctx, const void *W_gate, const void *W_up, int w_dtype, const float *x,
+                  const float *norm_w, float eps, float *y, int rows, int cols, int batch);
+
+/* Split-half RoPE in place on `rows` flat vectors of heads*head_dim at position pos.
+ * reshapeToSplitHalfRope -> ropeRotation -> reshapeFromSplitHalfRope
+ * (engine/ml/.../AttentionFeatures.java:195-237; engine/ml/.../RotationFeatures.java:124-208). */
+int ar_hip_rope(ar_hip_ctx *ctx, float *x, int heads, int head_dim, int pos, double theta, int rows);
+
+/* First index of the maximum of each of `rows` vectors of n (ties -> lowest index).
+ * AggregationFeatures.indexOfMax (compute/algebra/.../AggregationFeatures.java:111-121). */
+int ar_hip_index_of_max(ar_hip_ctx *ctx, const float *x, int rows, int n, int32_t *out_device);
+
+/* Decode-step GQA attention block core for one position: QK-norm of the raw q and k
+ * projections, split-half RoPE, cache write of k and v at row `pos`, causal attention over
+ * rows 0..pos with a split-context online softmax.
+ *   q (heads*hd), k, v (kv_heads*hd): raw projections (fp32, device)
+ *   k_cache, v_cache: (kv_heads, max_seq, hd) fp32, device; row pos is overwritten
+ *   out: (heads*hd) fp32, device
+ * AttentionFeatures.attentionImpl (engine/ml/.../AttentionFeatures.java:785-929): the block
+ * between the projections and the o_proj dense. */
+int ar_hip_attention_decode(ar_hip_ctx *ctx, const float *q, const float *k, const float *v,
+                            const float *q_norm, const float *k_norm, float qk_eps, int qk_norm_mode,
+                            float *k_cache, float *v_cache, int max_seq, int pos, int heads,
+                            int kv_heads, int head_dim, double rope_theta, float *out);
+
+/* ---- Qwen3 model -------------------------------------------------------------------
+ * Replaces Qwen3.model + CompiledModel.forward + AutoregressiveModel
+ * (engine/ml/.../qwen3/Qwen3.java:334-415, domain/graph/.../model/CompiledModel.java:189-197,
+ * engine/ml/.../AutoregressiveModel.java:295-308,405-434) with one fused decode-step plan. */
+typedef struct ar_qwen3_cfg {
+    int32_t dim;           /* TransformerConfig.dim */
+    int32_t hidden_dim;    /* FFN width */
+    int32_t layer_count;
+    int32_t head_count;
+    int32_t kv_head_count;
+    int32_t head_size;     /* explicit; the reference derives dim/headCount (TransformerConfig.java:79) */
+    int32_t vocab_size;
+    int32_t seq_len;       /* KV-cache capacity in positions */
+    int32_t max_batch;     /* independent sequences decoded together (1..8) */
+    int32_t weight_dtype;  /* AR_DTYPE_F32 or AR_DTYPE_BF16 (fp32 accumulation either way) */
+    int32_t qk_norm_mode;  /* AR_QK_NORM_WHOLE (reference) or AR_QK_NORM_PER_HEAD */
+    int32_t shared_weights;/* tied embeddings: logits use model.embed_tokens.weight */
+    int32_t qkv_bias;      /* q/k/v projection biases present */
+    int32_t reserved;
+    double rope_theta;
+    double epsilon;        /* RMSNorm eps (1e-6, Qwen3.java:397,402); QK-norm uses the same */
+} ar_qwen3_cfg;
+
+int ar_hip_qwen3_create(ar_hip_ctx *ctx, const ar_qwen3_cfg *cfg, ar_qwen3 **out);
+int ar_hip_qwen3_destroy(ar_qwen3 *m);
+
+/* Uploads one tensor by its HF state-dict key, as StateDictionary.get supplies them to
+ * Qwen3.model (engine/ml/.../StateDictionary.java; Qwen3.java:338-384).  src is host memory
+ * holding n_elems values of src_dtype in the HF (out, in) row-major layout. */
+int ar_hip_qwen3_set_weight(ar_qwen3 *m, const char *key, const void *src, int src_dtype, int64_t n_elems);
+/* Checks every required tensor is present and builds the decode plan. */
+int ar_hip_qwen3_finalize(ar_qwen3 *m);
+
+/* AutoregressiveModel.reset (AutoregressiveModel.java:203-207): position 0. */
+int ar_hip_qwen3_reset(ar_qwen3 *m);
+/* AutoregressiveModel.setPrompt: prompt ids for sequence `seq` (all sequences of a batch
+ * share one prompt length). */
+int ar_hip_qwen3_set_prompt(ar_qwen3 *m, int seq, const int32_t *ids, int n);
+/* AutoregressiveModel.next (AutoregressiveModel.java:295-308) for every sequence: feeds the
+ * prompt token or the greedy choice from the previous step's logits, runs one forward pass
+ * and advances.  tokens_out[b] receives the token fed at this step; logits_out (optional,
+ * batch x vocab floats, host) receives this step's logits. */
+int ar_hip_qwen3_next(ar_qwen3 *m, int32_t *tokens_out, float *logits_out);
+/* `steps` calls of next() enqueued back to back without host synchronisation (the token
+ * loop stays on the device); tokens_out is batch x steps (row-major by sequence). */
+int ar_hip_qwen3_run(ar_qwen3 *m, int steps, int32_t *tokens_out);
+/* Current position (AutoregressiveModel.getCurrentStep). */
+int ar_hip_qwen3_position(ar_qwen3 *m, int *pos);
+/* Residual-stream vector after the last step (batch x dim floats, host) for activation checks. */
+int ar_hip_qwen3_hidden(ar_qwen3 *m, float *out);
+
+/* Kernel timing probe: when enabled, HIP events bracket every launch of kernel class `which`
+ * (AR_KT_*) on the model's stream; ar_hip_qwen3_kernel_time returns the summed milliseconds and
+ * the launch count since the last enable. */
+#define AR_KT_NONE 0
+#define AR_KT_LOGITS 1      /* final RMSNorm + logits GEMV + argmax */
+#define AR_KT_GATE_UP 2     /* RMSNorm + gate/up GEMV + SwiGLU */
+#define AR_KT_QKV 3
+#define AR_KT_ATTENTION 4
+#define AR_KT_DOWN 5
+#define AR_KT_O 6
+int ar_hip_qwen3_kernel_timing(ar_qwen3 *m, int which);
+int ar_hip_qwen3_kernel_time(ar_qwen3 *m, double *ms, int *launches);
+/* Use a captured HIP graph per decode step (1, default) or plain launches (0). */
+int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AR_HIP_H */
