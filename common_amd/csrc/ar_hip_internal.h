@@ -82,26 +82,20 @@ struct GemvLaunch {
     float* y = nullptr;            // [batch][y_stride]
     int y_stride = 0;
     int epilogue = 0;              // GEMV_EPI_*
-    // argmax epilogue
-    float* part_val = nullptr;     // [grid][batch]
-    int* part_idx = nullptr;
-    unsigned* counter = nullptr;   // zero before first use; the last block resets it
-    int* tokens = nullptr;         // [batch][token_stride]
-    int token_stride = 0;
-    int* state = nullptr;          // device {position, prompt length}: tokens[pos+1] is written only
-                                   // when pos+1 >= prompt length; advance=1 increments position
-    int advance = 0;
+    // argmax epilogue: packed (value, index) maxima, [batch][kArgmaxSlots], zero before use
+    unsigned long long* keys = nullptr;
 };
+
+constexpr int kArgmaxSlots = 64;
 
 enum {
     GEMV_EPI_STORE = 0,     // y = W x (+ b)
     GEMV_EPI_RESIDUAL = 1,  // y += W x
     GEMV_EPI_SWIGLU = 2,    // y = (W2 x) * silu(W x)
-    GEMV_EPI_ARGMAX = 3,    // optional y = W x; greedy token; optional position advance
+    GEMV_EPI_ARGMAX = 3,    // optional y = W x; greedy-token keys
 };
 
 int launch_gemv(const GemvLaunch& a, hipStream_t stream);
-int gemv_argmax_partials(int rows, int batch);  // partial slots the argmax epilogue needs
 
 struct AttnLaunch {
     const float* qkv = nullptr;   // [batch][qkv_stride]: q | k | v raw projections
@@ -116,21 +110,29 @@ struct AttnLaunch {
     const int* pos = nullptr;     // device position (same for every sequence)
     int heads = 0, kv_heads = 0, head_dim = 0;
     double rope_theta = 1e6;
-    int tile = 64;                // positions per split
-    int max_splits = 0;           // grid.x (splits past the live context exit at once)
+    const float2* rope_tab = nullptr;  // [max_seq][hd/2] (cos, sin) of pos*invf, or null: computed
+    int max_splits = 0;           // grid.x; the live context pos+1 is cut into at most this many
+                                  // splits of >= 16 rows (splits past it exit at once)
     float* part_o = nullptr;      // [batch][heads][max_splits][hd]
     float* part_ml = nullptr;     // [batch][heads][max_splits][2]
-    unsigned* counters = nullptr; // [batch][kv_heads], zero before first use
     float* out = nullptr;         // [batch][out_stride]
     int out_stride = 0;
     int batch = 1;
 };
 
+// Attention partials + (when the context is split) the combine kernel.
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);
+// Splits for a cache of max_seq rows: enough blocks to cover the chip, rows per split <= 256.
+int attention_max_splits(int max_seq, int kv_heads, int batch);
 
-int launch_embed(const void* table, int wdtype, int dim, const int* tokens, int token_stride,
-                 const int* pos, int batch, float* x, int x_stride, hipStream_t stream);
+// Start of a decode step (one block).  state = device {current position, prompt length, next
+// position}.  Position p = next: the token fed is the prompt token tokens[b][p] while p is inside
+// the prompt, else the greedy choice decoded from keys[b] (the previous step's logits), which is
+// also stored at tokens[b][p]; keys are then cleared, x[b] = E[token], current = p, next = p+1.
+// AutoregressiveModel.next + the embedding copy (engine/ml/.../AutoregressiveModel.java:295-308,430).
+int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* tokens, int token_stride,
+                      unsigned long long* keys, int* state, int batch, float* x, int x_stride, hipStream_t stream);
 int launch_rmsnorm(const float* x, const float* w, float* y, int rows, int n, float eps,
                    hipStream_t stream);
 int launch_rope(float* x, int heads, int hd, int pos, double theta, int rows, int row_stride,

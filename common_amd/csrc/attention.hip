@@ -17,13 +17,14 @@
 // reads KV head h / (heads / kv_heads), which holds exactly what the reference's GQA-expanded
 // cache copy (:823-826) holds.
 //
-// Grid (splits, kv_heads, batch), 256 threads.  Block (s, g, b) handles context rows
-// [s*tile, min((s+1)*tile, pos+1)) for the heads/kv_heads query heads sharing KV head g:
+// Grid (max_splits, kv_heads, batch), 256 threads.  The live context [0, pos] is cut into
+// nsplit contiguous splits of >= 16 rows (at most max_splits); block (s, g, b) handles split s
+// for the heads/kv_heads query heads sharing KV head g:
 //   phase 1: 16-lane groups compute one row's scores for all heads of the group (K row read once)
 //   phase 2: each wavefront accumulates a[t] * V[t] for every fourth row (V row read once)
-// and writes unnormalised partials (o, max, sum).  The last block of a (b, g) to finish, found
-// with an atomic counter, merges the splits and writes the normalised output; it also resets the
-// counter, so no memset is needed between launches.
+// With one split the block writes the normalised output; otherwise it writes unnormalised
+// partials (o, max, sum) that attn_combine_kernel merges in the next launch (the kernel boundary
+// makes them visible, so no block needs a device-wide fence).
 #include "ar_hip_internal.h"
 
 namespace {
@@ -44,10 +45,10 @@ struct AttnParams {
     const int* pos;
     int heads, kv_heads;
     double rope_c;  // -2 ln(theta) / hd
-    int tile, max_splits;
+    const float2* rope_tab;  // [max_seq][hd/2] (cos, sin) or null
+    int max_splits;
     float* part_o;
     float* part_ml;
-    unsigned* counters;
     float* out;
     int out_stride;
 };
@@ -77,7 +78,24 @@ __device__ inline float block_sum(float v, float* scratch) {
     return t;
 }
 
-__device__ inline void rope_cs(int pos, int f, double c, float* cs, float* sn) {
+// Split plan for a live context of n rows: nsplit splits of `tile` rows (the last may be short).
+__device__ inline void split_plan(int n, int max_splits, int* nsplit, int* tile) {
+    int ns = min(max_splits, (n + 15) / 16);
+    if (ns < 1) ns = 1;
+    const int t = (n + ns - 1) / ns;
+    *tile = t;
+    *nsplit = (n + t - 1) / t;
+}
+
+// (cos, sin) of pos * exp(f * -2 ln(theta) / hd): from the table the model precomputes in
+// double on the host, or evaluated here in double when no table is given.
+__device__ inline void rope_cs(const float2* row, int pos, int f, double c, float* cs, float* sn) {
+    if (row) {
+        const float2 t = row[f];
+        *cs = t.x;
+        *sn = t.y;
+        return;
+    }
     const double invf = exp((double)f * c);
     const double ang = (double)pos * invf;
     *cs = (float)cos(ang);
@@ -87,33 +105,71 @@ __device__ inline void rope_cs(int pos, int f, double c, float* cs, float* sn) {
 template <int HD, int G>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     constexpr int FD = HD / 2;
-    constexpr int EPL = HD / 16;     // elements per lane in a 16-lane row group
-    constexpr int VPL = HD / 64;     // value columns per lane in phase 2
+    constexpr int EPL = HD / 16;     // elements per lane in a 16-lane row group (phase 1)
+    constexpr int VPL = HD / 64;     // value columns per lane (phase 2)
+    constexpr int KU = 4;            // K rows per 16-lane group per pass  (16 groups -> 64 rows)
+    constexpr int VU = 16;           // V rows per wavefront per pass      (4 waves   -> 64 rows)
+    constexpr int PASS = 64;
     __shared__ __attribute__((aligned(16))) float q_s[G][HD];
+    __shared__ __attribute__((aligned(16))) float k_new[HD];
+    __shared__ __attribute__((aligned(16))) float v_new[HD];
     __shared__ float s_s[G][kMaxTile];
     __shared__ __attribute__((aligned(16))) float red_s[kThreads / 64][G][HD];
     __shared__ float m_s[G], l_s[G];
     __shared__ float scratch[kThreads / 64];
     __shared__ float rq_s[G], rk_s;
-    __shared__ int last_s;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = tid >> 4, gl = tid & 15;
     const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
     const int pos = *p.pos;
     if (pos < 0 || pos >= p.max_seq) return;
     const int n = pos + 1;
-    const int nsplit = (n + p.tile - 1) / p.tile;
+    int nsplit, tile;
+    split_plan(n, p.max_splits, &nsplit, &tile);
     if (split >= nsplit) return;
-    const int t0 = split * p.tile;
-    const int t1 = min(t0 + p.tile, n);
+    const int t0 = split * tile;
+    const int t1 = min(t0 + tile, n);
     const int heads = p.heads, kvH = p.kv_heads;
     const int q_dim = heads * HD, kv_dim = kvH * HD;
-    const float* q_raw = p.qkv + (size_t)b * p.qkv_stride;
-    const float* k_raw = q_raw + q_dim;
-    const float* v_raw = k_raw + kv_dim;
     const size_t head_base = ((size_t)b * kvH + kvh) * (size_t)p.max_seq * HD;
     float* kc = p.kcache + head_base;
     float* vc = p.vcache + head_base;
+
+    // ---- first pass of K and V rows, issued before anything that depends on the QKV kernel.
+    // Rows are clamped to the split (duplicates are dropped below); row `pos` is stale in the
+    // cache until this block writes it, so that row is taken from LDS instead.
+    float kr[KU][EPL];
+    float vr[VU][VPL];
+    auto load_k = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int t = min(base + grp + 16 * u, t1 - 1);
+#pragma unroll
+            for (int j = 0; j < EPL / 4; j++) {
+                const float4 v = *reinterpret_cast<const float4*>(kc + (size_t)t * HD + j * 64 + gl * 4);
+                kr[u][j * 4] = v.x; kr[u][j * 4 + 1] = v.y; kr[u][j * 4 + 2] = v.z; kr[u][j * 4 + 3] = v.w;
+            }
+        }
+    };
+    auto load_v = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int t = min(base + wave + 4 * u, t1 - 1);
+            if constexpr (VPL == 2) {
+                const float2 v = *reinterpret_cast<const float2*>(vc + (size_t)t * HD + lane * 2);
+                vr[u][0] = v.x; vr[u][1] = v.y;
+            } else {
+                vr[u][0] = vc[(size_t)t * HD + lane];
+            }
+        }
+    };
+    load_k(t0);
+    load_v(t0);
+
+    const float* q_raw = p.qkv + (size_t)b * p.qkv_stride;
+    const float* k_raw = q_raw + q_dim;
+    const float* v_raw = k_raw + kv_dim;
 
     // ---- QK-norm factors ----------------------------------------------------------
     if (p.q_norm || p.k_norm) {
@@ -145,6 +201,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     }
 
     // ---- normalised, rotated queries of this group -> LDS ---------------------------
+    const float2* rope_row = p.rope_tab ? p.rope_tab + (size_t)pos * FD : nullptr;
     for (int idx = tid; idx < G * FD; idx += kThreads) {
         const int g = idx / FD, f = idx - g * FD;
         const int h = kvh * G + g;
@@ -154,12 +211,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
             x2 = (p.q_norm[(size_t)h * HD + f + FD] * x2) * rq_s[g];
         }
         float c, s;
-        rope_cs(pos, f, p.rope_c, &c, &s);
+        rope_cs(rope_row, pos, f, p.rope_c, &c, &s);
         q_s[g][f] = x1 * c - x2 * s;
         q_s[g][f + FD] = x2 * c + x1 * s;
     }
-    // ---- the split holding `pos` writes this step's k and v rows ---------------------
-    if (pos >= t0 && pos < t1) {
+    // ---- the split holding `pos` writes this step's k and v rows (cache + LDS) ---------
+    const bool has_pos = pos >= t0 && pos < t1;
+    if (has_pos) {
         for (int f = tid; f < FD; f += kThreads) {
             float x1 = k_raw[(size_t)kvh * HD + f], x2 = k_raw[(size_t)kvh * HD + f + FD];
             if (p.k_norm) {
@@ -167,41 +225,44 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
                 x2 = (p.k_norm[(size_t)kvh * HD + f + FD] * x2) * rk_s;
             }
             float c, s;
-            rope_cs(pos, f, p.rope_c, &c, &s);
-            kc[(size_t)pos * HD + f] = x1 * c - x2 * s;
-            kc[(size_t)pos * HD + f + FD] = x2 * c + x1 * s;
+            rope_cs(rope_row, pos, f, p.rope_c, &c, &s);
+            const float o1 = x1 * c - x2 * s, o2 = x2 * c + x1 * s;
+            k_new[f] = o1;
+            k_new[f + FD] = o2;
+            kc[(size_t)pos * HD + f] = o1;
+            kc[(size_t)pos * HD + f + FD] = o2;
         }
-        for (int i = tid; i < HD; i += kThreads) vc[(size_t)pos * HD + i] = v_raw[(size_t)kvh * HD + i];
-        __threadfence_block();
+        for (int i = tid; i < HD; i += kThreads) {
+            const float v = v_raw[(size_t)kvh * HD + i];
+            v_new[i] = v;
+            vc[(size_t)pos * HD + i] = v;
+        }
     }
     __syncthreads();
 
     // ---- phase 1: scores -----------------------------------------------------------
     {
-        const int grp = tid >> 4, gl = tid & 15;
         float qr[G][EPL];
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
             for (int j = 0; j < EPL / 4; j++) {
-                float4 t = *reinterpret_cast<const float4*>(&q_s[g][j * 64 + gl * 4]);
+                const float4 t = *reinterpret_cast<const float4*>(&q_s[g][j * 64 + gl * 4]);
                 qr[g][j * 4] = t.x; qr[g][j * 4 + 1] = t.y; qr[g][j * 4 + 2] = t.z; qr[g][j * 4 + 3] = t.w;
             }
         const float scale = sqrtf((float)HD);
-        for (int tb = t0 + grp; tb < t1; tb += 4 * 16) {
-            float kr[4][EPL];
+        for (int base = t0; base < t1; base += PASS) {
+            if (base != t0) load_k(base);
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = min(tb + u * 16, t1 - 1);
+            for (int u = 0; u < KU; u++) {
+                const int t = base + grp + 16 * u;
+                if (has_pos && t == pos) {
 #pragma unroll
-                for (int j = 0; j < EPL / 4; j++) {
-                    float4 v = *reinterpret_cast<const float4*>(kc + (size_t)t * HD + j * 64 + gl * 4);
-                    kr[u][j * 4] = v.x; kr[u][j * 4 + 1] = v.y; kr[u][j * 4 + 2] = v.z; kr[u][j * 4 + 3] = v.w;
+                    for (int j = 0; j < EPL / 4; j++) {
+                        const float4 v = *reinterpret_cast<const float4*>(&k_new[j * 64 + gl * 4]);
+                        kr[u][j * 4] = v.x; kr[u][j * 4 + 1] = v.y; kr[u][j * 4 + 2] = v.z; kr[u][j * 4 + 3] = v.w;
+                    }
                 }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = tb + u * 16;
 #pragma unroll
                 for (int g = 0; g < G; g++) {
                     float d = 0.f;
@@ -240,22 +301,16 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
         for (int g = 0; g < G; g++)
 #pragma unroll
             for (int j = 0; j < VPL; j++) acc[g][j] = 0.f;
-        for (int tb = t0 + wave; tb < t1; tb += 4 * 4) {
-            float vr[4][VPL];
+        for (int base = t0; base < t1; base += PASS) {
+            if (base != t0) load_v(base);
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = min(tb + u * 4, t1 - 1);
-                if constexpr (VPL == 2) {
-                    float2 v = *reinterpret_cast<const float2*>(vc + (size_t)t * HD + lane * 2);
-                    vr[u][0] = v.x; vr[u][1] = v.y;
-                } else {
-                    vr[u][0] = vc[(size_t)t * HD + lane];
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = tb + u * 4;
+            for (int u = 0; u < VU; u++) {
+                const int t = base + wave + 4 * u;
                 if (t < t1) {
+                    if (has_pos && t == pos) {
+#pragma unroll
+                        for (int j = 0; j < VPL; j++) vr[u][j] = v_new[lane * VPL + j];
+                    }
 #pragma unroll
                     for (int g = 0; g < G; g++) {
                         const float a = s_s[g][t - t0];
@@ -273,50 +328,43 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     __syncthreads();
 
     const int hbase = kvh * G;
-    if (nsplit == 1) {
-        for (int idx = tid; idx < G * HD; idx += kThreads) {
-            const int g = idx / HD, i = idx - g * HD;
-            float o = 0.f;
-#pragma unroll
-            for (int w = 0; w < kThreads / 64; w++) o += red_s[w][g][i];
-            p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = o / l_s[g];
-        }
-        return;
-    }
-
     for (int idx = tid; idx < G * HD; idx += kThreads) {
         const int g = idx / HD, i = idx - g * HD;
         float o = 0.f;
 #pragma unroll
         for (int w = 0; w < kThreads / 64; w++) o += red_s[w][g][i];
-        const size_t slot = ((size_t)b * heads + hbase + g) * p.max_splits + split;
-        p.part_o[slot * HD + i] = o;
-        if (i == 0) {
-            p.part_ml[slot * 2] = m_s[g];
-            p.part_ml[slot * 2 + 1] = l_s[g];
+        if (nsplit == 1) {
+            p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = o / l_s[g];
+        } else {
+            const size_t slot = ((size_t)b * heads + hbase + g) * p.max_splits + split;
+            p.part_o[slot * HD + i] = o;
+            if (i == 0) {
+                p.part_ml[slot * 2] = m_s[g];
+                p.part_ml[slot * 2 + 1] = l_s[g];
+            }
         }
     }
-    __threadfence();
-    __syncthreads();
-    unsigned* ctr = p.counters + (size_t)b * kvH + kvh;
-    if (tid == 0) last_s = (atomicAdd(ctr, 1u) == (unsigned)(nsplit - 1));
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();
-    for (int idx = tid; idx < G * HD; idx += kThreads) {
-        const int g = idx / HD, i = idx - g * HD;
-        const size_t slot0 = ((size_t)b * heads + hbase + g) * p.max_splits;
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; s++) M = fmaxf(M, p.part_ml[(slot0 + s) * 2]);
-        float L = 0.f, O = 0.f;
-        for (int s = 0; s < nsplit; s++) {
-            const float w = expf(p.part_ml[(slot0 + s) * 2] - M);
-            L = fmaf(p.part_ml[(slot0 + s) * 2 + 1], w, L);
-            O = fmaf(p.part_o[(slot0 + s) * HD + i], w, O);
-        }
-        p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = O / L;
+}
+
+// Merges the split partials of every query head: o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
+    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    const int pos = *p.pos;
+    if (pos < 0 || pos >= p.max_seq) return;
+    int nsplit, tile;
+    split_plan(pos + 1, p.max_splits, &nsplit, &tile);
+    if (nsplit == 1) return;  // the attention kernel wrote the output itself
+    const size_t slot0 = ((size_t)b * p.heads + h) * p.max_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, p.part_ml[(slot0 + s) * 2]);
+    float L = 0.f, O = 0.f;
+    for (int s = 0; s < nsplit; s++) {
+        const float w = expf(p.part_ml[(slot0 + s) * 2] - M);
+        L = fmaf(p.part_ml[(slot0 + s) * 2 + 1], w, L);
+        O = fmaf(p.part_o[(slot0 + s) * HD + i], w, O);
     }
-    if (tid == 0) *ctr = 0u;
+    p.out[(size_t)b * p.out_stride + (size_t)h * HD + i] = O / L;
 }
 
 template <int HD, int G>
@@ -326,11 +374,16 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
     p.qk_eps = a.qk_eps; p.per_head_norm = a.per_head_norm; p.kcache = a.kcache; p.vcache = a.vcache;
     p.max_seq = a.max_seq; p.pos = a.pos; p.heads = a.heads; p.kv_heads = a.kv_heads;
     p.rope_c = -2.0 * log(a.rope_theta) / (double)HD;
-    p.tile = a.tile; p.max_splits = a.max_splits; p.part_o = a.part_o; p.part_ml = a.part_ml;
-    p.counters = a.counters; p.out = a.out; p.out_stride = a.out_stride;
+    p.rope_tab = a.rope_tab;
+    p.max_splits = a.max_splits; p.part_o = a.part_o; p.part_ml = a.part_ml;
+    p.out = a.out; p.out_stride = a.out_stride;
     hipLaunchKernelGGL((attn_decode_kernel<HD, G>), dim3(a.max_splits, a.kv_heads, a.batch), dim3(kThreads), 0,
                        stream, p);
     AR_LAUNCH_CHECK();
+    if (a.max_splits > 1) {
+        hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.heads, a.batch), dim3(HD), 0, stream, p);
+        AR_LAUNCH_CHECK();
+    }
     return AR_HIP_OK;
 }
 
@@ -352,15 +405,22 @@ size_t attention_partial_floats(int batch, int heads, int max_splits, int hd) {
     return (size_t)batch * heads * max_splits * (size_t)hd;
 }
 
+int attention_max_splits(int max_seq, int kv_heads, int batch) {
+    const int need = (max_seq + kMaxTile - 1) / kMaxTile;      // rows per split <= kMaxTile
+    const int want = (1024 + kv_heads * batch - 1) / (kv_heads * batch);  // ~4 blocks per CU
+    const int cap = (max_seq + 15) / 16;                       // splits of >= 16 rows
+    int s = want < cap ? want : cap;
+    if (s < need) s = need;
+    return s < 1 ? 1 : s;
+}
+
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(a.qkv && a.kcache && a.vcache && a.pos && a.out, "attention: null pointer");
     AR_CHECK_ARG(a.heads > 0 && a.kv_heads > 0 && a.heads % a.kv_heads == 0, "attention: bad head counts %d/%d",
                  a.heads, a.kv_heads);
-    AR_CHECK_ARG(a.tile >= 16 && a.tile <= kMaxTile && a.tile % 16 == 0, "attention: tile %d outside 16..%d",
-                 a.tile, kMaxTile);
-    AR_CHECK_ARG(a.max_splits >= 1 && (long long)a.max_splits * a.tile >= a.max_seq,
-                 "attention: %d splits of %d do not cover %d rows", a.max_splits, a.tile, a.max_seq);
-    AR_CHECK_ARG(a.max_splits == 1 || (a.part_o && a.part_ml && a.counters), "attention: missing split buffers");
+    AR_CHECK_ARG(a.max_splits >= 1 && (long long)a.max_splits * kMaxTile >= a.max_seq,
+                 "attention: %d splits of at most %d rows do not cover %d rows", a.max_splits, kMaxTile, a.max_seq);
+    AR_CHECK_ARG(a.max_splits == 1 || (a.part_o && a.part_ml), "attention: missing split buffers");
     AR_CHECK_ARG(a.batch >= 1 && a.batch <= 65535, "attention: bad batch %d", a.batch);
     AR_CHECK_ARG((reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.vcache) & 15) == 0,
                  "attention: caches must be 16-byte aligned");

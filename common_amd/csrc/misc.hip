@@ -13,20 +13,56 @@ __device__ inline bool better(float v1, int i1, float v2, int i2) {
     return v1 > v2 || (v1 == v2 && i1 < i2);
 }
 
-// x[b] = E[tokens[b][pos]]: the embedding lookup AutoregressiveModel does with a host copy
-// (engine/ml/.../AutoregressiveModel.java:430), done on the device so the token never leaves it.
+// Start of a decode step, one block: picks the token fed at position p for every sequence (the
+// prompt token, or the greedy choice of the previous step decoded from the packed argmax keys),
+// clears the keys, copies the embedding row and publishes p as the step's position.
+// AutoregressiveModel.next + embedding copy (engine/ml/.../AutoregressiveModel.java:295-308,430).
 template <typename WT>
-__global__ void embed_kernel(const WT* table, int dim, const int* tokens, int token_stride, const int* pos,
-                             float* x, int x_stride) {
-    const int b = blockIdx.y;
-    const int p = pos ? *pos : 0;
-    const int tok = tokens[(size_t)b * token_stride + p];
-    const WT* row = table + (size_t)tok * dim;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x) {
-        float v;
-        if constexpr (sizeof(WT) == 2) v = __uint_as_float((unsigned)row[i] << 16);
-        else v = row[i];
-        x[(size_t)b * x_stride + i] = v;
+__global__ __launch_bounds__(256) void step_begin_kernel(const WT* table, int dim, int vocab, int* tokens,
+                                                         int token_stride, unsigned long long* keys, int* state,
+                                                         int batch, float* x, int x_stride) {
+    __shared__ int tok_s[8];
+    __shared__ unsigned long long red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int p = state[2];
+    const int plen = state[1];
+    for (int b = 0; b < batch; b++) {
+        if (p > 0 && p >= plen) {
+            unsigned long long k = (tid < kArgmaxSlots) ? keys[(size_t)b * kArgmaxSlots + tid] : 0ull;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const unsigned long long o = __shfl_xor(k, off, 64);
+                k = o > k ? o : k;
+            }
+            if (lane == 0) red[wave] = k;
+            __syncthreads();
+            if (tid == 0) {
+                unsigned long long m = red[0];
+                for (int w = 1; w < 4; w++) m = red[w] > m ? red[w] : m;
+                int t = m ? (int)(0xFFFFFFFFu - (unsigned)(m & 0xFFFFFFFFull)) : 0;
+                if (t < 0 || t >= vocab) t = 0;
+                tokens[(size_t)b * token_stride + p] = t;
+                tok_s[b] = t;
+            }
+            __syncthreads();
+        } else if (tid == 0) {
+            tok_s[b] = tokens[(size_t)b * token_stride + p];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < batch * kArgmaxSlots; i += blockDim.x) keys[i] = 0ull;
+    for (int b = 0; b < batch; b++) {
+        const WT* row = table + (size_t)tok_s[b] * dim;
+        for (int i = tid; i < dim; i += blockDim.x) {
+            float v;
+            if constexpr (sizeof(WT) == 2) v = __uint_as_float((unsigned)row[i] << 16);
+            else v = row[i];
+            x[(size_t)b * x_stride + i] = v;
+        }
+    }
+    if (tid == 0) {
+        state[0] = p;
+        state[2] = p + 1;
     }
 }
 
@@ -112,16 +148,16 @@ int grid_for(size_t n, int threads, int cap = 4096) {
 
 }  // namespace
 
-int launch_embed(const void* table, int wdtype, int dim, const int* tokens, int token_stride, const int* pos,
-                 int batch, float* x, int x_stride, hipStream_t stream) {
-    AR_CHECK_ARG(table && tokens && x && dim > 0 && batch >= 1, "embed: bad arguments");
-    dim3 grid(grid_for(dim, 256, 64), batch);
+int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* tokens, int token_stride,
+                      unsigned long long* keys, int* state, int batch, float* x, int x_stride, hipStream_t stream) {
+    AR_CHECK_ARG(table && tokens && keys && state && x && dim > 0, "step begin: bad arguments");
+    AR_CHECK_ARG(batch >= 1 && batch <= 8, "step begin: batch %d outside 1..8", batch);
     if (wdtype == AR_DTYPE_BF16)
-        hipLaunchKernelGGL(embed_kernel<uint16_t>, grid, dim3(256), 0, stream, (const uint16_t*)table, dim, tokens,
-                           token_stride, pos, x, x_stride);
+        hipLaunchKernelGGL(step_begin_kernel<uint16_t>, dim3(1), dim3(256), 0, stream, (const uint16_t*)table, dim,
+                           vocab, tokens, token_stride, keys, state, batch, x, x_stride);
     else
-        hipLaunchKernelGGL(embed_kernel<float>, grid, dim3(256), 0, stream, (const float*)table, dim, tokens,
-                           token_stride, pos, x, x_stride);
+        hipLaunchKernelGGL(step_begin_kernel<float>, dim3(1), dim3(256), 0, stream, (const float*)table, dim, vocab,
+                           tokens, token_stride, keys, state, batch, x, x_stride);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -38,14 +38,13 @@ extern "C" int ar_hip_index_of_max(ar_hip_ctx* ctx, const float* x, int rows, in
 }
 
 namespace {
-// Scratch the stand-alone attention op keeps between calls: packed q|k|v, the position, split
-// partials and counters.  Grown on demand; freed with the context's allocations.
+// Scratch the stand-alone attention op keeps between calls: packed q|k|v, the position and the
+// split partials.  Grown on demand; freed with the context's allocations.
 struct AttnScratch {
-    size_t qkv_floats = 0, part_floats = 0, ml_floats = 0, ctr_count = 0;
+    size_t qkv_floats = 0, part_floats = 0, ml_floats = 0;
     float* qkv = nullptr;
     float* part_o = nullptr;
     float* part_ml = nullptr;
-    unsigned* counters = nullptr;
     int* pos = nullptr;
 };
 std::mutex g_attn_mu;
@@ -73,18 +72,12 @@ extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const fl
     std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnScratch& s = g_attn[ctx];
     const int q_dim = heads * head_dim, kv_dim = kv_heads * head_dim;
-    const int tile = max_seq >= 1024 ? 64 : 32;
-    const int max_splits = (max_seq + tile - 1) / tile;
+    const int max_splits = attention_max_splits(max_seq, kv_heads, 1);
     size_t dummy = 0;
     AR_TRY(grow(ctx, (void**)&s.qkv, &s.qkv_floats, (size_t)q_dim + 2 * kv_dim, sizeof(float)));
     AR_TRY(grow(ctx, (void**)&s.part_o, &s.part_floats, attention_partial_floats(1, heads, max_splits, head_dim),
                 sizeof(float)));
     AR_TRY(grow(ctx, (void**)&s.part_ml, &s.ml_floats, (size_t)heads * max_splits * 2, sizeof(float)));
-    if (!s.counters) {
-        AR_TRY(grow(ctx, (void**)&s.counters, &s.ctr_count, 64, sizeof(unsigned)));
-        AR_HIP_TRY(hipMemsetAsync(s.counters, 0, 64 * sizeof(unsigned), ctx->stream));
-    }
-    AR_CHECK_ARG(kv_heads <= 64, "attention: more than 64 KV heads");
     if (!s.pos) AR_TRY(grow(ctx, (void**)&s.pos, &dummy, 1, sizeof(int)));
     AR_HIP_TRY(hipMemcpyAsync(s.qkv, q, sizeof(float) * q_dim, hipMemcpyDeviceToDevice, ctx->stream));
     AR_HIP_TRY(hipMemcpyAsync(s.qkv + q_dim, k, sizeof(float) * kv_dim, hipMemcpyDeviceToDevice, ctx->stream));
@@ -94,8 +87,8 @@ extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const fl
     a.qkv = s.qkv; a.qkv_stride = q_dim + 2 * kv_dim; a.q_norm = q_norm; a.k_norm = k_norm; a.qk_eps = qk_eps;
     a.per_head_norm = qk_norm_mode == AR_QK_NORM_PER_HEAD; a.kcache = k_cache; a.vcache = v_cache;
     a.max_seq = max_seq; a.pos = s.pos; a.heads = heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
-    a.rope_theta = rope_theta; a.tile = tile; a.max_splits = max_splits; a.part_o = s.part_o; a.part_ml = s.part_ml;
-    a.counters = s.counters; a.out = out; a.out_stride = q_dim; a.batch = 1;
+    a.rope_theta = rope_theta; a.max_splits = max_splits; a.part_o = s.part_o; a.part_ml = s.part_ml;
+    a.out = out; a.out_stride = q_dim; a.batch = 1;
     return launch_attention_decode(a, ctx->stream);
 }
 

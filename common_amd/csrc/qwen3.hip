@@ -41,14 +41,6 @@ struct Layer {
     float* bqkv = nullptr;
 };
 
-int attention_tile(int seq) {
-    int t = (seq + 15) / 16;
-    t = (t + 15) / 16 * 16;
-    if (t < 16) t = 16;
-    if (t > 128) t = 128;
-    return t;
-}
-
 }  // namespace
 
 struct ar_qwen3 {
@@ -75,15 +67,13 @@ struct ar_qwen3 {
     float* vcache = nullptr;
     float* part_o = nullptr;
     float* part_ml = nullptr;
-    unsigned* attn_ctr = nullptr;
-    float* am_val = nullptr;
-    int* am_idx = nullptr;
-    unsigned* am_ctr = nullptr;
+    unsigned long long* am_keys = nullptr;  // [B][kArgmaxSlots] greedy-token keys
+    float2* rope_tab = nullptr;             // [S][hd/2] (cos, sin), computed in double on the host
     int* tokens = nullptr;    // [B][S+1]
-    int* state = nullptr;     // {position, prompt length}
+    int* state = nullptr;     // {current position, prompt length, next position}
     float* staging = nullptr; // fp32 upload staging for dtype conversion
     size_t staging_floats = 0;
-    int tile = 32, max_splits = 1;
+    int max_splits = 1;
 
     int host_pos = 0;
     int prompt_len = 0;
@@ -114,7 +104,7 @@ void release(ar_qwen3* m) {
         hipEventDestroy(e.second);
     }
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->attn_ctr, m->am_val, m->am_idx, m->am_ctr, m->tokens, m->state, m->staging};
+                    m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     delete m;
@@ -163,7 +153,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         return AR_HIP_OK;
     };
 
-    AR_TRY(launch_embed(m->embed, c.weight_dtype, dim, m->tokens, m->S + 1, m->state, B, m->x, dim, st));
+    AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys, m->state,
+                             B, m->x, dim, st));
     const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
     for (int l = 0; l < c.layer_count; l++) {
         const Layer& L = m->layers[l];
@@ -183,8 +174,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         a.qk_eps = (float)c.epsilon; a.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
         a.kcache = m->kcache + l * layer_cache; a.vcache = m->vcache + l * layer_cache; a.max_seq = m->S;
         a.pos = m->state; a.heads = c.head_count; a.kv_heads = c.kv_head_count; a.head_dim = c.head_size;
-        a.rope_theta = c.rope_theta; a.tile = m->tile; a.max_splits = m->max_splits; a.part_o = m->part_o;
-        a.part_ml = m->part_ml; a.counters = m->attn_ctr; a.out = m->attn; a.out_stride = m->q_dim; a.batch = B;
+        a.rope_theta = c.rope_theta; a.rope_tab = m->rope_tab; a.max_splits = m->max_splits; a.part_o = m->part_o;
+        a.part_ml = m->part_ml; a.out = m->attn; a.out_stride = m->q_dim; a.batch = B;
         AR_TRY(timed_begin(AR_KT_ATTENTION));
         AR_TRY(launch_attention_decode(a, st));
         AR_TRY(timed_end(AR_KT_ATTENTION));
@@ -218,8 +209,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     GemvLaunch h;
     h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
     h.cols = dim; h.x = m->x; h.x_stride = dim; h.norm_w = m->final_norm; h.y = store_logits ? m->logits : nullptr;
-    h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.part_val = m->am_val; h.part_idx = m->am_idx;
-    h.counter = m->am_ctr; h.tokens = m->tokens; h.token_stride = m->S + 1; h.state = m->state; h.advance = 1;
+    h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.keys = m->am_keys;
     AR_TRY(timed_begin(AR_KT_LOGITS));
     AR_TRY(launch_gemv(h, st));
     AR_TRY(timed_end(AR_KT_LOGITS));
@@ -307,8 +297,7 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     m->wbytes = c.weight_dtype == AR_DTYPE_BF16 ? 2 : 4;
     m->layers.resize(c.layer_count);
     m->prompt_set.assign(m->B, 0);
-    m->tile = attention_tile(m->S);
-    m->max_splits = (m->S + m->tile - 1) / m->tile;
+    m->max_splits = attention_max_splits(m->S, c.kv_head_count, m->B);
 
     // ---- weight arena: every tensor 256-byte aligned --------------------------------
     const size_t d = c.dim, F = c.hidden_dim, V = c.vocab_size, wb = m->wbytes;
@@ -382,7 +371,6 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     // ---- activations, caches, loop state -------------------------------------------
     const size_t B = m->B;
     const size_t cache = (size_t)c.layer_count * B * c.kv_head_count * m->S * c.head_size;
-    const int am_parts = gemv_argmax_partials(c.vocab_size, m->B);
     m->staging_floats = 16u << 20;
 #define ALLOC(ptr, bytes)                                          \
     do {                                                           \
@@ -398,14 +386,30 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     ALLOC(vcache, cache * 4);
     ALLOC(part_o, attention_partial_floats(m->B, c.head_count, m->max_splits, c.head_size) * 4);
     ALLOC(part_ml, B * c.head_count * m->max_splits * 2 * 4);
-    ALLOC(attn_ctr, B * c.kv_head_count * 4);
-    ALLOC(am_val, (size_t)am_parts * 4);
-    ALLOC(am_idx, (size_t)am_parts * 4);
-    ALLOC(am_ctr, 64);
+    ALLOC(am_keys, B * kArgmaxSlots * 8);
+    ALLOC(rope_tab, (size_t)m->S * (c.head_size / 2) * sizeof(float2));
     ALLOC(tokens, B * (m->S + 1) * 4);
     ALLOC(state, 64);
     ALLOC(staging, m->staging_floats * 4);
 #undef ALLOC
+    {
+        // RoPE (cos, sin) for every cache position, in double as computeRopeFreqs defines them
+        // (engine/ml/.../RotationFeatures.java:189-208): invf[f] = exp(f * -2 ln(theta) / hd).
+        const int fd = c.head_size / 2;
+        std::vector<float2> tab((size_t)m->S * fd);
+        const double cexp = -2.0 * std::log(c.rope_theta) / (double)c.head_size;
+        for (int pos = 0; pos < m->S; pos++)
+            for (int f = 0; f < fd; f++) {
+                const double ang = (double)pos * std::exp((double)f * cexp);
+                tab[(size_t)pos * fd + f] = make_float2((float)std::cos(ang), (float)std::sin(ang));
+            }
+        if (hipMemcpyAsync(m->rope_tab, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice,
+                           ctx->stream) != hipSuccess) {
+            release(m);
+            ar_set_error("RoPE table upload failed");
+            return AR_HIP_ERR_HIP;
+        }
+    }
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
         release(m);
         ar_set_error("stream synchronize after allocation failed");
@@ -465,7 +469,7 @@ extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
 extern "C" int ar_hip_qwen3_reset(ar_qwen3* m) {
     AR_CHECK_ARG(m, "null model");
     m->host_pos = 0;
-    int st[2] = {0, m->prompt_len};
+    int st[3] = {0, m->prompt_len, 0};
     AR_HIP_TRY(hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, m->ctx->stream));
     AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     return AR_HIP_OK;
@@ -486,8 +490,7 @@ extern "C" int ar_hip_qwen3_set_prompt(ar_qwen3* m, int seq, const int32_t* ids,
                                   m->ctx->stream));
     m->prompt_len = n;
     m->prompt_set[seq] = 1;
-    int st[2] = {m->host_pos, m->prompt_len};
-    AR_HIP_TRY(hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, m->ctx->stream));
+    AR_HIP_TRY(hipMemcpyAsync(m->state + 1, &m->prompt_len, sizeof(int), hipMemcpyHostToDevice, m->ctx->stream));
     AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     return AR_HIP_OK;
 }
