@@ -70,6 +70,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=160, help="oracle steps timed for the CPU baseline (0: skip)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--prefetch", type=int, default=0,
+                    help="blocks of the Infinity-Cache weight prefetch branch (0 disables)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the path has no "
@@ -97,6 +99,7 @@ def main():
     log(f"[bench] weights generated + uploaded in {time.time() - t0:.1f}s on {info}")
     am = model.model
     am.use_graph(not args.no_graph)
+    am.use_prefetch(args.prefetch)
     am.reset()
     am.set_prompt(prompt)
 
@@ -192,7 +195,8 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
         "config": {"workload": "C3: Qwen3-0.6B shape fp32 (d1024, 28L, 16Q/8KV, hd128, F3072, V151936), "
                                "batch 1, prompt 128, greedy decode",
-                   "decode_positions": f"{pos0}..{pos0 + args.steps - 1}", "graph": not args.no_graph},
+                   "decode_positions": f"{pos0}..{pos0 + args.steps - 1}", "graph": not args.no_graph,
+                   "prefetch_blocks": args.prefetch},
         "hbm": {"algorithmic_bytes_per_token": round(mean_bytes), "achieved_GBs": round(e2e_gbs, 1),
                 "frac_of_peak": round(e2e_gbs / HBM_PEAK_GBS, 4)},
         "prefill": {"tok_s": round(n_prompt / prefill_s, 1), "tokens": n_prompt,

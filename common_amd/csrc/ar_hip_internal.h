@@ -86,7 +86,7 @@ struct GemvLaunch {
     unsigned long long* keys = nullptr;
 };
 
-constexpr int kArgmaxSlots = 64;
+constexpr int kArgmaxSlots = 1024;
 
 enum {
     GEMV_EPI_STORE = 0,     // y = W x (+ b)
@@ -140,5 +140,7 @@ int launch_rope(float* x, int heads, int hd, int pos, double theta, int rows, in
 int launch_index_of_max(const float* x, int rows, int n, int* out, hipStream_t stream);
 int launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream);
 int launch_fill_i32(int* dst, int value, size_t n, hipStream_t stream);
+// Reads [p, p+bytes) (16-byte aligned) with `blocks` x 256 threads so it lands in the Infinity Cache.
+int launch_prefetch(const void* p, size_t bytes, unsigned* sink, int blocks, hipStream_t stream);
 
 void ar_ops_release(ar_hip_ctx* ctx);

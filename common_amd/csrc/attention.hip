@@ -31,6 +31,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxTile = 256;
+constexpr int kMaxSplits = 1024;
 
 struct AttnParams {
     const float* qkv;
@@ -122,7 +123,46 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = tid >> 4, gl = tid & 15;
     const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
+    const int heads = p.heads, kvH = p.kv_heads;
+    const int q_dim = heads * HD, kv_dim = kvH * HD;
+    const float* q_raw = p.qkv + (size_t)b * p.qkv_stride;
+    const float* k_raw = q_raw + q_dim;
+    const float* v_raw = k_raw + kv_dim;
+    const bool whole_norm = (p.q_norm || p.k_norm) && !p.per_head_norm;
+
+    // ---- every load that does not depend on the position, issued together with it ----------
     const int pos = *p.pos;
+    constexpr int QPT = (G * FD + kThreads - 1) / kThreads;  // query (f, f+hd/2) pairs per thread
+    float qx1[QPT], qx2[QPT], qg1[QPT], qg2[QPT];
+#pragma unroll
+    for (int j = 0; j < QPT; j++) {
+        const int idx = min(tid + j * kThreads, G * FD - 1);
+        const int g = idx / FD, f = idx - g * FD;
+        const size_t off = (size_t)(kvh * G + g) * HD + f;
+        qx1[j] = q_raw[off];
+        qx2[j] = q_raw[off + FD];
+        qg1[j] = p.q_norm ? p.q_norm[off] : 1.f;
+        qg2[j] = p.q_norm ? p.q_norm[off + FD] : 1.f;
+    }
+    const int kf = min(tid, FD - 1);
+    const float kx1 = k_raw[(size_t)kvh * HD + kf], kx2 = k_raw[(size_t)kvh * HD + kf + FD];
+    const float kg1 = p.k_norm ? p.k_norm[(size_t)kvh * HD + kf] : 1.f;
+    const float kg2 = p.k_norm ? p.k_norm[(size_t)kvh * HD + kf + FD] : 1.f;
+    const float vnew = v_raw[(size_t)kvh * HD + min(tid, HD - 1)];
+    float sq = 0.f, sk = 0.f;  // this thread's share of sum(q^2), sum(k^2) over the whole vectors
+    if (whole_norm) {
+#pragma unroll 4
+        for (int i = tid * 4; i < q_dim; i += kThreads * 4) {
+            const float4 v = *reinterpret_cast<const float4*>(q_raw + i);
+            sq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+#pragma unroll 2
+        for (int i = tid * 4; i < kv_dim; i += kThreads * 4) {
+            const float4 v = *reinterpret_cast<const float4*>(k_raw + i);
+            sk += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    }
+
     if (pos < 0 || pos >= p.max_seq) return;
     const int n = pos + 1;
     int nsplit, tile;
@@ -130,8 +170,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     if (split >= nsplit) return;
     const int t0 = split * tile;
     const int t1 = min(t0 + tile, n);
-    const int heads = p.heads, kvH = p.kv_heads;
-    const int q_dim = heads * HD, kv_dim = kvH * HD;
     const size_t head_base = ((size_t)b * kvH + kvh) * (size_t)p.max_seq * HD;
     float* kc = p.kcache + head_base;
     float* vc = p.vcache + head_base;
@@ -166,17 +204,18 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     };
     load_k(t0);
     load_v(t0);
-
-    const float* q_raw = p.qkv + (size_t)b * p.qkv_stride;
-    const float* k_raw = q_raw + q_dim;
-    const float* v_raw = k_raw + kv_dim;
+    const float2* rope_row = p.rope_tab ? p.rope_tab + (size_t)pos * FD : nullptr;
+    float2 qcs[QPT], kcs;
+#pragma unroll
+    for (int j = 0; j < QPT; j++) {
+        const int idx = min(tid + j * kThreads, G * FD - 1);
+        rope_cs(rope_row, pos, idx % FD, p.rope_c, &qcs[j].x, &qcs[j].y);
+    }
+    rope_cs(rope_row, pos, kf, p.rope_c, &kcs.x, &kcs.y);
 
     // ---- QK-norm factors ----------------------------------------------------------
     if (p.q_norm || p.k_norm) {
-        if (!p.per_head_norm) {
-            float sq = 0.f, sk = 0.f;
-            for (int i = tid; i < q_dim; i += kThreads) sq += q_raw[i] * q_raw[i];
-            for (int i = tid; i < kv_dim; i += kThreads) sk += k_raw[i] * k_raw[i];
+        if (whole_norm) {
             sq = block_sum(sq, scratch);
             sk = block_sum(sk, scratch);
             if (tid == 0) {
@@ -201,41 +240,38 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     }
 
     // ---- normalised, rotated queries of this group -> LDS ---------------------------
-    const float2* rope_row = p.rope_tab ? p.rope_tab + (size_t)pos * FD : nullptr;
-    for (int idx = tid; idx < G * FD; idx += kThreads) {
-        const int g = idx / FD, f = idx - g * FD;
-        const int h = kvh * G + g;
-        float x1 = q_raw[(size_t)h * HD + f], x2 = q_raw[(size_t)h * HD + f + FD];
-        if (p.q_norm) {
-            x1 = (p.q_norm[(size_t)h * HD + f] * x1) * rq_s[g];
-            x2 = (p.q_norm[(size_t)h * HD + f + FD] * x2) * rq_s[g];
+#pragma unroll
+    for (int j = 0; j < QPT; j++) {
+        const int idx = tid + j * kThreads;
+        if (idx < G * FD) {
+            const int g = idx / FD, f = idx - g * FD;
+            float x1 = qx1[j], x2 = qx2[j];
+            if (p.q_norm) {
+                x1 = (qg1[j] * x1) * rq_s[g];
+                x2 = (qg2[j] * x2) * rq_s[g];
+            }
+            q_s[g][f] = x1 * qcs[j].x - x2 * qcs[j].y;
+            q_s[g][f + FD] = x2 * qcs[j].x + x1 * qcs[j].y;
         }
-        float c, s;
-        rope_cs(rope_row, pos, f, p.rope_c, &c, &s);
-        q_s[g][f] = x1 * c - x2 * s;
-        q_s[g][f + FD] = x2 * c + x1 * s;
     }
     // ---- the split holding `pos` writes this step's k and v rows (cache + LDS) ---------
     const bool has_pos = pos >= t0 && pos < t1;
     if (has_pos) {
-        for (int f = tid; f < FD; f += kThreads) {
-            float x1 = k_raw[(size_t)kvh * HD + f], x2 = k_raw[(size_t)kvh * HD + f + FD];
+        if (tid < FD) {
+            float x1 = kx1, x2 = kx2;
             if (p.k_norm) {
-                x1 = (p.k_norm[(size_t)kvh * HD + f] * x1) * rk_s;
-                x2 = (p.k_norm[(size_t)kvh * HD + f + FD] * x2) * rk_s;
+                x1 = (kg1 * x1) * rk_s;
+                x2 = (kg2 * x2) * rk_s;
             }
-            float c, s;
-            rope_cs(rope_row, pos, f, p.rope_c, &c, &s);
-            const float o1 = x1 * c - x2 * s, o2 = x2 * c + x1 * s;
-            k_new[f] = o1;
-            k_new[f + FD] = o2;
-            kc[(size_t)pos * HD + f] = o1;
-            kc[(size_t)pos * HD + f + FD] = o2;
+            const float o1 = x1 * kcs.x - x2 * kcs.y, o2 = x2 * kcs.x + x1 * kcs.y;
+            k_new[tid] = o1;
+            k_new[tid + FD] = o2;
+            kc[(size_t)pos * HD + tid] = o1;
+            kc[(size_t)pos * HD + tid + FD] = o2;
         }
-        for (int i = tid; i < HD; i += kThreads) {
-            const float v = v_raw[(size_t)kvh * HD + i];
-            v_new[i] = v;
-            vc[(size_t)pos * HD + i] = v;
+        if (tid < HD) {
+            v_new[tid] = vnew;
+            vc[(size_t)pos * HD + tid] = vnew;
         }
     }
     __syncthreads();
@@ -347,23 +383,55 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
 }
 
 // Merges the split partials of every query head: o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+// The (m, l) pairs are loaded in parallel into LDS, the weights e^(m_s - M) computed once per
+// split, then every thread sums its column over the splits eight loads at a time.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
+    __shared__ float w_s[kMaxSplits];
+    __shared__ float red[HD / 64];
     const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    const int lane = i & 63, wave = i >> 6;
     const int pos = *p.pos;
     if (pos < 0 || pos >= p.max_seq) return;
     int nsplit, tile;
     split_plan(pos + 1, p.max_splits, &nsplit, &tile);
     if (nsplit == 1) return;  // the attention kernel wrote the output itself
     const size_t slot0 = ((size_t)b * p.heads + h) * p.max_splits;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, p.part_ml[(slot0 + s) * 2]);
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        const float w = expf(p.part_ml[(slot0 + s) * 2] - M);
-        L = fmaf(p.part_ml[(slot0 + s) * 2 + 1], w, L);
-        O = fmaf(p.part_o[(slot0 + s) * HD + i], w, O);
+    float m_loc = -INFINITY;
+    for (int s = i; s < nsplit; s += HD) {
+        const float m = p.part_ml[(slot0 + s) * 2];
+        w_s[s] = m;
+        m_loc = fmaxf(m_loc, m);
     }
+    m_loc = wave_max(m_loc);
+    if (lane == 0) red[wave] = m_loc;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < HD / 64; w++) M = fmaxf(M, red[w]);
+    float l_loc = 0.f;
+    for (int s = i; s < nsplit; s += HD) {
+        const float w = expf(w_s[s] - M);
+        w_s[s] = w;
+        l_loc = fmaf(p.part_ml[(slot0 + s) * 2 + 1], w, l_loc);
+    }
+    l_loc = wave_sum(l_loc);
+    __syncthreads();
+    if (lane == 0) red[wave] = l_loc;
+    __syncthreads();
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < HD / 64; w++) L += red[w];
+    float O = 0.f;
+    int s = 0;
+    for (; s + 8 <= nsplit; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = p.part_o[(slot0 + s + u) * HD + i];
+#pragma unroll
+        for (int u = 0; u < 8; u++) O = fmaf(v[u], w_s[s + u], O);
+    }
+    for (; s < nsplit; s++) O = fmaf(p.part_o[(slot0 + s) * HD + i], w_s[s], O);
     p.out[(size_t)b * p.out_stride + (size_t)h * HD + i] = O / L;
 }
 
@@ -418,6 +486,7 @@ int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(a.qkv && a.kcache && a.vcache && a.pos && a.out, "attention: null pointer");
     AR_CHECK_ARG(a.heads > 0 && a.kv_heads > 0 && a.heads % a.kv_heads == 0, "attention: bad head counts %d/%d",
                  a.heads, a.kv_heads);
+    AR_CHECK_ARG(a.max_splits <= kMaxSplits, "attention: %d splits exceed %d", a.max_splits, kMaxSplits);
     AR_CHECK_ARG(a.max_splits >= 1 && (long long)a.max_splits * kMaxTile >= a.max_seq,
                  "attention: %d splits of at most %d rows do not cover %d rows", a.max_splits, kMaxTile, a.max_seq);
     AR_CHECK_ARG(a.max_splits == 1 || (a.part_o && a.part_ml), "attention: missing split buffers");

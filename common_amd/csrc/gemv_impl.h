@@ -137,7 +137,60 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
     float rn[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) rn[b] = 1.0f;
-    if (p.norm_w) {
+    // Short inputs (batch <= 2, cols <= 4096, one slice): x and the gain are read once into
+    // registers, reduced, and written normalised to LDS -- one global round trip instead of two.
+    constexpr int XV = 4;
+    const bool fast = NB <= 2 && cols <= kThreads * 4 * XV && cols <= SLICE;
+    if (fast) {
+        float4 xr[NB <= 2 ? NB : 1][XV], gr[XV];
+#pragma unroll
+        for (int j = 0; j < XV; j++) {
+            const int i = (tid + j * kThreads) * 4;
+            const bool in = i < cols;
+            gr[j] = (in && p.norm_w) ? *reinterpret_cast<const float4*>(p.norm_w + i) : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+            for (int b = 0; b < (NB <= 2 ? NB : 1); b++)
+                xr[b][j] = (in && b < p.batch) ? *reinterpret_cast<const float4*>(p.x + (size_t)b * p.x_stride + i)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (p.norm_w) {
+#pragma unroll
+            for (int b = 0; b < (NB <= 2 ? NB : 1); b++) {
+                float ss = 0.f;
+#pragma unroll
+                for (int j = 0; j < XV; j++)
+                    ss += xr[b][j].x * xr[b][j].x + xr[b][j].y * xr[b][j].y + xr[b][j].z * xr[b][j].z +
+                          xr[b][j].w * xr[b][j].w;
+                ss = wave_sum(ss);
+                if (lane == 0) red[wave][b] = ss;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int b = 0; b < (NB <= 2 ? NB : 1); b++) {
+                float ss = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) ss += red[w][b];
+                rn[b] = 1.0f / sqrtf(ss / (float)cols + p.eps);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < XV; j++) {
+            const int i = (tid + j * kThreads) * 4;
+            if (i < cols) {
+#pragma unroll
+                for (int b = 0; b < (NB <= 2 ? NB : 1); b++) {
+                    float4 h = xr[b][j];
+                    if (p.norm_w) {
+                        h.x = (gr[j].x * h.x) * rn[b];
+                        h.y = (gr[j].y * h.y) * rn[b];
+                        h.z = (gr[j].z * h.z) * rn[b];
+                        h.w = (gr[j].w * h.w) * rn[b];
+                    }
+                    *reinterpret_cast<float4*>(&hs[b * SLICE + i]) = h;
+                }
+            }
+        }
+    } else if (p.norm_w) {
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             float ss = 0.f;
@@ -170,8 +223,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Params p) {
     for (int s0 = 0; s0 < cols; s0 += SLICE) {
         const int sl = min(SLICE, cols - s0);
         __syncthreads();
-        // stage x (normalised if asked) for this slice
-        for (int i = tid * 4; i < sl; i += kThreads * 4) {
+        // stage x (normalised if asked) for this slice (already staged on the short-input path)
+        for (int i = tid * 4; !fast && i < sl; i += kThreads * 4) {
             float4 gw = make_float4(1.f, 1.f, 1.f, 1.f);
             if (p.norm_w) gw = *reinterpret_cast<const float4*>(p.norm_w + s0 + i);
 #pragma unroll

@@ -18,11 +18,11 @@ __device__ inline bool better(float v1, int i1, float v2, int i2) {
 // clears the keys, copies the embedding row and publishes p as the step's position.
 // AutoregressiveModel.next + embedding copy (engine/ml/.../AutoregressiveModel.java:295-308,430).
 template <typename WT>
-__global__ __launch_bounds__(256) void step_begin_kernel(const WT* table, int dim, int vocab, int* tokens,
+__global__ __launch_bounds__(1024) void step_begin_kernel(const WT* table, int dim, int vocab, int* tokens,
                                                          int token_stride, unsigned long long* keys, int* state,
                                                          int batch, float* x, int x_stride) {
     __shared__ int tok_s[8];
-    __shared__ unsigned long long red[4];
+    __shared__ unsigned long long red[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int p = state[2];
     const int plen = state[1];
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void step_begin_kernel(const WT* table, int di
             __syncthreads();
             if (tid == 0) {
                 unsigned long long m = red[0];
-                for (int w = 1; w < 4; w++) m = red[w] > m ? red[w] : m;
+                for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = red[w] > m ? red[w] : m;
                 int t = m ? (int)(0xFFFFFFFFu - (unsigned)(m & 0xFFFFFFFFull)) : 0;
                 if (t < 0 || t >= vocab) t = 0;
                 tokens[(size_t)b * token_stride + p] = t;
@@ -139,6 +139,28 @@ __global__ void fill_i32_kernel(int* dst, int value, size_t n) {
         dst[i] = value;
 }
 
+// Streams [p, p + n16*16) through the memory hierarchy so a later kernel finds it in the
+// Infinity Cache.  The loaded words are folded into an XOR that is stored only when it equals a
+// value no weight tensor produces in practice, which keeps the loads from being removed.
+__global__ __launch_bounds__(256) void prefetch_kernel(const uint4* __restrict__ p, size_t n16, unsigned sentinel,
+                                                       unsigned* sink) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    unsigned acc = 0;
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = p[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == sentinel) sink[0] = acc;
+}
+
 int grid_for(size_t n, int threads, int cap = 4096) {
     size_t g = (n + threads - 1) / threads;
     if (g < 1) g = 1;
@@ -153,10 +175,10 @@ int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* to
     AR_CHECK_ARG(table && tokens && keys && state && x && dim > 0, "step begin: bad arguments");
     AR_CHECK_ARG(batch >= 1 && batch <= 8, "step begin: batch %d outside 1..8", batch);
     if (wdtype == AR_DTYPE_BF16)
-        hipLaunchKernelGGL(step_begin_kernel<uint16_t>, dim3(1), dim3(256), 0, stream, (const uint16_t*)table, dim,
+        hipLaunchKernelGGL(step_begin_kernel<uint16_t>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)table, dim,
                            vocab, tokens, token_stride, keys, state, batch, x, x_stride);
     else
-        hipLaunchKernelGGL(step_begin_kernel<float>, dim3(1), dim3(256), 0, stream, (const float*)table, dim, vocab,
+        hipLaunchKernelGGL(step_begin_kernel<float>, dim3(1), dim3(1024), 0, stream, (const float*)table, dim, vocab,
                            tokens, token_stride, keys, state, batch, x, x_stride);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
@@ -188,6 +210,15 @@ int launch_index_of_max(const float* x, int rows, int n, int* out, hipStream_t s
 int launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream) {
     if (!n) return AR_HIP_OK;
     hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, src, dst, n);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
+int launch_prefetch(const void* p, size_t bytes, unsigned* sink, int blocks, hipStream_t stream) {
+    AR_CHECK_ARG(p && sink && (reinterpret_cast<uintptr_t>(p) & 15) == 0, "prefetch: bad arguments");
+    if (bytes < 16) return AR_HIP_OK;
+    hipLaunchKernelGGL(prefetch_kernel, dim3(blocks), dim3(256), 0, stream, (const uint4*)p, bytes / 16,
+                       0x9E3779B9u, sink);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -82,6 +82,16 @@ struct ar_qwen3 {
     bool use_graph = true;
     hipGraphExec_t graph[2] = {nullptr, nullptr};  // [store logits]
 
+    // Infinity-Cache prefetch branch: a second stream streams layer l+1's weights while layer l
+    // computes (forked from the compute stream by an event at the start of each layer, joined at
+    // the end of the step).  0 blocks disables it.
+    int prefetch_blocks = 0;
+    hipStream_t pstream = nullptr;
+    std::vector<hipEvent_t> fork_ev;   // one per layer + 1
+    hipEvent_t join_ev = nullptr;
+    unsigned* sink = nullptr;
+    std::vector<std::pair<size_t, size_t>> layer_bytes;  // [offset, end) of each layer in the arena
+
     int timed = AR_KT_NONE;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
     size_t events_used = 0;
@@ -103,8 +113,11 @@ void release(ar_qwen3* m) {
         hipEventDestroy(e.first);
         hipEventDestroy(e.second);
     }
+    for (auto& e : m->fork_ev) hipEventDestroy(e);
+    if (m->join_ev) hipEventDestroy(m->join_ev);
+    if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging};
+                    m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     delete m;
@@ -153,11 +166,20 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         return AR_HIP_OK;
     };
 
+    const bool pf = m->prefetch_blocks > 0;
+    auto prefetch_layer = [&](int l, int ev) -> int {
+        AR_HIP_TRY(hipEventRecord(m->fork_ev[ev], st));
+        AR_HIP_TRY(hipStreamWaitEvent(m->pstream, m->fork_ev[ev], 0));
+        const auto& r = m->layer_bytes[l];
+        return launch_prefetch(m->arena + r.first, r.second - r.first, m->sink, m->prefetch_blocks, m->pstream);
+    };
+    if (pf) AR_TRY(prefetch_layer(0, 0));
     AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys, m->state,
                              B, m->x, dim, st));
     const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
     for (int l = 0; l < c.layer_count; l++) {
         const Layer& L = m->layers[l];
+        if (pf && l + 1 < c.layer_count) AR_TRY(prefetch_layer(l + 1, l + 1));
         GemvLaunch g;
         g.wdtype = c.weight_dtype;
         g.batch = B;
@@ -213,6 +235,10 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     AR_TRY(timed_begin(AR_KT_LOGITS));
     AR_TRY(launch_gemv(h, st));
     AR_TRY(timed_end(AR_KT_LOGITS));
+    if (pf) {  // join the prefetch branch back into the compute stream
+        AR_HIP_TRY(hipEventRecord(m->join_ev, m->pstream));
+        AR_HIP_TRY(hipStreamWaitEvent(st, m->join_ev, 0));
+    }
     return AR_HIP_OK;
 }
 
@@ -326,6 +352,7 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
         o[7] = place(p + "self_attn.q_norm.weight", m->q_dim, false, false);
         o[8] = place(p + "self_attn.k_norm.weight", m->kv_dim, false, false);
         o[9] = c.qkv_bias ? place(p + "self_attn.qkv_bias", m->qkv_dim, false) : (size_t)-1;
+        m->layer_bytes.push_back({o[0], off});
     }
     m->arena_bytes = off;
     int rc = ar_ctx_alloc(ctx, m->arena_bytes, (void**)&m->arena);
@@ -391,7 +418,22 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     ALLOC(tokens, B * (m->S + 1) * 4);
     ALLOC(state, 64);
     ALLOC(staging, m->staging_floats * 4);
+    ALLOC(sink, 64);
 #undef ALLOC
+    {
+        hipError_t e = hipStreamCreateWithFlags(&m->pstream, hipStreamNonBlocking);
+        for (int i = 0; e == hipSuccess && i <= c.layer_count; i++) {
+            hipEvent_t ev;
+            e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+            if (e == hipSuccess) m->fork_ev.push_back(ev);
+        }
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&m->join_ev, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            release(m);
+            ar_set_error("prefetch stream/event creation failed: %s", hipGetErrorString(e));
+            return AR_HIP_ERR_HIP;
+        }
+    }
     {
         // RoPE (cos, sin) for every cache position, in double as computeRopeFreqs defines them
         // (engine/ml/.../RotationFeatures.java:189-208): invf[f] = exp(f * -2 ln(theta) / hd).
@@ -587,5 +629,14 @@ extern "C" int ar_hip_qwen3_kernel_time(ar_qwen3* m, double* ms, int* launches) 
 extern "C" int ar_hip_qwen3_use_graph(ar_qwen3* m, int enable) {
     AR_CHECK_ARG(m, "null model");
     m->use_graph = enable != 0;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_use_prefetch(ar_qwen3* m, int blocks) {
+    AR_CHECK_ARG(m, "null model");
+    AR_CHECK_ARG(blocks >= 0 && blocks <= 4096, "prefetch blocks %d outside 0..4096", blocks);
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    AR_TRY(invalidate_graphs(m));
+    m->prefetch_blocks = blocks;
     return AR_HIP_OK;
 }

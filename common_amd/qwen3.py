@@ -77,6 +77,10 @@ class AutoregressiveModel:
     def use_graph(self, enable: bool):
         hw.check(hw.lib().ar_hip_qwen3_use_graph(self.handle, int(enable)))
 
+    def use_prefetch(self, blocks: int):
+        """Infinity-Cache prefetch of the next layer's weights on a second stream (0 disables)."""
+        hw.check(hw.lib().ar_hip_qwen3_use_prefetch(self.handle, int(blocks)))
+
     def kernel_timing(self, which: int):
         hw.check(hw.lib().ar_hip_qwen3_kernel_timing(self.handle, which))
 

@@ -179,6 +179,11 @@ int ar_hip_qwen3_kernel_timing(ar_qwen3 *m, int which);
 int ar_hip_qwen3_kernel_time(ar_qwen3 *m, double *ms, int *launches);
 /* Use a captured HIP graph per decode step (1, default) or plain launches (0). */
 int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
+/* Infinity-Cache prefetch: a second stream reads layer l+1's weights while layer l computes, with
+ * `blocks` x 256 threads (default 0 = off: on MI355X the extra
+ * cross-stream dependencies cost more than the cache hits save).  No counterpart in the reference (its CPU
+ * backend has no memory hierarchy to manage); a throughput knob only, results are unchanged. */
+int ar_hip_qwen3_use_prefetch(ar_qwen3 *m, int blocks);
 
 #ifdef __cplusplus
 }
