@@ -97,6 +97,50 @@ enum {
 
 int launch_gemv(const GemvLaunch& a, hipStream_t stream);
 
+// Prefill GEMM on MFMA: C[M x N] = A[M x K] . W[N x K]^T, 16-bit operands (bf16, or fp16 when
+// f16 is set), fp32 accumulation.
+// epilogue GEMV_EPI_STORE (C = acc + bias), GEMV_EPI_RESIDUAL (C += acc) with fp32 C, or
+// GEMV_EPI_SWIGLU (O = 16-bit((W2-product) * silu(W-product))).  N % 128 == 0, K % 64 == 0.
+struct GemmLaunch {
+    const uint16_t* A = nullptr;
+    const uint16_t* W = nullptr;
+    const uint16_t* W2 = nullptr;
+    int M = 0, N = 0, K = 0, lda = 0, ldw = 0;
+    const float* bias = nullptr;
+    float* C = nullptr;
+    int ldc = 0;
+    uint16_t* O = nullptr;
+    int ldo = 0;
+    int epilogue = GEMV_EPI_STORE;
+    bool f16 = false;
+};
+int launch_gemm(const GemmLaunch& a, hipStream_t stream);
+
+// ---- prefill (prefill.hip) ---------------------------------------------------------
+// x[r] = E[tokens[b][t]] for r = b*T + t.
+int launch_embed_rows(const void* table, int wdtype, int dim, const int* tokens, int token_stride, int T, int rows,
+                      float* x, hipStream_t stream);
+int launch_rmsnorm_rows_f16(const float* x, const float* w, uint16_t* out, int rows, int n, float eps,
+                            hipStream_t stream);
+// fp16 copy of bf16 data (exact for |v| >= 2^-17 inside the fp16 range), for the prefill GEMMs.
+int launch_bf16_to_f16(const uint16_t* src, uint16_t* dst, size_t n, hipStream_t stream);
+struct PrefillPrep {
+    const float* qkv = nullptr;
+    int qkv_stride = 0;
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+    float eps = 1e-6f;
+    int per_head = 0;
+    const float2* rope_tab = nullptr;
+    float* kcache = nullptr;
+    float* vcache = nullptr;
+    int B = 1, S = 0, T = 0, p0 = 0, heads = 0, kv_heads = 0, hd = 0;
+    uint16_t* qb = nullptr;
+};
+int launch_qk_prep(const PrefillPrep& a, hipStream_t stream);
+int launch_flash_prefill(const uint16_t* qb, const float* kcache, const float* vcache, uint16_t* out, int B, int S,
+                         int T, int p0, int heads, int kv_heads, int hd, hipStream_t stream);
+
 struct AttnLaunch {
     const float* qkv = nullptr;   // [batch][qkv_stride]: q | k | v raw projections
     int qkv_stride = 0;

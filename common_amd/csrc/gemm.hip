@@ -1,0 +1,226 @@
+// Multi-token (prefill) contractions on the MFMA units: C[M x N] = A[M x K] . W[N x K]^T with
+// 16-bit operands (bf16, or fp16 for the prefill path's higher-precision activations) and fp32
+// accumulation.
+//
+// The reference has no multi-token path: AutoregressiveModel feeds prompt tokens one per step
+// through the decode graph (engine/ml/.../AutoregressiveModel.java:295-308), i.e. every projection
+// is a GEMV per token.  Stacking the T prompt rows turns each projection (LayerFeatures.dense,
+// domain/graph/.../LayerFeatures.java:785-830) into one GEMM; rows are independent, so the result
+// per row is the same contraction the GEMV computes.
+//
+// Both operands are K-contiguous (activations [M][K] row-major, HF weights [N][K] row-major), which
+// is exactly the operand layout of v_mfma_f32_32x32x16_bf16: lane l supplies row (l % 32) and the
+// 8 consecutive k values (l / 32) * 8 .. +7 of a 16-wide k slice; the 32x32 fp32 result lands in
+// 16 registers per lane, register r holding row (r/4)*8 + (l/32)*4 + r%4, column l % 32.
+//
+// Tiling: 128 x 128 block tile, BK = 64, 256 threads as 2 x 2 wavefronts of 64 x 64 (2 x 2 MFMA
+// tiles each).  Global tiles are loaded 16 bytes per lane into registers one k-step ahead and
+// stored into the other half of a double-buffered, row-padded LDS tile (row stride 72 bf16 =
+// 144 B, so the 16-byte fragment reads of consecutive rows fall in different bank groups).
+// Epilogues: fp32 store (+bias), fp32 residual add, and SwiGLU of two weight matrices written as
+// bf16 (the next GEMM's A operand).
+#include "ar_hip_internal.h"
+
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 halfx8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+
+// MFMA operand element: bf16 (v_mfma_f32_32x32x16_bf16) or fp16 (v_mfma_f32_32x32x16_f16); both
+// take 8 consecutive k values per lane in the same lane layout and accumulate in fp32.
+template <bool F16>
+struct Mfma;
+template <>
+struct Mfma<false> {
+    using frag = bf16x8;
+    __device__ static inline floatx16 mac(frag a, frag b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static inline uint16_t from_float(float f) {
+        unsigned u = __float_as_uint(f);
+        if ((u & 0x7F800000u) == 0x7F800000u) return (uint16_t)((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
+        u += 0x7FFFu + ((u >> 16) & 1u);
+        return (uint16_t)(u >> 16);
+    }
+};
+template <>
+struct Mfma<true> {
+    using frag = halfx8;
+    __device__ static inline floatx16 mac(frag a, frag b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    __device__ static inline uint16_t from_float(float f) {
+        const _Float16 h = (_Float16)f;
+        return *reinterpret_cast<const uint16_t*>(&h);
+    }
+};
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row
+constexpr int kThreads = 256;
+
+struct GemmParams {
+    const uint16_t* A;  // [M][lda] bf16
+    const uint16_t* W;  // [N][ldw] bf16
+    const uint16_t* W2; // second weight (SwiGLU up projection) or null
+    int M, N, K, lda, ldw;
+    const float* bias;  // [N] or null (STORE)
+    float* C;           // fp32 [M][ldc] (STORE, RESIDUAL)
+    int ldc;
+    uint16_t* O;        // bf16 [M][ldo] (SWIGLU)
+    int ldo;
+};
+
+template <int NW>  // 1 weight matrix, or 2 for SwiGLU
+struct Tiles {
+    uint16_t a[2][BM * LDS_STRIDE];
+    uint16_t w[NW][2][BN * LDS_STRIDE];
+};
+
+template <bool F16, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
+    using M = Mfma<F16>;
+    using frag = typename M::frag;
+    constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) Tiles<NW> t;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    // global -> register staging: 4 x 16 B of A and of each W per thread per k-step
+    // element (row = tid/8 + 32*i, k chunk = (tid%8)*8)
+    const int lrow = tid >> 3, lk = (tid & 7) * 8;
+    uint4 ra[4], rw[NW][4];
+#define AR_GEMM_LOAD_GLOBAL(k0)                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                      \
+        const int r = lrow + 32 * i;                                                                     \
+        const int am = min(m0 + r, p.M - 1);                                                             \
+        ra[i] = *reinterpret_cast<const uint4*>(p.A + (size_t)am * p.lda + (k0) + lk);                   \
+        rw[0][i] = *reinterpret_cast<const uint4*>(p.W + (size_t)(n0 + r) * p.ldw + (k0) + lk);          \
+        if constexpr (NW == 2)                                                                           \
+            rw[NW - 1][i] = *reinterpret_cast<const uint4*>(p.W2 + (size_t)(n0 + r) * p.ldw + (k0) + lk);\
+    }
+#define AR_GEMM_STORE_LDS(buf)                                                                           \
+    _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                      \
+        const int r = lrow + 32 * i;                                                                     \
+        *reinterpret_cast<uint4*>(&t.a[buf][r * LDS_STRIDE + lk]) = ra[i];                               \
+        _Pragma("unroll") for (int w = 0; w < NW; w++)                                                   \
+            *reinterpret_cast<uint4*>(&t.w[w][buf][r * LDS_STRIDE + lk]) = rw[w][i];                     \
+    }
+
+    floatx16 acc[NW][2][2];
+#pragma unroll
+    for (int w = 0; w < NW; w++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[w][i][j][r] = 0.f;
+
+    const int nk = p.K / BK;
+    AR_GEMM_LOAD_GLOBAL(0)
+    AR_GEMM_STORE_LDS(0)
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        // next tile in flight during the MFMAs (the last step reloads its own tile: a cache hit
+        // into the idle buffer, kept unconditional so the staging stays in registers)
+        const int knext = (kt + 1 < nk ? kt + 1 : kt) * BK;
+        AR_GEMM_LOAD_GLOBAL(knext)
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; kk++) {
+            const int kofs = kk * 16 + (lane >> 5) * 8;
+            frag af[2], bfr[NW][2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int r = wm * 64 + i * 32 + (lane & 31);
+                af[i] = *reinterpret_cast<const frag*>(&t.a[buf][r * LDS_STRIDE + kofs]);
+            }
+#pragma unroll
+            for (int w = 0; w < NW; w++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int r = wn * 64 + j * 32 + (lane & 31);
+                    bfr[w][j] = *reinterpret_cast<const frag*>(&t.w[w][buf][r * LDS_STRIDE + kofs]);
+                }
+#pragma unroll
+            for (int w = 0; w < NW; w++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[w][i][j] = M::mac(af[i], bfr[w][j], acc[w][i][j]);
+        }
+        AR_GEMM_STORE_LDS(buf ^ 1)
+        __syncthreads();
+    }
+#undef AR_GEMM_LOAD_GLOBAL
+#undef AR_GEMM_STORE_LDS
+
+    // ---- epilogue ----------------------------------------------------------------------
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (row >= p.M) continue;
+                const float v = acc[0][i][j][r];
+                if (EPI == GEMV_EPI_STORE) {
+                    p.C[(size_t)row * p.ldc + col] = p.bias ? v + p.bias[col] : v;
+                } else if (EPI == GEMV_EPI_RESIDUAL) {
+                    float* c = p.C + (size_t)row * p.ldc + col;
+                    *c = *c + v;
+                } else {
+                    const float g = v, u = acc[NW - 1][i][j][r];
+                    const float sg = 1.0f / (expf(-g) + 1.0f);
+                    p.O[(size_t)row * p.ldo + col] = M::from_float(u * (g * sg));
+                }
+            }
+        }
+}
+
+template <int EPI>
+int launch_t(const GemmParams& p, bool f16, hipStream_t st) {
+    dim3 grid(p.N / BN, (p.M + BM - 1) / BM);
+    if (f16)
+        hipLaunchKernelGGL((gemm_kernel<true, EPI>), grid, dim3(kThreads), 0, st, p);
+    else
+        hipLaunchKernelGGL((gemm_kernel<false, EPI>), grid, dim3(kThreads), 0, st, p);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
+}  // namespace
+
+int launch_gemm(const GemmLaunch& a, hipStream_t stream) {
+    AR_CHECK_ARG(a.A && a.W, "GEMM: null operand");
+    AR_CHECK_ARG(a.M > 0 && a.N > 0 && a.K > 0, "GEMM: empty shape");
+    AR_CHECK_ARG(a.N % BN == 0, "GEMM: N=%d must be a multiple of %d", a.N, BN);
+    AR_CHECK_ARG(a.K % BK == 0, "GEMM: K=%d must be a multiple of %d", a.K, BK);
+    AR_CHECK_ARG(a.lda >= a.K && a.ldw >= a.K && a.lda % 8 == 0 && a.ldw % 8 == 0, "GEMM: bad leading dims");
+    AR_CHECK_ARG((reinterpret_cast<uintptr_t>(a.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.W) & 15) == 0,
+                 "GEMM: operands must be 16-byte aligned");
+    GemmParams p;
+    p.A = a.A; p.W = a.W; p.W2 = a.W2; p.M = a.M; p.N = a.N; p.K = a.K; p.lda = a.lda; p.ldw = a.ldw;
+    p.bias = a.bias; p.C = a.C; p.ldc = a.ldc; p.O = a.O; p.ldo = a.ldo;
+    switch (a.epilogue) {
+        case GEMV_EPI_STORE:
+            AR_CHECK_ARG(a.C && a.ldc >= a.N, "GEMM: bad fp32 output");
+            return launch_t<GEMV_EPI_STORE>(p, a.f16, stream);
+        case GEMV_EPI_RESIDUAL:
+            AR_CHECK_ARG(a.C && a.ldc >= a.N, "GEMM: bad fp32 output");
+            return launch_t<GEMV_EPI_RESIDUAL>(p, a.f16, stream);
+        case GEMV_EPI_SWIGLU:
+            AR_CHECK_ARG(a.W2 && (reinterpret_cast<uintptr_t>(a.W2) & 15) == 0, "GEMM: SwiGLU needs an aligned W2");
+            AR_CHECK_ARG(a.O && a.ldo >= a.N, "GEMM: bad bf16 output");
+            return launch_t<GEMV_EPI_SWIGLU>(p, a.f16, stream);
+    }
+    ar_set_error("GEMM: unsupported epilogue %d", a.epilogue);
+    return AR_HIP_ERR_INVALID;
+}

@@ -134,6 +134,13 @@ __global__ void f32_to_bf16_kernel(const float* src, uint16_t* dst, size_t n) {
     }
 }
 
+__global__ void bf16_to_f16_kernel(const uint16_t* src, uint16_t* dst, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const _Float16 h = (_Float16)__uint_as_float((unsigned)src[i] << 16);
+        dst[i] = *reinterpret_cast<const uint16_t*>(&h);
+    }
+}
+
 __global__ void fill_i32_kernel(int* dst, int value, size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         dst[i] = value;
@@ -219,6 +226,13 @@ int launch_prefetch(const void* p, size_t bytes, unsigned* sink, int blocks, hip
     if (bytes < 16) return AR_HIP_OK;
     hipLaunchKernelGGL(prefetch_kernel, dim3(blocks), dim3(256), 0, stream, (const uint4*)p, bytes / 16,
                        0x9E3779B9u, sink);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
+int launch_bf16_to_f16(const uint16_t* src, uint16_t* dst, size_t n, hipStream_t stream) {
+    if (!n) return AR_HIP_OK;
+    hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, src, dst, n);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

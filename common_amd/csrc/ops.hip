@@ -97,3 +97,18 @@ void ar_ops_release(ar_hip_ctx* ctx) {
     std::lock_guard<std::mutex> lk(g_attn_mu);
     g_attn.erase(ctx);  // the allocations themselves are freed with the context
 }
+
+extern "C" int ar_hip_gemm_bf16(ar_hip_ctx* ctx, const uint16_t* A, const uint16_t* W, const uint16_t* W2,
+                                const float* bias, float* C, uint16_t* O, int M, int N, int K, int epilogue) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    GemmLaunch g;
+    g.A = A; g.W = W; g.W2 = W2; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldw = K; g.bias = bias; g.C = C; g.ldc = N;
+    g.O = O; g.ldo = N;
+    switch (epilogue) {
+        case AR_GEMM_STORE: g.epilogue = GEMV_EPI_STORE; break;
+        case AR_GEMM_RESIDUAL: g.epilogue = GEMV_EPI_RESIDUAL; break;
+        case AR_GEMM_SWIGLU: g.epilogue = GEMV_EPI_SWIGLU; break;
+        default: AR_CHECK_ARG(false, "GEMM: unknown epilogue %d", epilogue);
+    }
+    return launch_gemm(g, ctx->stream);
+}

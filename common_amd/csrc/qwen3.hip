@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstring>
 #include <string>
+#include <algorithm>
 #include <vector>
 
 #include "ar_hip_internal.h"
@@ -92,6 +93,17 @@ struct ar_qwen3 {
     unsigned* sink = nullptr;
     std::vector<std::pair<size_t, size_t>> layer_bytes;  // [offset, end) of each layer in the arena
 
+    // prefill buffers, sized for pf_rows = batch x prompt rows on first use
+    size_t pf_rows = 0;
+    float* pf_x = nullptr;       // [R][dim] residual stream
+    uint16_t* pf_h = nullptr;    // [R][max(dim, q_dim)] fp16 GEMM input (normalised x / attention out)
+    float* pf_qkv = nullptr;     // [R][qkv_dim]
+    uint16_t* pf_q = nullptr;    // [R][q_dim] fp16 normalised, rotated queries
+    uint16_t* pf_act = nullptr;  // [R][F] fp16 SwiGLU output
+    // fp16 copies of the projection matrices for the prefill GEMMs (made on the first prefill)
+    uint16_t* pf_w16 = nullptr;
+    bool pf_w16_valid = false;
+
     int timed = AR_KT_NONE;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
     size_t events_used = 0;
@@ -117,7 +129,8 @@ void release(ar_qwen3* m) {
     if (m->join_ev) hipEventDestroy(m->join_ev);
     if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink};
+                    m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
+                    m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_w16};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     delete m;
@@ -482,6 +495,7 @@ extern "C" int ar_hip_qwen3_set_weight(ar_qwen3* m, const char* key, const void*
     AR_TRY(upload(m, s, src, src_dtype, n));
     s.filled = true;
     m->finalized = false;
+    m->pf_w16_valid = false;
     return AR_HIP_OK;
 }
 
@@ -638,5 +652,128 @@ extern "C" int ar_hip_qwen3_use_prefetch(ar_qwen3* m, int blocks) {
     AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     AR_TRY(invalidate_graphs(m));
     m->prefetch_blocks = blocks;
+    return AR_HIP_OK;
+}
+
+namespace {
+
+int ensure_prefill_buffers(ar_qwen3* m, size_t rows) {
+    if (m->pf_rows >= rows) return AR_HIP_OK;
+    void** bufs[] = {(void**)&m->pf_x, (void**)&m->pf_h, (void**)&m->pf_qkv, (void**)&m->pf_q, (void**)&m->pf_act};
+    for (void** b : bufs)
+        if (*b) {
+            AR_TRY(ar_ctx_free(m->ctx, *b));
+            *b = nullptr;
+        }
+    m->pf_rows = 0;
+    const ar_qwen3_cfg& c = m->cfg;
+    const size_t hw = (size_t)std::max(c.dim, m->q_dim);
+    AR_TRY(ar_ctx_alloc(m->ctx, rows * c.dim * 4, (void**)&m->pf_x));
+    AR_TRY(ar_ctx_alloc(m->ctx, rows * hw * 2, (void**)&m->pf_h));
+    AR_TRY(ar_ctx_alloc(m->ctx, rows * m->qkv_dim * 4, (void**)&m->pf_qkv));
+    AR_TRY(ar_ctx_alloc(m->ctx, rows * m->q_dim * 2, (void**)&m->pf_q));
+    AR_TRY(ar_ctx_alloc(m->ctx, rows * c.hidden_dim * 2, (void**)&m->pf_act));
+    m->pf_rows = rows;
+    return AR_HIP_OK;
+}
+
+// fp16 copy of a layer's projection matrices, in the same order as the arena: qkv, o, gate, up, down.
+int ensure_f16_weights(ar_qwen3* m) {
+    if (m->pf_w16_valid) return AR_HIP_OK;
+    const ar_qwen3_cfg& c = m->cfg;
+    const size_t d = c.dim, F = c.hidden_dim;
+    const size_t per_layer = (size_t)m->qkv_dim * d + d * m->q_dim + 3 * F * d;
+    if (!m->pf_w16) AR_TRY(ar_ctx_alloc(m->ctx, per_layer * c.layer_count * 2, (void**)&m->pf_w16));
+    uint16_t* dst = m->pf_w16;
+    for (int l = 0; l < c.layer_count; l++) {
+        const Layer& L = m->layers[l];
+        const void* srcs[5] = {L.wqkv, L.wo, L.w1, L.w3, L.w2};
+        const size_t counts[5] = {(size_t)m->qkv_dim * d, d * m->q_dim, F * d, F * d, d * F};
+        for (int i = 0; i < 5; i++) {
+            AR_TRY(launch_bf16_to_f16((const uint16_t*)srcs[i], dst, counts[i], m->ctx->stream));
+            dst += counts[i];
+        }
+    }
+    m->pf_w16_valid = true;
+    return AR_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
+    AR_CHECK_ARG(m, "null model");
+    const int T = m->prompt_len;
+    AR_TRY(check_ready(m, T));
+    AR_CHECK_ARG(m->host_pos == 0, "prefill starts a sequence: reset() first (position is %d)", m->host_pos);
+    const ar_qwen3_cfg& c = m->cfg;
+    if (c.weight_dtype != AR_DTYPE_BF16) {
+        // fp32 weights: the MFMA path needs bf16 operands, so the prompt goes through the decode
+        // step token by token (the reference's own prefill)
+        if (T > 1) AR_TRY(ar_hip_qwen3_run(m, T - 1, nullptr));
+        return ar_hip_qwen3_next(m, nullptr, logits_out);
+    }
+    hipStream_t st = m->ctx->stream;
+    const int B = m->B, d = c.dim, F = c.hidden_dim, qd = m->q_dim;
+    const size_t R = (size_t)B * T;
+    AR_CHECK_ARG(R <= (size_t)INT32_MAX / 16, "prefill: %zu rows too many", R);
+    AR_TRY(ensure_prefill_buffers(m, R));
+    AR_TRY(ensure_f16_weights(m));
+    const size_t dd = d, FF = F;
+    const size_t per_layer16 = (size_t)m->qkv_dim * dd + dd * qd + 3 * FF * dd;
+    AR_TRY(launch_embed_rows(m->embed, c.weight_dtype, d, m->tokens, m->S + 1, T, (int)R, m->pf_x, st));
+    const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
+    for (int l = 0; l < c.layer_count; l++) {
+        const Layer& L = m->layers[l];
+        const uint16_t* w16 = m->pf_w16 + per_layer16 * l;
+        const uint16_t* wqkv16 = w16;
+        const uint16_t* wo16 = wqkv16 + (size_t)m->qkv_dim * dd;
+        const uint16_t* w1_16 = wo16 + dd * qd;
+        const uint16_t* w3_16 = w1_16 + FF * dd;
+        const uint16_t* w2_16 = w3_16 + FF * dd;
+        AR_TRY(launch_rmsnorm_rows_f16(m->pf_x, L.attn_norm, m->pf_h, (int)R, d, (float)c.epsilon, st));
+        GemmLaunch g;
+        g.A = m->pf_h; g.lda = d; g.W = wqkv16; g.ldw = d; g.M = (int)R; g.N = m->qkv_dim; g.K = d;
+        g.bias = L.bqkv; g.C = m->pf_qkv; g.ldc = m->qkv_dim; g.epilogue = GEMV_EPI_STORE; g.f16 = true;
+        AR_TRY(launch_gemm(g, st));
+        PrefillPrep pp;
+        pp.qkv = m->pf_qkv; pp.qkv_stride = m->qkv_dim; pp.q_norm = L.q_norm; pp.k_norm = L.k_norm;
+        pp.eps = (float)c.epsilon; pp.per_head = c.qk_norm_mode == AR_QK_NORM_PER_HEAD; pp.rope_tab = m->rope_tab;
+        pp.kcache = m->kcache + l * layer_cache; pp.vcache = m->vcache + l * layer_cache; pp.B = B; pp.S = m->S;
+        pp.T = T; pp.p0 = 0; pp.heads = c.head_count; pp.kv_heads = c.kv_head_count; pp.hd = c.head_size;
+        pp.qb = m->pf_q;
+        AR_TRY(launch_qk_prep(pp, st));
+        AR_TRY(launch_flash_prefill(m->pf_q, pp.kcache, pp.vcache, m->pf_h, B, m->S, T, 0, c.head_count,
+                                    c.kv_head_count, c.head_size, st));
+        GemmLaunch o;
+        o.A = m->pf_h; o.lda = qd; o.W = wo16; o.ldw = qd; o.M = (int)R; o.N = d; o.K = qd;
+        o.C = m->pf_x; o.ldc = d; o.epilogue = GEMV_EPI_RESIDUAL; o.f16 = true;
+        AR_TRY(launch_gemm(o, st));
+        AR_TRY(launch_rmsnorm_rows_f16(m->pf_x, L.ffn_norm, m->pf_h, (int)R, d, (float)c.epsilon, st));
+        GemmLaunch u;
+        u.A = m->pf_h; u.lda = d; u.W = w1_16; u.W2 = w3_16; u.ldw = d; u.M = (int)R;
+        u.N = F; u.K = d; u.O = m->pf_act; u.ldo = F; u.epilogue = GEMV_EPI_SWIGLU; u.f16 = true;
+        AR_TRY(launch_gemm(u, st));
+        GemmLaunch dn;
+        dn.A = m->pf_act; dn.lda = F; dn.W = w2_16; dn.ldw = F; dn.M = (int)R; dn.N = d; dn.K = F;
+        dn.C = m->pf_x; dn.ldc = d; dn.epilogue = GEMV_EPI_RESIDUAL; dn.f16 = true;
+        AR_TRY(launch_gemm(dn, st));
+    }
+    // last prompt row of every sequence -> residual stream of the decode plan, then the final
+    // RMSNorm + logits GEMV leaves the greedy keys for the next step
+    for (int b = 0; b < B; b++)
+        AR_HIP_TRY(hipMemcpyAsync(m->x + (size_t)b * d, m->pf_x + ((size_t)b * T + T - 1) * d, (size_t)d * 4,
+                                  hipMemcpyDeviceToDevice, st));
+    AR_HIP_TRY(hipMemsetAsync(m->am_keys, 0, (size_t)B * kArgmaxSlots * 8, st));
+    GemvLaunch h;
+    h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
+    h.cols = d; h.x = m->x; h.x_stride = d; h.norm_w = m->final_norm; h.y = logits_out ? m->logits : nullptr;
+    h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.keys = m->am_keys;
+    AR_TRY(launch_gemv(h, st));
+    const int state[3] = {T - 1, T, T};
+    AR_HIP_TRY(hipMemcpyAsync(m->state, state, sizeof(state), hipMemcpyHostToDevice, st));
+    if (logits_out)
+        AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)B * c.vocab_size * 4, hipMemcpyDeviceToHost, st));
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    m->host_pos = T;
     return AR_HIP_OK;
 }

@@ -26,6 +26,8 @@ AR_HIP_ERR_NOT_FOUND = 5
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
+GEMM_STORE, GEMM_RESIDUAL, GEMM_SWIGLU = 0, 1, 2
+
 _c_void_pp = ctypes.POINTER(ctypes.c_void_p)
 _c_int_p = ctypes.POINTER(ctypes.c_int)
 _c_float_p = ctypes.c_void_p
@@ -78,6 +80,8 @@ _SIGS = {
     "ar_hip_qwen3_kernel_time": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), _c_int_p]),
     "ar_hip_qwen3_use_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_use_prefetch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "ar_hip_qwen3_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_gemm_bf16": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4),
 }
 
 
@@ -220,6 +224,12 @@ class HipContext:
 
     def index_of_max(self, x: DeviceBuffer, rows: int, n: int, out: DeviceBuffer):
         check(lib().ar_hip_index_of_max(self.handle, x.ptr, rows, n, out.ptr))
+
+    def gemm_bf16(self, A: DeviceBuffer, W: DeviceBuffer, M: int, N: int, K: int, epilogue: int = GEMM_STORE,
+                  W2: DeviceBuffer | None = None, bias: DeviceBuffer | None = None, C: DeviceBuffer | None = None,
+                  O: DeviceBuffer | None = None):
+        check(lib().ar_hip_gemm_bf16(self.handle, A.ptr, W.ptr, W2.ptr if W2 else None, bias.ptr if bias else None,
+                                     C.ptr if C else None, O.ptr if O else None, M, N, K, epilogue))
 
     def attention_decode(self, q, k, v, q_norm, k_norm, qk_eps, qk_norm_mode, k_cache, v_cache, max_seq, pos,
                          heads, kv_heads, head_dim, theta, out):

@@ -58,6 +58,13 @@ class AutoregressiveModel:
                                             logits.ctypes.data if return_logits else None))
         return (toks, logits) if return_logits else toks
 
+    def prefill(self, return_logits: bool = False):
+        """The whole prompt at once (MFMA path for bf16 weights); afterwards the model is where
+        prompt-length next() calls would leave it.  Optionally returns the last prompt row's logits."""
+        logits = np.empty((self.batch, self.qwen.config.vocab_size), dtype=np.float32) if return_logits else None
+        hw.check(hw.lib().ar_hip_qwen3_prefill(self.handle, logits.ctypes.data if return_logits else None))
+        return logits
+
     def run(self, steps: int) -> np.ndarray:
         """``steps`` calls of next() without host synchronisation; returns (batch, steps) tokens."""
         out = np.empty((self.batch, steps), dtype=np.int32)

@@ -114,6 +114,19 @@ int ar_hip_attention_decode(ar_hip_ctx *ctx, const float *q, const float *k, con
                             float *k_cache, float *v_cache, int max_seq, int pos, int heads,
                             int kv_heads, int head_dim, double rope_theta, float *out);
 
+/* Multi-token projection on the MFMA units: C[M x N] = A[M x K] . W[N x K]^T, A and W bf16
+ * (raw uint16 bits, K contiguous), fp32 accumulation.  N % 128 == 0, K % 64 == 0.
+ *   AR_GEMM_STORE:    C (fp32, [M][N]) = result (+ bias[N] if non-null)
+ *   AR_GEMM_RESIDUAL: C += result
+ *   AR_GEMM_SWIGLU:   O (bf16, [M][N]) = (A.W2^T) * silu(A.W^T)
+ * The stacked-row form of LayerFeatures.dense (domain/graph/.../LayerFeatures.java:785-830) for
+ * prompt rows, which the reference feeds one per step (AutoregressiveModel.java:295-308). */
+#define AR_GEMM_STORE 0
+#define AR_GEMM_RESIDUAL 1
+#define AR_GEMM_SWIGLU 2
+int ar_hip_gemm_bf16(ar_hip_ctx *ctx, const uint16_t *A, const uint16_t *W, const uint16_t *W2, const float *bias,
+                     float *C, uint16_t *O, int M, int N, int K, int epilogue);
+
 /* ---- Qwen3 model -------------------------------------------------------------------
  * Replaces Qwen3.model + CompiledModel.forward + AutoregressiveModel
  * (engine/ml/.../qwen3/Qwen3.java:334-415, domain/graph/.../model/CompiledModel.java:189-197,
@@ -160,6 +173,13 @@ int ar_hip_qwen3_next(ar_qwen3 *m, int32_t *tokens_out, float *logits_out);
 /* `steps` calls of next() enqueued back to back without host synchronisation (the token
  * loop stays on the device); tokens_out is batch x steps (row-major by sequence). */
 int ar_hip_qwen3_run(ar_qwen3 *m, int steps, int32_t *tokens_out);
+/* Whole-prompt prefill from position 0: the prompt rows of every sequence run together (bf16
+ * weights: MFMA GEMMs + causal flash attention; fp32 weights: the decode step per token).  Leaves
+ * the model exactly where prompt_len calls of next() would: position = prompt length, KV cache
+ * rows 0..prompt_len-1 written, and the next next() feeds the greedy token of the last prompt
+ * row.  logits_out (optional, batch x vocab, host) receives the last prompt row's logits.
+ * AutoregressiveModel.next over the prompt (AutoregressiveModel.java:295-299), batched. */
+int ar_hip_qwen3_prefill(ar_qwen3 *m, float *logits_out);
 /* Current position (AutoregressiveModel.getCurrentStep). */
 int ar_hip_qwen3_position(ar_qwen3 *m, int *pos);
 /* Residual-stream vector after the last step (batch x dim floats, host) for activation checks. */

@@ -1,0 +1,149 @@
+"""GPU parity of the MFMA prefill path, through the C-ABI.
+
+GEMM: against float64 products of the same bf16-rounded operands (fp32 accumulation, 1e-5
+relative; the SwiGLU epilogue rounds its output to bf16, 8e-3).  Prefill: a batched prompt must
+leave the model where sequential next() calls would (north-star bf16 tolerance 2e-2 on logits,
+since prefill feeds bf16 activations to the MFMA units), checked against the GPU decode path and
+against the FP64 oracle on the same bf16-rounded weights.
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import oracle
+from common_amd import config as C
+from common_amd import hardware as hw
+from common_amd import synthetic
+from common_amd.qwen3 import Qwen3
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+BF16_TOL = 2e-2
+
+
+def bf16(a):
+    return synthetic.bf16_round(np.asarray(a, np.float32))
+
+
+def bits(a):
+    return (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (300, 512, 256), (129, 768, 1024), (2048, 4096, 2048)])
+def test_gemm_store_bias(ctx, M, N, K):
+    r = np.random.default_rng(M + N + K)
+    A = bf16(r.standard_normal((M, K)))
+    W = bf16(r.standard_normal((N, K)) * 0.05)
+    b = r.standard_normal(N).astype(np.float32)
+    Cd = ctx.allocate(M * N * 4)
+    ctx.gemm_bf16(ctx.to_device(bits(A)), ctx.to_device(bits(W)), M, N, K, hw.GEMM_STORE, bias=ctx.to_device(b), C=Cd)
+    ctx.synchronize()
+    got = Cd.download(np.float32, M * N).reshape(M, N)
+    ref = A.astype(np.float64) @ W.astype(np.float64).T + b
+    assert rel_err(got, ref) <= 1e-5
+
+
+def test_gemm_residual_and_swiglu(ctx):
+    M, N, K = 200, 384, 512
+    r = np.random.default_rng(9)
+    A = bf16(r.standard_normal((M, K)))
+    W = bf16(r.standard_normal((N, K)) * 0.05)
+    W2 = bf16(r.standard_normal((N, K)) * 0.05)
+    C0 = r.standard_normal((M, N)).astype(np.float32)
+    Cd = ctx.to_device(C0)
+    Ad, Wd, W2d = ctx.to_device(bits(A)), ctx.to_device(bits(W)), ctx.to_device(bits(W2))
+    ctx.gemm_bf16(Ad, Wd, M, N, K, hw.GEMM_RESIDUAL, C=Cd)
+    Od = ctx.allocate(M * N * 2)
+    ctx.gemm_bf16(Ad, Wd, M, N, K, hw.GEMM_SWIGLU, W2=W2d, O=Od)
+    ctx.synchronize()
+    g = A.astype(np.float64) @ W.astype(np.float64).T
+    u = A.astype(np.float64) @ W2.astype(np.float64).T
+    assert rel_err(Cd.download(np.float32, M * N).reshape(M, N), C0 + g) <= 1e-5
+    o = (Od.download(np.uint16, M * N).astype(np.uint32) << 16).view(np.float32).reshape(M, N)
+    assert rel_err(o, u * (g / (1 + np.exp(-g)))) <= 8e-3
+
+
+def test_gemm_rejects_bad_shapes(ctx):
+    z = ctx.allocate(1 << 16)
+    with pytest.raises(hw.HardwareException):
+        ctx.gemm_bf16(z, z, 4, 100, 64, hw.GEMM_STORE, C=z)   # N not a multiple of 128
+    with pytest.raises(hw.HardwareException):
+        ctx.gemm_bf16(z, z, 4, 128, 40, hw.GEMM_STORE, C=z)   # K not a multiple of 64
+
+
+def _bf16_cfg(base, **kw):
+    return dataclasses.replace(base, weight_dtype=C.DTYPE_BF16, **kw)
+
+
+@pytest.mark.parametrize("per_head,batch", [(False, 1), (True, 2)])
+def test_prefill_matches_sequential_decode_and_oracle(ctx, per_head, batch):
+    cfg = _bf16_cfg(C.C1_TINY, seq_len=200, max_batch=batch,
+                    qk_norm_mode=C.QK_NORM_PER_HEAD if per_head else C.QK_NORM_WHOLE)
+    sd = synthetic.state_dict(cfg, seed=5)
+    T = 150  # several 128-row query tiles, ragged
+    prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=20 + b) for b in range(batch)]
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        lp = am.prefill(return_logits=True)
+        assert am.get_current_step() == T
+        after_prefill = am.run(6)
+        # the same prompt fed one token per step through the decode plan
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        am.run(T - 1)
+        _, ls = am.next(return_logits=True)
+        after_seq = am.run(6)
+    assert rel_err(lp, ls) <= BF16_TOL
+    for b, p in enumerate(prompts):
+        ref = oracle.OracleQwen3(cfg, sd, precision="fp64")
+        rf, rl = ref.generate(p, 6)
+        assert rel_err(lp[b], rl[T - 1]) <= BF16_TOL
+        # greedy continuations agree unless the oracle's top-2 margin is within the bf16 tolerance
+        for s in range(6):
+            top = np.sort(rl[T - 1 + s])[-2:]
+            if (top[1] - top[0]) / abs(top[1]) < BF16_TOL:
+                break
+            assert after_prefill[b, s] == rf[T + s] == after_seq[b, s]
+
+
+def test_prefill_fp32_weights_uses_decode_path(ctx):
+    cfg = dataclasses.replace(C.C1_TINY)
+    sd = synthetic.state_dict(cfg, seed=0)
+    prompt = synthetic.prompt_ids(C.C1_PROMPT, cfg.vocab_size, seed=0)
+    ref = oracle.OracleQwen3(cfg, sd, precision="fp64")
+    rf, rl = ref.generate(prompt, 4)
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        am.reset()
+        am.set_prompt(prompt)
+        lp = am.prefill(return_logits=True)
+        toks = am.run(4)
+    assert rel_err(lp[0], rl[len(prompt) - 1]) <= 1e-4
+    np.testing.assert_array_equal(toks[0], rf[len(prompt):])
+
+
+def test_prefill_c4_shape_matches_sequential_decode(ctx):
+    """Qwen3-1.7B shape, bf16 weights, prefill 2048 tokens vs the decode step."""
+    cfg = dataclasses.replace(C.C4_1_7B, seq_len=C.C4_PROMPT + 8)
+    T = C.C4_PROMPT
+    prompt = synthetic.prompt_ids(T, cfg.vocab_size, seed=4)
+    with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=4), ctx) as m:
+        am = m.model
+        am.reset()
+        am.set_prompt(prompt)
+        lp = am.prefill(return_logits=True)
+        after_prefill = am.run(4)
+        am.reset()
+        am.set_prompt(prompt)
+        am.run(T - 1)
+        _, ls = am.next(return_logits=True)
+        after_seq = am.run(4)
+    assert rel_err(lp, ls) <= BF16_TOL
+    top = np.sort(ls[0])[-2:]
+    if (top[1] - top[0]) / abs(top[1]) > BF16_TOL:
+        assert after_prefill[0, 0] == after_seq[0, 0]
