@@ -136,10 +136,14 @@ struct PrefillPrep {
     float* vcache = nullptr;
     int B = 1, S = 0, T = 0, p0 = 0, heads = 0, kv_heads = 0, hd = 0;
     uint16_t* qb = nullptr;
+    uint16_t* k16 = nullptr;   // [B][KV][Tp][hd] fp16 keys of the prompt rows
+    uint16_t* vt16 = nullptr;  // [B][KV][hd][Tp] fp16 values, transposed
+    int Tp = 0;                // rows reserved per (sequence, KV head), multiple of 32
 };
 int launch_qk_prep(const PrefillPrep& a, hipStream_t stream);
-int launch_flash_prefill(const uint16_t* qb, const float* kcache, const float* vcache, uint16_t* out, int B, int S,
-                         int T, int p0, int heads, int kv_heads, int hd, hipStream_t stream);
+// Causal attention over prompt rows 0..T-1 (prefill from position 0), fp16 MFMAs, fp16 output.
+int launch_flash_prefill(const uint16_t* qb, const uint16_t* k16, const uint16_t* vt16, uint16_t* out, int B, int T,
+                         int Tp, int heads, int kv_heads, int hd, hipStream_t stream);
 
 struct AttnLaunch {
     const float* qkv = nullptr;   // [batch][qkv_stride]: q | k | v raw projections

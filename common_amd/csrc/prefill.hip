@@ -76,6 +76,9 @@ struct PrepParams {
     float* vcache;
     int S, T, p0, heads, kv_heads, hd;
     uint16_t* qb;           // [R][heads*hd] fp16 normalised, rotated queries
+    uint16_t* k16;          // [B][KV][Tp][hd] fp16 keys of the prompt rows (for the attention MFMAs)
+    uint16_t* vt16;         // [B][KV][hd][Tp] fp16 values, transposed
+    int Tp;
 };
 
 // One block per prompt row: QK-norm (whole vector or per head), RoPE at position p0 + t, k and v
@@ -132,52 +135,54 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
         }
         const float2 cs = rope[f];
         float* kc = p.kcache + (((size_t)b * p.kv_heads + g) * p.S + pos) * hd;
-        kc[f] = x1 * cs.x - x2 * cs.y;
-        kc[f + fd] = x2 * cs.x + x1 * cs.y;
+        const float o1 = x1 * cs.x - x2 * cs.y, o2 = x2 * cs.x + x1 * cs.y;
+        kc[f] = o1;
+        kc[f + fd] = o2;
+        uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
+        k16[f] = f2h(o1);
+        k16[f + fd] = f2h(o2);
     }
     for (int idx = threadIdx.x; idx < kv_dim; idx += blockDim.x) {
         const int g = idx / hd, i = idx - g * hd;
         p.vcache[(((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i] = v[idx];
+        p.vt16[(((size_t)b * p.kv_heads + g) * hd + i) * p.Tp + t] = f2h(v[idx]);
     }
 }
 
 struct FlashParams {
-    const uint16_t* qb;   // [B*T][heads*hd] fp16
-    const float* kcache;  // [B][KV][S][hd]
-    const float* vcache;
+    const uint16_t* qb;   // [B*T][heads*hd] fp16 queries
+    const uint16_t* k16;  // [B][KV][Tp][hd] fp16 keys (prompt rows)
+    const uint16_t* vt16; // [B][KV][hd][Tp] fp16 values, transposed
     uint16_t* out;        // [B*T][heads*hd] fp16
-    int S, T, p0, heads, kv_heads;
+    int T, Tp, heads, kv_heads;
 };
 
-// Causal attention for a tile of 128 query rows (4 wavefronts x 32 rows) of one head, over key
-// tiles of 32 rows with an online softmax.  S = Q K^T and O += P V run on
-// v_mfma_f32_32x32x16_f16; K and V tiles are converted to fp16 in LDS (V transposed, so a lane
-// can read 8 consecutive keys of one column); P goes through LDS to change from the result layout
-// (column = key) to the operand layout (row = query, 8 consecutive keys).
+// Causal attention over the prompt for 32 query rows of one head per wavefront (one wavefront per
+// block, heaviest query tiles dispatched first), online softmax over key tiles of 32.
+// Computed transposed so every lane owns one query:
+//   S^T (32 keys x 32 queries) = K . Q^T   A = K rows (16-byte loads of k16), B = Q (registers)
+//   O^T (hd x 32 queries)     += V^T . P^T A = V^T rows (vt16), B = P^T straight from registers
+// In the result layout lane l holds query l%32 and keys (r/4)*8 + (l/32)*4 + r%4 (r = 0..15), so a
+// query's 32 scores sit in lanes l and l^32: its max and sum need one shuffle.  The P.V contraction
+// runs over keys in that same register order (any order of a sum's terms gives the same sum up to
+// rounding), so P^T registers are the B operand as they are, and V^T is read in the matching
+// order.  Per-query rescaling multiplies whole lanes.
 template <int HD>
-__global__ __launch_bounds__(256) void flash_prefill_kernel(FlashParams p) {
-    constexpr int BQ = 128, BKV = 32;
-    constexpr int KS = HD + 8;   // LDS row stride of the K tile (fp16)
-    constexpr int VS = BKV + 8;  // LDS row stride of the transposed V tile (fp16)
-    constexpr int PS = BKV + 8;  // LDS row stride of a wave's P tile
-    constexpr int NT = HD / 32;  // 32-column output tiles
-    __shared__ __attribute__((aligned(16))) uint16_t ks[BKV * KS];
-    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * VS];
-    __shared__ __attribute__((aligned(16))) uint16_t ps[4][32 * PS];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+__global__ __launch_bounds__(64) void flash_prefill_kernel(FlashParams p) {
+    constexpr int NT = HD / 32;  // 32-row hd tiles of O^T
+    const int lane = threadIdx.x, h2 = lane >> 5, lq = lane & 31;
+    const int qt = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int g = h / (p.heads / p.kv_heads);
     const int q_dim = p.heads * HD;
-    const int row0 = qt * BQ + wave * 32;  // first query row (within the sequence) of this wave
-    const float* kc = p.kcache + ((size_t)b * p.kv_heads + g) * (size_t)p.S * HD;
-    const float* vc = p.vcache + ((size_t)b * p.kv_heads + g) * (size_t)p.S * HD;
+    const int row0 = qt * 32;
+    const int myq = row0 + lq;  // this lane's query row (may be >= T on the last tile: not stored)
+    const uint16_t* kb = p.k16 + ((size_t)b * p.kv_heads + g) * (size_t)p.Tp * HD;
+    const uint16_t* vb = p.vt16 + ((size_t)b * p.kv_heads + g) * (size_t)HD * p.Tp;
 
-    // this wave's queries in operand layout: row l%32, hd (l/32)*8 + 16*kk .. +7
-    halfx8 qf[HD / 16];
+    halfx8 qf[HD / 16];  // B operand: query lq, hd (l/32)*8 + 16*kk .. +7
     {
-        const int t = min(row0 + (lane & 31), p.T - 1);
-        const uint16_t* qrow = p.qb + ((size_t)b * p.T + t) * q_dim + (size_t)h * HD + (lane >> 5) * 8;
+        const int t = min(myq, p.T - 1);
+        const uint16_t* qrow = p.qb + ((size_t)b * p.T + t) * q_dim + (size_t)h * HD + h2 * 8;
 #pragma unroll
         for (int kk = 0; kk < HD / 16; kk++) qf[kk] = *reinterpret_cast<const halfx8*>(qrow + kk * 16);
     }
@@ -186,96 +191,91 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(FlashParams p) {
     for (int j = 0; j < NT; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[j][r] = 0.f;
-    float m_r[16], l_r[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) { m_r[r] = -INFINITY; l_r[r] = 0.f; }
+    float m = -INFINITY, l = 0.f;
     const float scale = sqrtf((float)HD);
+    const int kend = min(row0 + 32, p.T);  // keys 0 .. last query of the tile
 
-    // keys 0 .. p0 + (last query row of the block)
-    const int qlast = min(qt * BQ + BQ, p.T) - 1;
-    const int kend = p.p0 + qlast + 1;
-    for (int k0 = 0; k0 < kend; k0 += BKV) {
-        __syncthreads();  // previous tile's LDS reads are done
-        // K tile -> ks[key][hd], V tile -> vt[hd][key], as fp16 (rows past kend are clamped;
-        // the causal mask drops them)
-        for (int e = tid * 4; e < BKV * HD; e += 256 * 4) {
-            const int kr = e / HD, c = e - kr * HD;
-            const int key = min(k0 + kr, kend - 1);
-            const float4 kv4 = *reinterpret_cast<const float4*>(kc + (size_t)key * HD + c);
-            const float4 vv4 = *reinterpret_cast<const float4*>(vc + (size_t)key * HD + c);
-            uint16_t* kd = &ks[kr * KS + c];
-            kd[0] = f2h(kv4.x); kd[1] = f2h(kv4.y); kd[2] = f2h(kv4.z); kd[3] = f2h(kv4.w);
-            vt[(c + 0) * VS + kr] = f2h(vv4.x);
-            vt[(c + 1) * VS + kr] = f2h(vv4.y);
-            vt[(c + 2) * VS + kr] = f2h(vv4.z);
-            vt[(c + 3) * VS + kr] = f2h(vv4.w);
-        }
-        __syncthreads();
-        if (k0 > p.p0 + row0 + 31) continue;  // every key of this tile is after this wave's rows
-
-        // S = Q K^T for 32 rows x 32 keys
+    // software pipeline: the next tile's K and this tile's V are in flight while the current
+    // tile's MFMAs and softmax run
+    halfx8 kf[HD / 16];
+    auto load_k = [&](int k0) {
+        const uint16_t* krow = kb + (size_t)min(k0 + lq, p.T - 1) * HD + h2 * 8;
+#pragma unroll
+        for (int kk = 0; kk < HD / 16; kk++) kf[kk] = *reinterpret_cast<const halfx8*>(krow + kk * 16);
+    };
+    load_k(0);
+    for (int k0 = 0; k0 < kend; k0 += 32) {
+        uint2 vlo[2][NT], vhi[2][NT];
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                const uint16_t* vrow = vb + (size_t)(j * 32 + lq) * p.Tp + k0 + 16 * kk + h2 * 4;
+                vlo[kk][j] = *reinterpret_cast<const uint2*>(vrow);
+                vhi[kk][j] = *reinterpret_cast<const uint2*>(vrow + 8);
+            }
+        // S^T = K Q^T
         floatx16 s;
 #pragma unroll
         for (int r = 0; r < 16; r++) s[r] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < HD / 16; kk++) {
-            const halfx8 kf = *reinterpret_cast<const halfx8*>(&ks[(lane & 31) * KS + kk * 16 + (lane >> 5) * 8]);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(qf[kk], kf, s, 0, 0, 0);
-        }
-        // mask, online softmax; lane holds key k0 + lane%32 for rows (r/4)*8 + (lane/32)*4 + r%4
-        const int key = k0 + (lane & 31);
-        float alpha[16];
+        for (int kk = 0; kk < HD / 16; kk++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], s, 0, 0, 0);
+        if (k0 + 32 < kend) load_k(k0 + 32);
+        // mask + online softmax (keys past the query, or past the prompt, get weight 0)
+        float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int qrow = row0 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            const int key = k0 + (r >> 2) * 8 + h2 * 4 + (r & 3);
             float v = s[r] / scale;
-            if (key > p.p0 + qrow) v = -INFINITY;
-            float mx = v;
-#pragma unroll
-            for (int off = 1; off < 32; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            const float m_new = fmaxf(m_r[r], mx);
-            const float e = (v == -INFINITY) ? 0.f : expf(v - m_new);
-            float sum = e;
-#pragma unroll
-            for (int off = 1; off < 32; off <<= 1) sum += __shfl_xor(sum, off, 64);
-            alpha[r] = (m_r[r] == -INFINITY) ? 0.f : expf(m_r[r] - m_new);
-            l_r[r] = l_r[r] * alpha[r] + sum;
-            m_r[r] = m_new;
-            s[r] = e;
+            if (key > myq || key >= p.T) v = -INFINITY;
+            s[r] = v;
+            mx = fmaxf(mx, v);
         }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float e = (s[r] == -INFINITY) ? 0.f : expf(s[r] - m_new);
+            s[r] = e;
+            sum += e;
+        }
+        sum += __shfl_xor(sum, 32, 64);
+        const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
+        l = l * alpha + sum;
+        m = m_new;
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) o[j][r] *= alpha[r];
-        // P (result layout) -> LDS -> operand layout
-        uint16_t* pw = ps[wave];
+            for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+        // O^T += V^T P^T over the 32 keys, in register order: k-step kk, slot i <-> register 8kk+i
+        // <-> key k0 + 16kk + 8*(i/4) + (l/32)*4 + i%4
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int prow = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            pw[prow * PS + (lane & 31)] = f2h(s[r]);
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's P writes are in LDS
+        for (int kk = 0; kk < 2; kk++) {
+            halfx8 pf;
 #pragma unroll
-        for (int kk = 0; kk < BKV / 16; kk++) {
-            const halfx8 pf = *reinterpret_cast<const halfx8*>(&pw[(lane & 31) * PS + kk * 16 + (lane >> 5) * 8]);
+            for (int i = 0; i < 8; i++) pf[i] = (_Float16)s[8 * kk + i];
 #pragma unroll
             for (int j = 0; j < NT; j++) {
-                const halfx8 vf =
-                    *reinterpret_cast<const halfx8*>(&vt[(j * 32 + (lane & 31)) * VS + kk * 16 + (lane >> 5) * 8]);
-                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pf, vf, o[j], 0, 0, 0);
+                halfx8 vf;
+                const uint16_t* lo16 = reinterpret_cast<const uint16_t*>(&vlo[kk][j]);
+                const uint16_t* hi16 = reinterpret_cast<const uint16_t*>(&vhi[kk][j]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    vf[i] = *reinterpret_cast<const _Float16*>(&lo16[i]);
+                    vf[i + 4] = *reinterpret_cast<const _Float16*>(&hi16[i]);
+                }
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[j], 0, 0, 0);
             }
         }
     }
-    // normalise and store
+    if (myq >= p.T) return;
+    const float inv = 1.0f / l;
+    uint16_t* orow = p.out + ((size_t)b * p.T + myq) * q_dim + (size_t)h * HD;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int qrow = row0 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (qrow >= p.T) continue;
-        const float inv = 1.0f / l_r[r];
-        uint16_t* orow = p.out + ((size_t)b * p.T + qrow) * q_dim + (size_t)h * HD;
+    for (int j = 0; j < NT; j++)
 #pragma unroll
-        for (int j = 0; j < NT; j++) orow[j * 32 + (lane & 31)] = f2h(o[j][r] * inv);
-    }
+        for (int r = 0; r < 16; r++) orow[j * 32 + (r >> 2) * 8 + h2 * 4 + (r & 3)] = f2h(o[j][r] * inv);
 }
 
 }  // namespace
@@ -302,7 +302,8 @@ int launch_rmsnorm_rows_f16(const float* x, const float* w, uint16_t* out, int r
 }
 
 int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
-    AR_CHECK_ARG(a.qkv && a.rope_tab && a.kcache && a.vcache && a.qb, "qk prep: null pointer");
+    AR_CHECK_ARG(a.qkv && a.rope_tab && a.kcache && a.vcache && a.qb && a.k16 && a.vt16, "qk prep: null pointer");
+    AR_CHECK_ARG(a.Tp >= a.T, "qk prep: fp16 copies hold %d rows, %d needed", a.Tp, a.T);
     AR_CHECK_ARG(a.heads + a.kv_heads <= 64, "qk prep: too many heads");
     AR_CHECK_ARG(a.p0 >= 0 && a.p0 + a.T <= a.S, "qk prep: rows %d..%d outside the %d-row cache", a.p0, a.p0 + a.T,
                  a.S);
@@ -310,23 +311,23 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     p.qkv = a.qkv; p.qkv_stride = a.qkv_stride; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.eps = a.eps;
     p.per_head = a.per_head; p.rope_tab = a.rope_tab; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.S;
     p.T = a.T; p.p0 = a.p0; p.heads = a.heads; p.kv_heads = a.kv_heads; p.hd = a.hd; p.qb = a.qb;
+    p.k16 = a.k16; p.vt16 = a.vt16; p.Tp = a.Tp;
     hipLaunchKernelGGL(qk_prep_kernel, dim3(a.B * a.T), dim3(256), 0, stream, p);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
 
-int launch_flash_prefill(const uint16_t* qb, const float* kcache, const float* vcache, uint16_t* out, int B, int S,
-                         int T, int p0, int heads, int kv_heads, int hd, hipStream_t stream) {
-    AR_CHECK_ARG(qb && kcache && vcache && out && T > 0 && B > 0, "flash prefill: bad arguments");
-    AR_CHECK_ARG(heads % kv_heads == 0 && p0 >= 0 && p0 + T <= S, "flash prefill: bad shape");
+int launch_flash_prefill(const uint16_t* qb, const uint16_t* k16, const uint16_t* vt16, uint16_t* out, int B, int T,
+                         int Tp, int heads, int kv_heads, int hd, hipStream_t stream) {
+    AR_CHECK_ARG(qb && k16 && vt16 && out && T > 0 && B > 0, "flash prefill: bad arguments");
+    AR_CHECK_ARG(heads % kv_heads == 0 && Tp >= T && Tp % 32 == 0, "flash prefill: bad shape");
     FlashParams p;
-    p.qb = qb; p.kcache = kcache; p.vcache = vcache; p.out = out; p.S = S; p.T = T; p.p0 = p0; p.heads = heads;
-    p.kv_heads = kv_heads;
-    dim3 grid((T + 127) / 128, heads, B);
+    p.qb = qb; p.k16 = k16; p.vt16 = vt16; p.out = out; p.T = T; p.Tp = Tp; p.heads = heads; p.kv_heads = kv_heads;
+    dim3 grid((T + 31) / 32, heads, B);
     if (hd == 128)
-        hipLaunchKernelGGL(flash_prefill_kernel<128>, grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(flash_prefill_kernel<128>, grid, dim3(64), 0, stream, p);
     else if (hd == 64)
-        hipLaunchKernelGGL(flash_prefill_kernel<64>, grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(flash_prefill_kernel<64>, grid, dim3(64), 0, stream, p);
     else {
         ar_set_error("flash prefill: head_dim %d not supported", hd);
         return AR_HIP_ERR_INVALID;

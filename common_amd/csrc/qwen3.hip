@@ -100,6 +100,10 @@ struct ar_qwen3 {
     float* pf_qkv = nullptr;     // [R][qkv_dim]
     uint16_t* pf_q = nullptr;    // [R][q_dim] fp16 normalised, rotated queries
     uint16_t* pf_act = nullptr;  // [R][F] fp16 SwiGLU output
+    uint16_t* pf_k16 = nullptr;  // [B][KV][Tp][hd] fp16 keys of the prompt rows
+    uint16_t* pf_vt16 = nullptr; // [B][KV][hd][Tp] fp16 values, transposed (zeroed once: padded keys
+                                 // get weight 0 and must not hold NaN bit patterns)
+    int pf_tp = 0;
     // fp16 copies of the projection matrices for the prefill GEMMs (made on the first prefill)
     uint16_t* pf_w16 = nullptr;
     bool pf_w16_valid = false;
@@ -130,7 +134,7 @@ void release(ar_qwen3* m) {
     if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
                     m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
-                    m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_w16};
+                    m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_w16, m->pf_k16, m->pf_vt16};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     delete m;
@@ -674,6 +678,14 @@ int ensure_prefill_buffers(ar_qwen3* m, size_t rows) {
     AR_TRY(ar_ctx_alloc(m->ctx, rows * m->q_dim * 2, (void**)&m->pf_q));
     AR_TRY(ar_ctx_alloc(m->ctx, rows * c.hidden_dim * 2, (void**)&m->pf_act));
     m->pf_rows = rows;
+    if (!m->pf_k16) {
+        m->pf_tp = (m->S + 31) / 32 * 32;
+        const size_t n = (size_t)m->B * c.kv_head_count * m->pf_tp * c.head_size * 2;
+        AR_TRY(ar_ctx_alloc(m->ctx, n, (void**)&m->pf_k16));
+        AR_TRY(ar_ctx_alloc(m->ctx, n, (void**)&m->pf_vt16));
+        AR_HIP_TRY(hipMemsetAsync(m->pf_k16, 0, n, m->ctx->stream));
+        AR_HIP_TRY(hipMemsetAsync(m->pf_vt16, 0, n, m->ctx->stream));
+    }
     return AR_HIP_OK;
 }
 
@@ -740,9 +752,9 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         pp.eps = (float)c.epsilon; pp.per_head = c.qk_norm_mode == AR_QK_NORM_PER_HEAD; pp.rope_tab = m->rope_tab;
         pp.kcache = m->kcache + l * layer_cache; pp.vcache = m->vcache + l * layer_cache; pp.B = B; pp.S = m->S;
         pp.T = T; pp.p0 = 0; pp.heads = c.head_count; pp.kv_heads = c.kv_head_count; pp.hd = c.head_size;
-        pp.qb = m->pf_q;
+        pp.qb = m->pf_q; pp.k16 = m->pf_k16; pp.vt16 = m->pf_vt16; pp.Tp = m->pf_tp;
         AR_TRY(launch_qk_prep(pp, st));
-        AR_TRY(launch_flash_prefill(m->pf_q, pp.kcache, pp.vcache, m->pf_h, B, m->S, T, 0, c.head_count,
+        AR_TRY(launch_flash_prefill(m->pf_q, m->pf_k16, m->pf_vt16, m->pf_h, B, T, m->pf_tp, c.head_count,
                                     c.kv_head_count, c.head_size, st));
         GemmLaunch o;
         o.A = m->pf_h; o.lda = qd; o.W = wo16; o.ldw = qd; o.M = (int)R; o.N = d; o.K = qd;
