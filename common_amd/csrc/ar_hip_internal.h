@@ -138,7 +138,7 @@ struct PrefillPrep {
     uint16_t* qb = nullptr;
     uint16_t* k16 = nullptr;   // [B][KV][Tp][hd] fp16 keys of the prompt rows
     uint16_t* vt16 = nullptr;  // [B][KV][hd][Tp] fp16 values, transposed
-    int Tp = 0;                // rows reserved per (sequence, KV head), multiple of 32
+    int Tp = 0;                // rows reserved per (sequence, KV head), multiple of 64
 };
 int launch_qk_prep(const PrefillPrep& a, hipStream_t stream);
 // Causal attention over prompt rows 0..T-1 (prefill from position 0), fp16 MFMAs, fp16 output.

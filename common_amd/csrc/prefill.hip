@@ -15,6 +15,7 @@ namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 halfx8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // fp32 -> fp16 bits (round to nearest even)
 __device__ inline uint16_t f2h(float f) {
@@ -155,29 +156,77 @@ struct FlashParams {
     const uint16_t* vt16; // [B][KV][hd][Tp] fp16 values, transposed
     uint16_t* out;        // [B*T][heads*hd] fp16
     int T, Tp, heads, kv_heads;
+    int gsub;   // query heads of one KV group per block (divides heads/kv_heads and 4)
+    int nsub;   // (heads/kv_heads) / gsub
+    int pairs;  // B * kv_heads
+    int nq;     // query blocks of 32 * (4/gsub) rows
 };
 
-// Causal attention over the prompt for 32 query rows of one head per wavefront (one wavefront per
-// block, heaviest query tiles dispatched first), online softmax over key tiles of 32.
-// Computed transposed so every lane owns one query:
-//   S^T (32 keys x 32 queries) = K . Q^T   A = K rows (16-byte loads of k16), B = Q (registers)
-//   O^T (hd x 32 queries)     += V^T . P^T A = V^T rows (vt16), B = P^T straight from registers
+// Causal attention over the prompt, one 8-wavefront block per (sequence, KV head, query block).
+// Waves w and w+4 own the same queries: `gsub` query heads of the KV group x (4/gsub) query tiles
+// of 32 rows.  Keys advance in super-tiles of 64, staged once per block in double-buffered LDS (the
+// next super-tile's global loads are in flight while the current one is used); wave w takes the
+// first 32 keys of each super-tile and wave w+4 the second 32, and the two partial softmax states
+// are merged through LDS at the end.  Blocks of one (sequence, KV head) are placed on one XCD when
+// the pair count allows, so that pair's K/V stays in that XCD's L2; the heaviest query blocks are
+// dispatched first.
+// Per wave the product is computed transposed so every lane owns one query:
+//   S^T (32 keys x 32 queries) = K . Q^T   A = K rows (LDS), B = Q (registers)
+//   O^T (hd x 32 queries)     += V^T . P^T A = V^T rows (LDS), B = P^T straight from registers
 // In the result layout lane l holds query l%32 and keys (r/4)*8 + (l/32)*4 + r%4 (r = 0..15), so a
 // query's 32 scores sit in lanes l and l^32: its max and sum need one shuffle.  The P.V contraction
 // runs over keys in that same register order (any order of a sum's terms gives the same sum up to
-// rounding), so P^T registers are the B operand as they are, and V^T is read in the matching
-// order.  Per-query rescaling multiplies whole lanes.
+// rounding), so P^T registers are the B operand as they are, and V^T is read in the matching order.
+// Softmax runs in base 2 on scores pre-multiplied by log2(e)/sqrt(hd); the running maximum is only
+// raised (and O, l rescaled) when a tile's maximum exceeds it by more than 8, so P <= 2^8 in fp16.
+constexpr int kFlashWaves = 8;   // per block: 4 query groups x 2 key halves
+constexpr int kFlashKeys = 64;   // keys per super-tile (Tp is a multiple of this)
+
 template <int HD>
-__global__ __launch_bounds__(64) void flash_prefill_kernel(FlashParams p) {
-    constexpr int NT = HD / 32;  // 32-row hd tiles of O^T
-    const int lane = threadIdx.x, h2 = lane >> 5, lq = lane & 31;
-    const int qt = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int g = h / (p.heads / p.kv_heads);
+struct FlashLds {
+    static constexpr int KS = HD + 8;  // K tile row stride (halves): 16-byte rows, conflict-free b128 reads
+    static constexpr int VS = 64 + 4;  // V^T tile row stride (halves): conflict-free b64 reads
+    static constexpr int K_HALVES = kFlashKeys * KS;
+    static constexpr int V_HALVES = HD * VS;
+    static constexpr int TILE_BYTES = 2 * 2 * (K_HALVES + V_HALVES);  // two buffers of K and V^T
+    static constexpr int MERGE_BYTES = 4 * (HD / 2 + 2) * 64 * 4;      // 4 waves x (O^T + m + l) x 64 lanes
+    static constexpr int BYTES = TILE_BYTES > MERGE_BYTES ? TILE_BYTES : MERGE_BYTES;
+};
+
+template <int HD>
+__global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
+    using L = FlashLds<HD>;
+    constexpr int NT = HD / 32;           // 32-row hd tiles of O^T
+    constexpr int CPT = HD * 8 / 512;     // 16-byte chunks per thread per super-tile (K and V^T alike)
+    __shared__ __attribute__((aligned(16))) unsigned char lds[L::BYTES];
+    uint16_t* const ks = reinterpret_cast<uint16_t*>(lds);              // [2][64][KS]
+    uint16_t* const vs = ks + 2 * L::K_HALVES;                          // [2][HD][VS]
+
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, h2 = lane >> 5, lq = lane & 31;
+    const int half = w >> 2, wq = w & 3;
+    // block -> (unit, query block); unit -> (pair = sequence*KV + g, head subset)
+    const int units = p.pairs * p.nsub;
+    int unit, qrank;
+    if (units % 8 == 0) {
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = units >> 3;
+        unit = xcd + 8 * (slot % per);
+        qrank = slot / per;
+    } else {
+        unit = blockIdx.x % units;
+        qrank = blockIdx.x / units;
+    }
+    const int pair = unit % p.pairs, sub = unit / p.pairs;
+    const int b = pair / p.kv_heads, g = pair % p.kv_heads;
+    const int qblk = p.nq - 1 - qrank;
+    const int rows_blk = 32 * (4 / p.gsub);
+    const int h = g * (p.heads / p.kv_heads) + sub * p.gsub + wq % p.gsub;
+    const int row0 = qblk * rows_blk + (wq / p.gsub) * 32;
+    const int myq = row0 + lq;  // this lane's query row (may be >= T: computed, not stored)
     const int q_dim = p.heads * HD;
-    const int row0 = qt * 32;
-    const int myq = row0 + lq;  // this lane's query row (may be >= T on the last tile: not stored)
-    const uint16_t* kb = p.k16 + ((size_t)b * p.kv_heads + g) * (size_t)p.Tp * HD;
-    const uint16_t* vb = p.vt16 + ((size_t)b * p.kv_heads + g) * (size_t)HD * p.Tp;
+    const uint16_t* kb = p.k16 + (size_t)pair * p.Tp * HD;
+    const uint16_t* vb = p.vt16 + (size_t)pair * HD * p.Tp;
+    const int kend = min(qblk * rows_blk + rows_blk, p.T);  // keys the block needs: 0 .. kend-1
+    const int ntiles = (kend + kFlashKeys - 1) / kFlashKeys;
 
     halfx8 qf[HD / 16];  // B operand: query lq, hd (l/32)*8 + 16*kk .. +7
     {
@@ -192,90 +241,124 @@ __global__ __launch_bounds__(64) void flash_prefill_kernel(FlashParams p) {
 #pragma unroll
         for (int r = 0; r < 16; r++) o[j][r] = 0.f;
     float m = -INFINITY, l = 0.f;
-    const float scale = sqrtf((float)HD);
-    const int kend = min(row0 + 32, p.T);  // keys 0 .. last query of the tile
+    const float c2 = 1.4426950408889634f / sqrtf((float)HD);
 
-    // software pipeline: the next tile's K and this tile's V are in flight while the current
-    // tile's MFMAs and softmax run
-    halfx8 kf[HD / 16];
-    auto load_k = [&](int k0) {
-        const uint16_t* krow = kb + (size_t)min(k0 + lq, p.T - 1) * HD + h2 * 8;
+    // super-tile staging: chunk c of K is key row c/(HD/8), halves (c%(HD/8))*8; of V^T, hd row c/8,
+    // keys (c%8)*8.  Rows k0..k0+63 < Tp always (k0 < T, Tp a multiple of 64).
+    u32x4 kreg[CPT], vreg[CPT];
+#define FLASH_LOAD_TILE(k0_)                                                                                     \
+    _Pragma("unroll") for (int i = 0; i < CPT; i++) {                                                            \
+        const int c = tid + 512 * i;                                                                             \
+        kreg[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)((k0_) + c / (HD / 8)) * HD + (c % (HD / 8)) * 8); \
+        vreg[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)(c / 8) * p.Tp + (k0_) + (c % 8) * 8);             \
+    }
+#define FLASH_STORE_TILE(buf_)                                                                                   \
+    _Pragma("unroll") for (int i = 0; i < CPT; i++) {                                                            \
+        const int c = tid + 512 * i;                                                                             \
+        *reinterpret_cast<u32x4*>(ks + (buf_) * L::K_HALVES + (c / (HD / 8)) * L::KS + (c % (HD / 8)) * 8) =      \
+            kreg[i];                                                                                             \
+        uint2* vd = reinterpret_cast<uint2*>(vs + (buf_) * L::V_HALVES + (c / 8) * L::VS + (c % 8) * 8);         \
+        vd[0] = make_uint2(vreg[i].x, vreg[i].y);                                                                \
+        vd[1] = make_uint2(vreg[i].z, vreg[i].w);                                                                \
+    }
+    FLASH_LOAD_TILE(0)
+    FLASH_STORE_TILE(0)
+    __syncthreads();
+    for (int t = 0; t < ntiles; t++) {
+        const int buf = t & 1, kh = t * kFlashKeys + 32 * half;  // this wave's 32 keys: kh .. kh+31
+        if (t + 1 < ntiles) {
+            FLASH_LOAD_TILE((t + 1) * kFlashKeys)
+        }
+        if (kh <= row0 + 31 && kh < p.T) {  // else every key of the tile is masked for this wave
+            const uint16_t* kt = ks + buf * L::K_HALVES + (32 * half + lq) * L::KS + h2 * 8;
+            floatx16 s;
 #pragma unroll
-        for (int kk = 0; kk < HD / 16; kk++) kf[kk] = *reinterpret_cast<const halfx8*>(krow + kk * 16);
-    };
-    load_k(0);
-    for (int k0 = 0; k0 < kend; k0 += 32) {
-        uint2 vlo[2][NT], vhi[2][NT];
+            for (int r = 0; r < 16; r++) s[r] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++)
+            for (int kk = 0; kk < HD / 16; kk++)
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const halfx8*>(kt + kk * 16), qf[kk], s,
+                                                           0, 0, 0);
+            float mx = -INFINITY;
+            const bool edge = (kh + 31 > row0) || (kh + 31 >= p.T);
 #pragma unroll
-            for (int j = 0; j < NT; j++) {
-                const uint16_t* vrow = vb + (size_t)(j * 32 + lq) * p.Tp + k0 + 16 * kk + h2 * 4;
-                vlo[kk][j] = *reinterpret_cast<const uint2*>(vrow);
-                vhi[kk][j] = *reinterpret_cast<const uint2*>(vrow + 8);
+            for (int r = 0; r < 16; r++) {
+                float v = s[r] * c2;
+                if (edge) {
+                    const int key = kh + (r >> 2) * 8 + h2 * 4 + (r & 3);
+                    if (key > myq || key >= p.T) v = -INFINITY;
+                }
+                s[r] = v;
+                mx = fmaxf(mx, v);
             }
-        // S^T = K Q^T
-        floatx16 s;
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            if (__ballot(mx > m + 8.0f)) {
+                const float m_new = fmaxf(m, mx);
+                const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+                l *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; r++) s[r] = 0.f;
+                for (int j = 0; j < NT; j++)
 #pragma unroll
-        for (int kk = 0; kk < HD / 16; kk++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], qf[kk], s, 0, 0, 0);
-        if (k0 + 32 < kend) load_k(k0 + 32);
-        // mask + online softmax (keys past the query, or past the prompt, get weight 0)
-        float mx = -INFINITY;
+                    for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+                m = m_new;
+            }
+            // a query whose keys so far are all masked keeps m = -inf: its weights are exp2(-inf) = 0
+            const float mu = (m == -INFINITY) ? 0.f : m;
+            float sum = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int key = k0 + (r >> 2) * 8 + h2 * 4 + (r & 3);
-            float v = s[r] / scale;
-            if (key > myq || key >= p.T) v = -INFINITY;
-            s[r] = v;
-            mx = fmaxf(mx, v);
+            for (int r = 0; r < 16; r++) {
+                const float e = __builtin_amdgcn_exp2f(s[r] - mu);
+                s[r] = e;
+                sum += e;
+            }
+            l += sum + __shfl_xor(sum, 32, 64);
+            // O^T += V^T P^T over the 32 keys, in register order: k-step kk, slot i <-> register 8kk+i
+            // <-> key kh + 16kk + 8*(i/4) + (l/32)*4 + i%4
+            const uint16_t* vt0 = vs + buf * L::V_HALVES + lq * L::VS + 32 * half + h2 * 4;
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                halfx8 pf;
+#pragma unroll
+                for (int i = 0; i < 8; i++) pf[i] = (_Float16)s[8 * kk + i];
+#pragma unroll
+                for (int j = 0; j < NT; j++) {
+                    const uint16_t* vt = vt0 + j * 32 * L::VS + 16 * kk;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(vt);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(vt + 8);
+                    const halfx8 vf = __builtin_bit_cast(halfx8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[j], 0, 0, 0);
+                }
+            }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m, mx);
-        float sum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float e = (s[r] == -INFINITY) ? 0.f : expf(s[r] - m_new);
-            s[r] = e;
-            sum += e;
+        if (t + 1 < ntiles) {  // buffer buf^1 was last read before the previous barrier
+            FLASH_STORE_TILE(buf ^ 1)
         }
-        sum += __shfl_xor(sum, 32, 64);
-        const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
-        l = l * alpha + sum;
-        m = m_new;
+        __syncthreads();
+    }
+#undef FLASH_LOAD_TILE
+#undef FLASH_STORE_TILE
+    // merge the second key half into the first (the tile buffers are free after the last barrier)
+    float* mg = reinterpret_cast<float*>(lds) + wq * (HD / 2 + 2) * 64 + lane;  // [wq][value][lane]
+    if (half == 1) {
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) o[j][r] *= alpha;
-        // O^T += V^T P^T over the 32 keys, in register order: k-step kk, slot i <-> register 8kk+i
-        // <-> key k0 + 16kk + 8*(i/4) + (l/32)*4 + i%4
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            halfx8 pf;
-#pragma unroll
-            for (int i = 0; i < 8; i++) pf[i] = (_Float16)s[8 * kk + i];
-#pragma unroll
-            for (int j = 0; j < NT; j++) {
-                halfx8 vf;
-                const uint16_t* lo16 = reinterpret_cast<const uint16_t*>(&vlo[kk][j]);
-                const uint16_t* hi16 = reinterpret_cast<const uint16_t*>(&vhi[kk][j]);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    vf[i] = *reinterpret_cast<const _Float16*>(&lo16[i]);
-                    vf[i + 4] = *reinterpret_cast<const _Float16*>(&hi16[i]);
-                }
-                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[j], 0, 0, 0);
-            }
-        }
+            for (int r = 0; r < 16; r++) mg[(j * 16 + r) * 64] = o[j][r];
+        mg[(HD / 2) * 64] = m;
+        mg[(HD / 2 + 1) * 64] = l;
     }
-    if (myq >= p.T) return;
-    const float inv = 1.0f / l;
+    __syncthreads();
+    if (half == 1 || myq >= p.T) return;
+    const float m1 = mg[(HD / 2) * 64], l1 = mg[(HD / 2 + 1) * 64];
+    const float m_all = fmaxf(m, m1);  // m is finite: key 0 is in this half's first tile
+    const float a0 = __builtin_amdgcn_exp2f(m - m_all);
+    const float a1 = (m1 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m1 - m_all);
+    const float inv = 1.0f / (l * a0 + l1 * a1);
     uint16_t* orow = p.out + ((size_t)b * p.T + myq) * q_dim + (size_t)h * HD;
 #pragma unroll
     for (int j = 0; j < NT; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) orow[j * 32 + (r >> 2) * 8 + h2 * 4 + (r & 3)] = f2h(o[j][r] * inv);
+        for (int r = 0; r < 16; r++)
+            orow[j * 32 + (r >> 2) * 8 + h2 * 4 + (r & 3)] = f2h((o[j][r] * a0 + mg[(j * 16 + r) * 64] * a1) * inv);
 }
 
 }  // namespace
@@ -320,14 +403,21 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
 int launch_flash_prefill(const uint16_t* qb, const uint16_t* k16, const uint16_t* vt16, uint16_t* out, int B, int T,
                          int Tp, int heads, int kv_heads, int hd, hipStream_t stream) {
     AR_CHECK_ARG(qb && k16 && vt16 && out && T > 0 && B > 0, "flash prefill: bad arguments");
-    AR_CHECK_ARG(heads % kv_heads == 0 && Tp >= T && Tp % 32 == 0, "flash prefill: bad shape");
+    AR_CHECK_ARG(heads % kv_heads == 0 && Tp >= T && Tp % kFlashKeys == 0, "flash prefill: bad shape");
     FlashParams p;
     p.qb = qb; p.k16 = k16; p.vt16 = vt16; p.out = out; p.T = T; p.Tp = Tp; p.heads = heads; p.kv_heads = kv_heads;
-    dim3 grid((T + 31) / 32, heads, B);
+    const int G = heads / kv_heads;
+    p.gsub = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+    p.nsub = G / p.gsub;
+    p.pairs = B * kv_heads;
+    p.nq = (T + 32 * (4 / p.gsub) - 1) / (32 * (4 / p.gsub));
+    const long long blocks = (long long)p.nq * p.pairs * p.nsub;
+    AR_CHECK_ARG(blocks <= 0x7fffffff, "flash prefill: too many blocks");
+    dim3 grid((unsigned)blocks);
     if (hd == 128)
-        hipLaunchKernelGGL(flash_prefill_kernel<128>, grid, dim3(64), 0, stream, p);
+        hipLaunchKernelGGL(flash_prefill_kernel<128>, grid, dim3(512), 0, stream, p);
     else if (hd == 64)
-        hipLaunchKernelGGL(flash_prefill_kernel<64>, grid, dim3(64), 0, stream, p);
+        hipLaunchKernelGGL(flash_prefill_kernel<64>, grid, dim3(512), 0, stream, p);
     else {
         ar_set_error("flash prefill: head_dim %d not supported", hd);
         return AR_HIP_ERR_INVALID;
