@@ -11,9 +11,11 @@ Extra fields on the JSON line:
   roofline      dominant kernel's achieved HBM GB/s, from HIP events bracketing every launch
                 of that kernel class on the model's stream over a probe pass of --probe-steps
   cpu_baseline  the CPU oracle (reference semantics, fp32) on this host, over a bounded sample
-  prefill       BASELINE config 4 (Qwen3-1.7B shape, bf16 weights): a 2048-token prompt through the
+  c4            BASELINE config 4 (Qwen3-1.7B shape, bf16 weights): a 2048-token prompt through the
                 MFMA prefill path (tok/s and fraction of the 2.5 PFLOP/s dense bf16/fp16 MFMA peak),
                 then greedy decode tok/s and HBM fraction on the same model
+  c5            BASELINE config 5 (Qwen3-4B shape, bf16 weights): 8 sequences x 8192-token prompts
+                prefilled together, then 64 greedy steps of all 8 (aggregate tok/s, HBM fraction)
 """
 from __future__ import annotations
 
@@ -128,6 +130,72 @@ def c4_section(args):
     return out
 
 
+def c5_section(args):
+    """8 independent sequences, each an 8192-token prompt through the MFMA
+    prefill path, then greedy decode of all 8 together (long-context GQA decode)."""
+    import dataclasses
+
+    import numpy as np
+
+    from common_amd import config as C
+    from common_amd import synthetic
+    from common_amd.qwen3 import Qwen3
+
+    B, T, n_dec = C.C5_BATCH, C.C5_PROMPT, C.C5_DECODE
+    cfg = dataclasses.replace(C.C5_4B, seq_len=T + n_dec + 8, max_batch=B)
+    prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=args.seed + 500 + b) for b in range(B)]
+    t0 = time.time()
+    model = Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed + 5))
+    log(f"[bench] C5 weights generated + uploaded in {time.time() - t0:.1f}s")
+    am = model.model
+
+    def start():
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        model.ctx.synchronize()
+
+    start()
+    am.prefill()  # first call makes the fp16 weight copies and the prefill buffers
+    start()
+    tp = time.perf_counter()
+    am.prefill()
+    t_pre = time.perf_counter() - tp
+    flops = B * prefill_flops(cfg, T)
+    warm = 4
+    am.run(warm)
+    model.ctx.synchronize()
+    td = time.perf_counter()
+    toks = am.run(n_dec - warm)
+    t_dec = time.perf_counter() - td
+    model.close()
+    steps = n_dec - warm
+    step_bytes = float(np.mean([step_bytes_batch(cfg, p, B) for p in range(T + warm, T + n_dec)]))
+    out = {
+        "workload": "C5: Qwen3-4B shape bf16 weights (d2560, 36L, 32Q/8KV, hd128, F9728, V151936), "
+                    f"batch {B} x {T}-token prompts, greedy decode {n_dec}",
+        "prefill": {"tokens": B * T, "ms": round(1000 * t_pre, 2), "tok_s": round(B * T / t_pre, 1),
+                    "tflop": round(flops / 1e12, 2), "achieved_tflops": round(flops / t_pre / 1e12, 1),
+                    "mfma_frac": round(flops / t_pre / 1e12 / MFMA_PEAK_TFLOPS, 4)},
+        "decode": {"steps": steps, "tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(1000 * t_dec / steps, 3),
+                   "algorithmic_bytes_per_step": round(step_bytes),
+                   "hbm_frac": round(step_bytes * steps / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+                   "kv_cache": "fp32"},
+        "distinct_sequences": int(len({tuple(t) for t in toks})),
+    }
+    log(f"[bench] C5 prefill {B}x{T} tokens: {1000 * t_pre:.1f} ms = {B * T / t_pre:.0f} tok/s, "
+        f"{flops / t_pre / 1e12:.0f} TFLOP/s; decode {out['decode']['tok_s']} tok/s aggregate, "
+        f"{out['decode']['ms_per_step']} ms/step ({100 * out['decode']['hbm_frac']:.1f}% of HBM)")
+    return out
+
+
+def step_bytes_batch(cfg, pos, batch):
+    """Bytes one batched decode step must move at position `pos`: weights once, KV per sequence."""
+    one = algorithmic_bytes_per_token(cfg, pos)
+    kv = cfg.layer_count * 2 * cfg.kv_dim * 4 * (pos + 1)
+    return one + (batch - 1) * (kv + cfg.dim * 4)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +206,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 prefill/decode section")
+    ap.add_argument("--no-c5", action="store_true", help="skip the config-5 batch-8 long-context section")
     ap.add_argument("--prefetch", type=int, default=0,
                     help="blocks of the Infinity-Cache weight prefetch branch (0 disables)")
     args = ap.parse_args()
@@ -270,6 +339,7 @@ def main():
         "prompt_c3": {"tok_s": round(n_prompt / prefill_s, 1), "tokens": n_prompt,
                       "path": "fp32 weights: token by token through the decode step (reference semantics)"},
         "c4": c4_section(args) if not args.no_c4 else None,
+        "c5": c5_section(args) if not args.no_c5 else None,
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,

@@ -22,6 +22,7 @@
 // for the heads/kv_heads query heads sharing KV head g:
 //   phase 1: 16-lane groups compute one row's scores for all heads of the group (K row read once)
 //   phase 2: each wavefront accumulates a[t] * V[t] for every fourth row (V row read once)
+// Both phases walk the split in passes of 64 rows with the next pass's loads in flight.
 // With one split the block writes the normalised output; otherwise it writes unnormalised
 // partials (o, max, sum) that attn_combine_kernel merges in the next launch (the kernel boundary
 // makes them visible, so no block needs a device-wide fence).
@@ -179,31 +180,31 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     // cache until this block writes it, so that row is taken from LDS instead.
     float kr[KU][EPL];
     float vr[VU][VPL];
-    auto load_k = [&](int base) {
+    auto load_k = [&](float (&dst)[KU][EPL], int base) {
 #pragma unroll
         for (int u = 0; u < KU; u++) {
             const int t = min(base + grp + 16 * u, t1 - 1);
 #pragma unroll
             for (int j = 0; j < EPL / 4; j++) {
                 const float4 v = *reinterpret_cast<const float4*>(kc + (size_t)t * HD + j * 64 + gl * 4);
-                kr[u][j * 4] = v.x; kr[u][j * 4 + 1] = v.y; kr[u][j * 4 + 2] = v.z; kr[u][j * 4 + 3] = v.w;
+                dst[u][j * 4] = v.x; dst[u][j * 4 + 1] = v.y; dst[u][j * 4 + 2] = v.z; dst[u][j * 4 + 3] = v.w;
             }
         }
     };
-    auto load_v = [&](int base) {
+    auto load_v = [&](float (&dst)[VU][VPL], int base) {
 #pragma unroll
         for (int u = 0; u < VU; u++) {
             const int t = min(base + wave + 4 * u, t1 - 1);
             if constexpr (VPL == 2) {
                 const float2 v = *reinterpret_cast<const float2*>(vc + (size_t)t * HD + lane * 2);
-                vr[u][0] = v.x; vr[u][1] = v.y;
+                dst[u][0] = v.x; dst[u][1] = v.y;
             } else {
-                vr[u][0] = vc[(size_t)t * HD + lane];
+                dst[u][0] = vc[(size_t)t * HD + lane];
             }
         }
     };
-    load_k(t0);
-    load_v(t0);
+    load_k(kr, t0);
+    load_v(vr, t0);
     const float2* rope_row = p.rope_tab ? p.rope_tab + (size_t)pos * FD : nullptr;
     float2 qcs[QPT], kcs;
 #pragma unroll
@@ -288,7 +289,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
             }
         const float scale = sqrtf((float)HD);
         for (int base = t0; base < t1; base += PASS) {
-            if (base != t0) load_k(base);
+            // the next pass's rows are in flight while this pass is scored
+            float kn[KU][EPL];
+            const bool more = base + PASS < t1;
+            if (more) load_k(kn, base + PASS);
 #pragma unroll
             for (int u = 0; u < KU; u++) {
                 const int t = base + grp + 16 * u;
@@ -309,6 +313,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
                     if (gl == 0 && t < t1) s_s[g][t - t0] = d / scale;
                 }
             }
+            if (more)
+#pragma unroll
+                for (int u = 0; u < KU; u++)
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) kr[u][e] = kn[u][e];
         }
     }
     __syncthreads();
@@ -338,7 +347,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
 #pragma unroll
             for (int j = 0; j < VPL; j++) acc[g][j] = 0.f;
         for (int base = t0; base < t1; base += PASS) {
-            if (base != t0) load_v(base);
+            float vn[VU][VPL];
+            const bool more = base + PASS < t1;
+            if (more) load_v(vn, base + PASS);
 #pragma unroll
             for (int u = 0; u < VU; u++) {
                 const int t = base + wave + 4 * u;
@@ -355,6 +366,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
                     }
                 }
             }
+            if (more)
+#pragma unroll
+                for (int u = 0; u < VU; u++)
+#pragma unroll
+                    for (int j = 0; j < VPL; j++) vr[u][j] = vn[u][j];
         }
 #pragma unroll
         for (int g = 0; g < G; g++)

@@ -23,6 +23,9 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
     p.w = a.w; p.w2 = a.w2; p.rows = a.rows; p.cols = a.cols; p.batch = a.batch;
     p.x = a.x; p.x_stride = a.x_stride; p.norm_w = a.norm_w; p.eps = a.eps; p.bias = a.bias;
     p.y = a.y; p.y_stride = a.y_stride; p.keys = a.keys;
+    if (a.batch >= 3 && a.wdtype == AR_DTYPE_BF16 && a.cols % 32 == 0)
+        return gemv_launch_mfma(p, a.epilogue, stream);
+    if (a.batch >= 3) return gemv_launch_batched(p, a.wdtype, a.epilogue, stream);
     const gemv::Shape s = gemv::shape_for(a.rows, a.cols, a.batch, a.wdtype, a.epilogue);
     if (a.wdtype == AR_DTYPE_F32) return gemv_launch_f32(p, a.epilogue, s, stream);
     return gemv_launch_bf16(p, a.epilogue, s, stream);

@@ -447,3 +447,7 @@ int dispatch_epi(const Params& p, int epi, const Shape& s, hipStream_t st) {
 // per-dtype entry points (gemv_f32.hip, gemv_bf16.hip)
 int gemv_launch_f32(const gemv::Params& p, int epi, const gemv::Shape& s, hipStream_t st);
 int gemv_launch_bf16(const gemv::Params& p, int epi, const gemv::Shape& s, hipStream_t st);
+// Batches of 3..8 sequences (gemv_batched.hip): input slices held in registers, 64/NB rows per block.
+int gemv_launch_batched(const gemv::Params& p, int wdtype, int epi, hipStream_t st);
+// bf16 weights, batches of 3..16, cols % 32 == 0 (gemv_mfma.hip): 16-row tiles on the MFMA units.
+int gemv_launch_mfma(const gemv::Params& p, int epi, hipStream_t st);

@@ -28,9 +28,12 @@ def _rng(seed):
     (1024, 2048, 1, False, False, False),
     (1024, 3072, 1, False, False, True),
     (300, 2048, 3, True, False, False),
+    (1001, 1024, 5, True, True, False),
+    (2560, 9728, 8, False, False, True),
     (17, 9728, 8, False, True, True),
     (8200, 2560, 8, True, False, True),
     (20000, 1024, 1, True, False, False),
+    (20000, 1024, 6, True, False, True),
 ])
 def test_dense(ctx, rows, cols, batch, norm, bias, bf16):
     r = _rng(rows * 7 + cols)
@@ -57,7 +60,8 @@ def test_dense(ctx, rows, cols, batch, norm, bias, bf16):
 
 
 @pytest.mark.parametrize("rows,cols,batch,bf16", [(768, 256, 1, False), (3072, 1024, 1, False),
-                                                  (6144, 2048, 2, True), (9728, 2560, 8, True)])
+                                                  (6144, 2048, 2, True), (9728, 2560, 8, True),
+                                                  (3000, 1024, 4, False)])
 def test_swiglu(ctx, rows, cols, batch, bf16):
     r = _rng(rows + cols)
     Wg = (r.standard_normal((rows, cols)) * 0.02).astype(np.float32)

@@ -147,3 +147,53 @@ def test_prefill_c4_shape_matches_sequential_decode(ctx):
     top = np.sort(ls[0])[-2:]
     if (top[1] - top[0]) / abs(top[1]) > BF16_TOL:
         assert after_prefill[0, 0] == after_seq[0, 0]
+
+
+def test_prefill_gqa4_batch8_matches_oracle(ctx):
+    """The C5 structure at small size: 4 query heads per KV head, q_dim != dim, batch 8, ragged prompt."""
+    cfg = _bf16_cfg(C.C1_TINY, head_count=8, kv_head_count=2, head_size=64, seq_len=140, max_batch=8)
+    assert cfg.q_dim != cfg.dim
+    sd = synthetic.state_dict(cfg, seed=7)
+    T, steps = 100, 4
+    prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=40 + b) for b in range(8)]
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        lp = am.prefill(return_logits=True)
+        after_prefill = am.run(steps)
+    for b, p in enumerate(prompts):
+        rf, rl = oracle.OracleQwen3(cfg, sd, precision="fp64").generate(p, steps)
+        assert rel_err(lp[b], rl[T - 1]) <= BF16_TOL, b
+        for s in range(steps):
+            top = np.sort(rl[T - 1 + s])[-2:]
+            if (top[1] - top[0]) / abs(top[1]) < BF16_TOL:
+                break
+            assert after_prefill[b, s] == rf[T + s], (b, s)
+
+
+def test_prefill_c5_shape_batch8_matches_sequential_decode(ctx):
+    """Qwen3-4B layer shape (d2560, 32Q/8KV, hd128, F9728), batch 8, two layers
+    and a 512-token context: batched prefill vs the decode step fed one token at a time."""
+    T = 512
+    cfg = dataclasses.replace(C.C5_4B, layer_count=2, seq_len=T + 8, max_batch=8)
+    prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=50 + b) for b in range(8)]
+    with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=5), ctx) as m:
+        am = m.model
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        lp = am.prefill(return_logits=True)
+        after_prefill = am.run(2)
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        am.run(T - 1)
+        _, ls = am.next(return_logits=True)
+        after_seq = am.run(2)
+    for b in range(8):
+        assert rel_err(lp[b], ls[b]) <= BF16_TOL, b
+        top = np.sort(ls[b])[-2:]
+        if (top[1] - top[0]) / abs(top[1]) > BF16_TOL:
+            assert after_prefill[b, 0] == after_seq[b, 0], b
