@@ -30,8 +30,9 @@
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kMaxTile = 256;
+constexpr int kThreads = 256;   // threads of the split (multi-block) form
+constexpr int kMaxTile = 256;   // rows per split in that form
+constexpr int kShortMax = 256;  // caches up to this many rows: one block per (sequence, KV head)
 constexpr int kMaxSplits = 1024;
 
 struct AttnParams {
@@ -68,6 +69,7 @@ __device__ inline float wave_max(float v) {
 }
 
 // Block-wide sum of per-thread values; every thread gets the result.
+template <int NT>
 __device__ inline float block_sum(float v, float* scratch) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     v = wave_sum(v);
@@ -76,7 +78,7 @@ __device__ inline float block_sum(float v, float* scratch) {
     __syncthreads();
     float t = 0.f;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; w++) t += scratch[w];
+    for (int w = 0; w < NT / 64; w++) t += scratch[w];
     return t;
 }
 
@@ -104,21 +106,26 @@ __device__ inline void rope_cs(const float2* row, int pos, int f, double c, floa
     *sn = (float)sin(ang);
 }
 
-template <int HD, int G>
-__global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
+// NT threads: 256 when the context is cut into splits across blocks, 512 / 1024 for a context of
+// at most kShortMax rows handled by one block per (sequence, KV head) with no combine launch.
+template <int HD, int G, int NT>
+__global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     constexpr int FD = HD / 2;
     constexpr int EPL = HD / 16;     // elements per lane in a 16-lane row group (phase 1)
     constexpr int VPL = HD / 64;     // value columns per lane (phase 2)
-    constexpr int KU = 4;            // K rows per 16-lane group per pass  (16 groups -> 64 rows)
-    constexpr int VU = 16;           // V rows per wavefront per pass      (4 waves   -> 64 rows)
-    constexpr int PASS = 64;
+    constexpr int NG = NT / 16;                // 16-lane row groups (phase 1)
+    constexpr int NWV = NT / 64;               // wavefronts (phase 2)
+    constexpr int KU = NT == 1024 ? 2 : 4;     // K rows per group per pass
+    constexpr int VU = NT == 1024 ? 8 : 16;    // V rows per wavefront per pass
+    constexpr int PASS1 = NG * KU, PASS2 = NWV * VU;
+    constexpr int TILE = NT == 256 ? kMaxTile : kShortMax;
     __shared__ __attribute__((aligned(16))) float q_s[G][HD];
     __shared__ __attribute__((aligned(16))) float k_new[HD];
     __shared__ __attribute__((aligned(16))) float v_new[HD];
-    __shared__ float s_s[G][kMaxTile];
-    __shared__ __attribute__((aligned(16))) float red_s[kThreads / 64][G][HD];
+    __shared__ float s_s[G][TILE];
+    __shared__ __attribute__((aligned(16))) float red_s[NWV][G][HD];
     __shared__ float m_s[G], l_s[G];
-    __shared__ float scratch[kThreads / 64];
+    __shared__ float scratch[NWV];
     __shared__ float rq_s[G], rk_s;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -133,11 +140,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
 
     // ---- every load that does not depend on the position, issued together with it ----------
     const int pos = *p.pos;
-    constexpr int QPT = (G * FD + kThreads - 1) / kThreads;  // query (f, f+hd/2) pairs per thread
+    constexpr int QPT = (G * FD + NT - 1) / NT;  // query (f, f+hd/2) pairs per thread
     float qx1[QPT], qx2[QPT], qg1[QPT], qg2[QPT];
 #pragma unroll
     for (int j = 0; j < QPT; j++) {
-        const int idx = min(tid + j * kThreads, G * FD - 1);
+        const int idx = min(tid + j * NT, G * FD - 1);
         const int g = idx / FD, f = idx - g * FD;
         const size_t off = (size_t)(kvh * G + g) * HD + f;
         qx1[j] = q_raw[off];
@@ -153,12 +160,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     float sq = 0.f, sk = 0.f;  // this thread's share of sum(q^2), sum(k^2) over the whole vectors
     if (whole_norm) {
 #pragma unroll 4
-        for (int i = tid * 4; i < q_dim; i += kThreads * 4) {
+        for (int i = tid * 4; i < q_dim; i += NT * 4) {
             const float4 v = *reinterpret_cast<const float4*>(q_raw + i);
             sq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
 #pragma unroll 2
-        for (int i = tid * 4; i < kv_dim; i += kThreads * 4) {
+        for (int i = tid * 4; i < kv_dim; i += NT * 4) {
             const float4 v = *reinterpret_cast<const float4*>(k_raw + i);
             sk += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
@@ -183,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     auto load_k = [&](float (&dst)[KU][EPL], int base) {
 #pragma unroll
         for (int u = 0; u < KU; u++) {
-            const int t = min(base + grp + 16 * u, t1 - 1);
+            const int t = min(base + grp + NG * u, t1 - 1);
 #pragma unroll
             for (int j = 0; j < EPL / 4; j++) {
                 const float4 v = *reinterpret_cast<const float4*>(kc + (size_t)t * HD + j * 64 + gl * 4);
@@ -194,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     auto load_v = [&](float (&dst)[VU][VPL], int base) {
 #pragma unroll
         for (int u = 0; u < VU; u++) {
-            const int t = min(base + wave + 4 * u, t1 - 1);
+            const int t = min(base + wave + NWV * u, t1 - 1);
             if constexpr (VPL == 2) {
                 const float2 v = *reinterpret_cast<const float2*>(vc + (size_t)t * HD + lane * 2);
                 dst[u][0] = v.x; dst[u][1] = v.y;
@@ -209,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     float2 qcs[QPT], kcs;
 #pragma unroll
     for (int j = 0; j < QPT; j++) {
-        const int idx = min(tid + j * kThreads, G * FD - 1);
+        const int idx = min(tid + j * NT, G * FD - 1);
         rope_cs(rope_row, pos, idx % FD, p.rope_c, &qcs[j].x, &qcs[j].y);
     }
     rope_cs(rope_row, pos, kf, p.rope_c, &kcs.x, &kcs.y);
@@ -217,8 +224,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     // ---- QK-norm factors ----------------------------------------------------------
     if (p.q_norm || p.k_norm) {
         if (whole_norm) {
-            sq = block_sum(sq, scratch);
-            sk = block_sum(sk, scratch);
+            sq = block_sum<NT>(sq, scratch);
+            sk = block_sum<NT>(sk, scratch);
             if (tid == 0) {
                 const float rq = 1.0f / sqrtf(sq / (float)q_dim + p.qk_eps);
                 for (int g = 0; g < G; g++) rq_s[g] = rq;
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
             }
         } else {
             // wave w reduces heads w, w+4, ...; the k head goes to the last slot
-            for (int j = wave; j < G + 1; j += kThreads / 64) {
+            for (int j = wave; j < G + 1; j += NWV) {
                 const float* src = (j < G) ? q_raw + (size_t)(kvh * G + j) * HD : k_raw + (size_t)kvh * HD;
                 float s = 0.f;
                 for (int i = lane; i < HD; i += 64) s += src[i] * src[i];
@@ -243,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     // ---- normalised, rotated queries of this group -> LDS ---------------------------
 #pragma unroll
     for (int j = 0; j < QPT; j++) {
-        const int idx = tid + j * kThreads;
+        const int idx = tid + j * NT;
         if (idx < G * FD) {
             const int g = idx / FD, f = idx - g * FD;
             float x1 = qx1[j], x2 = qx2[j];
@@ -288,14 +295,14 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
                 qr[g][j * 4] = t.x; qr[g][j * 4 + 1] = t.y; qr[g][j * 4 + 2] = t.z; qr[g][j * 4 + 3] = t.w;
             }
         const float scale = sqrtf((float)HD);
-        for (int base = t0; base < t1; base += PASS) {
+        for (int base = t0; base < t1; base += PASS1) {
             // the next pass's rows are in flight while this pass is scored
             float kn[KU][EPL];
-            const bool more = base + PASS < t1;
-            if (more) load_k(kn, base + PASS);
+            const bool more = base + PASS1 < t1;
+            if (more) load_k(kn, base + PASS1);
 #pragma unroll
             for (int u = 0; u < KU; u++) {
-                const int t = base + grp + 16 * u;
+                const int t = base + grp + NG * u;
                 if (has_pos && t == pos) {
 #pragma unroll
                     for (int j = 0; j < EPL / 4; j++) {
@@ -324,7 +331,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
 
     // ---- split-local softmax statistics --------------------------------------------
     const int len = t1 - t0;
-    for (int g = wave; g < G; g += kThreads / 64) {
+    for (int g = wave; g < G; g += NWV) {
         float m = -INFINITY;
         for (int i = lane; i < len; i += 64) m = fmaxf(m, s_s[g][i]);
         m = wave_max(m);
@@ -346,13 +353,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
         for (int g = 0; g < G; g++)
 #pragma unroll
             for (int j = 0; j < VPL; j++) acc[g][j] = 0.f;
-        for (int base = t0; base < t1; base += PASS) {
+        for (int base = t0; base < t1; base += PASS2) {
             float vn[VU][VPL];
-            const bool more = base + PASS < t1;
-            if (more) load_v(vn, base + PASS);
+            const bool more = base + PASS2 < t1;
+            if (more) load_v(vn, base + PASS2);
 #pragma unroll
             for (int u = 0; u < VU; u++) {
-                const int t = base + wave + 4 * u;
+                const int t = base + wave + NWV * u;
                 if (t < t1) {
                     if (has_pos && t == pos) {
 #pragma unroll
@@ -380,11 +387,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnParams p) {
     __syncthreads();
 
     const int hbase = kvh * G;
-    for (int idx = tid; idx < G * HD; idx += kThreads) {
+    for (int idx = tid; idx < G * HD; idx += NT) {
         const int g = idx / HD, i = idx - g * HD;
         float o = 0.f;
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; w++) o += red_s[w][g][i];
+        for (int w = 0; w < NWV; w++) o += red_s[w][g][i];
         if (nsplit == 1) {
             p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = o / l_s[g];
         } else {
@@ -461,8 +468,15 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
     p.rope_tab = a.rope_tab;
     p.max_splits = a.max_splits; p.part_o = a.part_o; p.part_ml = a.part_ml;
     p.out = a.out; p.out_stride = a.out_stride;
-    hipLaunchKernelGGL((attn_decode_kernel<HD, G>), dim3(a.max_splits, a.kv_heads, a.batch), dim3(kThreads), 0,
-                       stream, p);
+    if (a.max_splits == 1 && a.max_seq <= kShortMax) {
+        // whole context in one block: 1024 threads (512 when 8 query heads share a KV head, for registers)
+        constexpr int NT = G <= 4 ? 1024 : 512;
+        hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT>), dim3(1, a.kv_heads, a.batch), dim3(NT), 0, stream, p);
+        AR_LAUNCH_CHECK();
+        return AR_HIP_OK;
+    }
+    hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads>), dim3(a.max_splits, a.kv_heads, a.batch),
+                       dim3(kThreads), 0, stream, p);
     AR_LAUNCH_CHECK();
     if (a.max_splits > 1) {
         hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.heads, a.batch), dim3(HD), 0, stream, p);
@@ -490,6 +504,7 @@ size_t attention_partial_floats(int batch, int heads, int max_splits, int hd) {
 }
 
 int attention_max_splits(int max_seq, int kv_heads, int batch) {
+    if (max_seq <= kShortMax) return 1;  // one block per (sequence, KV head), no combine launch
     const int need = (max_seq + kMaxTile - 1) / kMaxTile;      // rows per split <= kMaxTile
     const int want = (1024 + kv_heads * batch - 1) / (kv_heads * batch);  // ~4 blocks per CU
     const int cap = (max_seq + 15) / 16;                       // splits of >= 16 rows
@@ -503,7 +518,8 @@ int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(a.heads > 0 && a.kv_heads > 0 && a.heads % a.kv_heads == 0, "attention: bad head counts %d/%d",
                  a.heads, a.kv_heads);
     AR_CHECK_ARG(a.max_splits <= kMaxSplits, "attention: %d splits exceed %d", a.max_splits, kMaxSplits);
-    AR_CHECK_ARG(a.max_splits >= 1 && (long long)a.max_splits * kMaxTile >= a.max_seq,
+    AR_CHECK_ARG(a.max_splits >= 1 && ((long long)a.max_splits * kMaxTile >= a.max_seq ||
+                                       (a.max_splits == 1 && a.max_seq <= kShortMax)),
                  "attention: %d splits of at most %d rows do not cover %d rows", a.max_splits, kMaxTile, a.max_seq);
     AR_CHECK_ARG(a.max_splits == 1 || (a.part_o && a.part_ml), "attention: missing split buffers");
     AR_CHECK_ARG(a.batch >= 1 && a.batch <= 65535, "attention: bad batch %d", a.batch);
