@@ -16,6 +16,7 @@ Extra fields on the JSON line:
                 then greedy decode tok/s and HBM fraction on the same model
   c5            BASELINE config 5 (Qwen3-4B shape, bf16 weights): 8 sequences x 8192-token prompts
                 prefilled together, then 64 greedy steps of all 8 (aggregate tok/s, HBM fraction)
+  c2            BASELINE config 2: the decode-step attention op at a 4096-row cache (us per call)
 """
 from __future__ import annotations
 
@@ -92,6 +93,7 @@ def c4_section(args):
     model = Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed + 4))
     log(f"[bench] C4 weights generated + uploaded in {time.time() - t0:.1f}s")
     am = model.model
+    am.use_graph(not args.no_graph)
     am.reset()
     am.set_prompt(prompt)
     am.prefill()  # first call makes the fp16 weight copies and the prefill buffers
@@ -148,6 +150,7 @@ def c5_section(args):
     model = Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed + 5))
     log(f"[bench] C5 weights generated + uploaded in {time.time() - t0:.1f}s")
     am = model.model
+    am.use_graph(not args.no_graph)
 
     def start():
         am.reset()
@@ -189,6 +192,88 @@ def c5_section(args):
     return out
 
 
+def c2_section(args):
+    """the decode-step GQA attention op (16 Q / 8 KV heads, hd 128, cache filled
+    to 4096 rows, query at position 4096) through ar_hip_attention_decode.  Eight caches are used in
+    turn (8 x 33.6 MB > the 256 MB Infinity Cache) so every call streams its cache from HBM."""
+    import numpy as np
+
+    from common_amd import hardware as hw
+
+    H, KV, HD, pos = 16, 8, 128, 4096
+    S = pos + 1
+    ncache, calls = 8, 200
+    r = np.random.default_rng(args.seed + 2)
+    with hw.HipContext() as ctx:
+        caches = []
+        for i in range(ncache):
+            kc = r.standard_normal(KV * S * HD, dtype=np.float32)
+            vc = r.standard_normal(KV * S * HD, dtype=np.float32)
+            caches.append((ctx.to_device(kc), ctx.to_device(vc)))
+        q = ctx.to_device(r.standard_normal(H * HD, dtype=np.float32))
+        k = ctx.to_device(r.standard_normal(KV * HD, dtype=np.float32))
+        v = ctx.to_device(r.standard_normal(KV * HD, dtype=np.float32))
+        qn = ctx.to_device((1 + 0.02 * r.standard_normal(H * HD)).astype(np.float32))
+        kn = ctx.to_device((1 + 0.02 * r.standard_normal(KV * HD)).astype(np.float32))
+        out = ctx.allocate(H * HD * 4)
+
+        def call(i):
+            kc, vc = caches[i % ncache]
+            ctx.attention_decode(q, k, v, qn, kn, 1e-6, 0, kc, vc, S, pos, H, KV, HD, 1e6, out)
+
+        for i in range(2 * ncache):
+            call(i)
+        ctx.synchronize()
+        t = time.perf_counter()
+        for i in range(calls):
+            call(i)
+        ctx.synchronize()
+        us = 1e6 * (time.perf_counter() - t) / calls
+    kv_bytes = 2 * KV * S * HD * 4
+    gbs = kv_bytes / us / 1e3
+    log(f"[bench] C2 attention op: {us:.2f} us/call, {gbs:.0f} GB/s of K/V ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+    return {"workload": "C2: decode-step GQA attention op, 16Q/8KV heads, hd 128, cache 0..4095 + new row at 4096, fp32",
+            "us_per_call": round(us, 2), "kv_bytes": kv_bytes, "GBs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "note": "wall time per C-ABI call, including the op's q/k/v staging copies and position upload"}
+
+
+def traffic_probe(args):
+    """Workload for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic: one plain
+    256 MiB device copy (the counter scale: known bytes), then a few eager C3 decode steps, so every
+    launch of the logits GEMV is its own dispatch."""
+    from common_amd import config as C
+    from common_amd import hardware as hw
+    from common_amd import synthetic
+    from common_amd.qwen3 import Qwen3
+
+    nbytes = 256 << 20
+    cfg = C.C3_0_6B
+    prompt = synthetic.prompt_ids(4, cfg.vocab_size, seed=args.seed)
+    with hw.HipContext() as ctx:
+        a, b = ctx.allocate(nbytes), ctx.allocate(nbytes)
+        ctx.copy(b, a, nbytes)
+        ctx.synchronize()
+        with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed), ctx) as model:
+            am = model.model
+            am.use_graph(False)
+            am.reset()
+            am.set_prompt(prompt)
+            am.run(8)
+            ctx.synchronize()
+    print(json.dumps({"traffic_probe": {"copy_bytes": nbytes, "decode_steps": 8}}), flush=True)
+
+
+def load_traffic():
+    """roofline.traffic from the committed rocprofv3 counter summary, when present."""
+    path = os.path.join(ROOT, "profiles", "logits_gemv_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def step_bytes_batch(cfg, pos, batch):
     """Bytes one batched decode step must move at position `pos`: weights once, KV per sequence."""
     one = algorithmic_bytes_per_token(cfg, pos)
@@ -207,6 +292,11 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 prefill/decode section")
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 batch-8 long-context section")
+    ap.add_argument("--no-c2", action="store_true", help="skip the config-2 attention-op section")
+    ap.add_argument("--sections", default="c3,c4,c5,c2",
+                    help="comma list of workloads to run (c3 is the headline; the others are extra fields)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the workload of the rocprofv3 FETCH_SIZE / WRITE_SIZE passes and exit")
     ap.add_argument("--prefetch", type=int, default=0,
                     help="blocks of the Infinity-Cache weight prefetch branch (0 disables)")
     args = ap.parse_args()
@@ -214,6 +304,16 @@ def main():
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the path has no "
               f"collectives. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.traffic_probe:
+        traffic_probe(args)
+        return
+    sections = {x.strip() for x in args.sections.split(",") if x.strip()}
+    if "c3" not in sections:  # profiling aid: only the named extra sections, one JSON line of them
+        out = {"c4": c4_section(args) if "c4" in sections and not args.no_c4 else None,
+               "c5": c5_section(args) if "c5" in sections and not args.no_c5 else None,
+               "c2": c2_section(args) if "c2" in sections and not args.no_c2 else None}
+        print(json.dumps(out), flush=True)
+        return
 
     import numpy as np
 
@@ -288,8 +388,11 @@ def main():
     roofline = None
     if dom:
         kd = kernels[dom]
+        tr = load_traffic()
         roofline = {"bound": "hbm", "kernel": dom, "achieved": kd["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                    "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4),
+                    "traffic": tr.get("hbm_bytes_per_launch") if tr else None,
+                    "traffic_source": "profiles/logits_gemv_traffic.md" if tr else None,
                     "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": kd["avg_us"]}
     model.close()
 
@@ -338,8 +441,9 @@ def main():
                 "frac_of_peak": round(e2e_gbs / HBM_PEAK_GBS, 4)},
         "prompt_c3": {"tok_s": round(n_prompt / prefill_s, 1), "tokens": n_prompt,
                       "path": "fp32 weights: token by token through the decode step (reference semantics)"},
-        "c4": c4_section(args) if not args.no_c4 else None,
-        "c5": c5_section(args) if not args.no_c5 else None,
+        "c4": c4_section(args) if "c4" in sections and not args.no_c4 else None,
+        "c5": c5_section(args) if "c5" in sections and not args.no_c5 else None,
+        "c2": c2_section(args) if "c2" in sections and not args.no_c2 else None,
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,

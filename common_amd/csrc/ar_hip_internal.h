@@ -146,7 +146,10 @@ int launch_flash_prefill(const uint16_t* qb, const uint16_t* k16, const uint16_t
                          int Tp, int heads, int kv_heads, int hd, hipStream_t stream);
 
 struct AttnLaunch {
-    const float* qkv = nullptr;   // [batch][qkv_stride]: q | k | v raw projections
+    const float* qkv = nullptr;   // [batch][qkv_stride]: q | k | v raw projections, or null:
+    const float* q = nullptr;     //   separate q, k, v rows (same stride)
+    const float* k = nullptr;
+    const float* v = nullptr;
     int qkv_stride = 0;
     const float* q_norm = nullptr;
     const float* k_norm = nullptr;
@@ -155,7 +158,8 @@ struct AttnLaunch {
     float* kcache = nullptr;      // [batch][kv_heads][max_seq][hd]
     float* vcache = nullptr;
     int max_seq = 0;
-    const int* pos = nullptr;     // device position (same for every sequence)
+    const int* pos = nullptr;     // device position (same for every sequence), or null: pos_value
+    int pos_value = 0;
     int heads = 0, kv_heads = 0, head_dim = 0;
     double rope_theta = 1e6;
     const float2* rope_tab = nullptr;  // [max_seq][hd/2] (cos, sin) of pos*invf, or null: computed
@@ -171,7 +175,8 @@ struct AttnLaunch {
 // Attention partials + (when the context is split) the combine kernel.
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);
-// Splits for a cache of max_seq rows: enough blocks to cover the chip, rows per split <= 256.
+// Splits for a cache of max_seq rows: about one block per CU, rows per split <= 256 (one split,
+// no combine, for caches of at most 256 rows).
 int attention_max_splits(int max_seq, int kv_heads, int batch);
 
 // Start of a decode step (one block).  state = device {current position, prompt length, next

@@ -20,9 +20,10 @@
 // Grid (max_splits, kv_heads, batch), 256 threads.  The live context [0, pos] is cut into
 // nsplit contiguous splits of >= 16 rows (at most max_splits); block (s, g, b) handles split s
 // for the heads/kv_heads query heads sharing KV head g:
-//   phase 1: 16-lane groups compute one row's scores for all heads of the group (K row read once)
-//   phase 2: each wavefront accumulates a[t] * V[t] for every fourth row (V row read once)
-// Both phases walk the split in passes of 64 rows with the next pass's loads in flight.
+// Each 16-lane group streams its own rows of the split (K and V row read once, for all heads of
+// the group) in chunks of 4 rows with an online softmax, the next chunk's loads in flight while the
+// current one is used; the groups' (max, sum, accumulator) states are merged by shuffles within a
+// wavefront and through LDS across wavefronts.
 // With one split the block writes the normalised output; otherwise it writes unnormalised
 // partials (o, max, sum) that attn_combine_kernel merges in the next launch (the kernel boundary
 // makes them visible, so no block needs a device-wide fence).
@@ -36,7 +37,9 @@ constexpr int kShortMax = 256;  // caches up to this many rows: one block per (s
 constexpr int kMaxSplits = 1024;
 
 struct AttnParams {
-    const float* qkv;
+    const float* q;        // [batch][stride]: this step's raw q, k, v (k and v may live elsewhere)
+    const float* k;
+    const float* v;
     int qkv_stride;
     const float* q_norm;
     const float* k_norm;
@@ -45,7 +48,8 @@ struct AttnParams {
     float* kcache;
     float* vcache;
     int max_seq;
-    const int* pos;
+    const int* pos;        // device position, or null: pos_value
+    int pos_value;
     int heads, kv_heads;
     double rope_c;  // -2 ln(theta) / hd
     const float2* rope_tab;  // [max_seq][hd/2] (cos, sin) or null
@@ -106,25 +110,22 @@ __device__ inline void rope_cs(const float2* row, int pos, int f, double c, floa
     *sn = (float)sin(ang);
 }
 
-// NT threads: 256 when the context is cut into splits across blocks, 512 / 1024 for a context of
-// at most kShortMax rows handled by one block per (sequence, KV head) with no combine launch.
+// NT threads: 256 when the context is cut into splits across blocks, 512 for a context of at most
+// kShortMax rows handled by one block per (sequence, KV head) with no combine launch.
 template <int HD, int G, int NT>
 __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     constexpr int FD = HD / 2;
-    constexpr int EPL = HD / 16;     // elements per lane in a 16-lane row group (phase 1)
-    constexpr int VPL = HD / 64;     // value columns per lane (phase 2)
-    constexpr int NG = NT / 16;                // 16-lane row groups (phase 1)
-    constexpr int NWV = NT / 64;               // wavefronts (phase 2)
-    constexpr int KU = NT == 1024 ? 2 : 4;     // K rows per group per pass
-    constexpr int VU = NT == 1024 ? 8 : 16;    // V rows per wavefront per pass
-    constexpr int PASS1 = NG * KU, PASS2 = NWV * VU;
-    constexpr int TILE = NT == 256 ? kMaxTile : kShortMax;
+    constexpr int EPL = HD / 16;     // dims per lane: a 16-lane group holds one row; lane gl holds dims
+                                     // 64*(e/4) + 4*gl + e%4, so each 16-byte load of the group covers
+                                     // 256 contiguous bytes of the row
+    constexpr int NGR = NT / 16;     // 16-lane row groups
+    constexpr int NWV = NT / 64;     // wavefronts
+    constexpr int RU = G >= 8 ? 2 : 4;  // rows per group per chunk (registers: G query fragments)
     __shared__ __attribute__((aligned(16))) float q_s[G][HD];
     __shared__ __attribute__((aligned(16))) float k_new[HD];
     __shared__ __attribute__((aligned(16))) float v_new[HD];
-    __shared__ float s_s[G][TILE];
-    __shared__ __attribute__((aligned(16))) float red_s[NWV][G][HD];
-    __shared__ float m_s[G], l_s[G];
+    __shared__ __attribute__((aligned(16))) float red_acc[NWV][G][HD];
+    __shared__ float red_m[NWV][G], red_l[NWV][G];
     __shared__ float scratch[NWV];
     __shared__ float rq_s[G], rk_s;
 
@@ -133,13 +134,13 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
     const int heads = p.heads, kvH = p.kv_heads;
     const int q_dim = heads * HD, kv_dim = kvH * HD;
-    const float* q_raw = p.qkv + (size_t)b * p.qkv_stride;
-    const float* k_raw = q_raw + q_dim;
-    const float* v_raw = k_raw + kv_dim;
+    const float* q_raw = p.q + (size_t)b * p.qkv_stride;
+    const float* k_raw = p.k + (size_t)b * p.qkv_stride;
+    const float* v_raw = p.v + (size_t)b * p.qkv_stride;
     const bool whole_norm = (p.q_norm || p.k_norm) && !p.per_head_norm;
 
     // ---- every load that does not depend on the position, issued together with it ----------
-    const int pos = *p.pos;
+    const int pos = p.pos ? *p.pos : p.pos_value;
     constexpr int QPT = (G * FD + NT - 1) / NT;  // query (f, f+hd/2) pairs per thread
     float qx1[QPT], qx2[QPT], qg1[QPT], qg2[QPT];
 #pragma unroll
@@ -182,36 +183,25 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     float* kc = p.kcache + head_base;
     float* vc = p.vcache + head_base;
 
-    // ---- first pass of K and V rows, issued before anything that depends on the QKV kernel.
-    // Rows are clamped to the split (duplicates are dropped below); row `pos` is stale in the
-    // cache until this block writes it, so that row is taken from LDS instead.
-    float kr[KU][EPL];
-    float vr[VU][VPL];
-    auto load_k = [&](float (&dst)[KU][EPL], int base) {
+    // ---- rows of the split: group `grp` takes rows t0 + grp + NGR*i (neighbouring groups read
+    // neighbouring rows), chunk c = rows i in [c*RU, c*RU + RU).  The first chunk's K and V rows are
+    // issued before anything that depends on the QKV kernel.  Rows are clamped to the split (their
+    // scores are masked below); row `pos` is stale in the cache until this block writes it, so
+    // that row is taken from LDS instead.
+    float kr[RU][EPL], vr[RU][EPL];
+    auto load_rows = [&](float (&dst)[RU][EPL], const float* src, int c) {
 #pragma unroll
-        for (int u = 0; u < KU; u++) {
-            const int t = min(base + grp + NG * u, t1 - 1);
+        for (int j = 0; j < RU; j++) {
+            const int t = min(t0 + grp + NGR * (c * RU + j), t1 - 1);
 #pragma unroll
-            for (int j = 0; j < EPL / 4; j++) {
-                const float4 v = *reinterpret_cast<const float4*>(kc + (size_t)t * HD + j * 64 + gl * 4);
-                dst[u][j * 4] = v.x; dst[u][j * 4 + 1] = v.y; dst[u][j * 4 + 2] = v.z; dst[u][j * 4 + 3] = v.w;
+            for (int e = 0; e < EPL; e += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(src + (size_t)t * HD + 16 * e + gl * 4);
+                dst[j][e] = v.x; dst[j][e + 1] = v.y; dst[j][e + 2] = v.z; dst[j][e + 3] = v.w;
             }
         }
     };
-    auto load_v = [&](float (&dst)[VU][VPL], int base) {
-#pragma unroll
-        for (int u = 0; u < VU; u++) {
-            const int t = min(base + wave + NWV * u, t1 - 1);
-            if constexpr (VPL == 2) {
-                const float2 v = *reinterpret_cast<const float2*>(vc + (size_t)t * HD + lane * 2);
-                dst[u][0] = v.x; dst[u][1] = v.y;
-            } else {
-                dst[u][0] = vc[(size_t)t * HD + lane];
-            }
-        }
-    };
-    load_k(kr, t0);
-    load_v(vr, t0);
+    load_rows(kr, kc, 0);
+    load_rows(vr, vc, 0);
     const float2* rope_row = p.rope_tab ? p.rope_tab + (size_t)pos * FD : nullptr;
     float2 qcs[QPT], kcs;
 #pragma unroll
@@ -284,122 +274,130 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     }
     __syncthreads();
 
-    // ---- phase 1: scores -----------------------------------------------------------
-    {
-        float qr[G][EPL];
+    // ---- one pass over K and V: online softmax per group, chunk by chunk ---------------
+    // Scores are kept in base 2: the query fragment is pre-multiplied by log2(e)/sqrt(hd), so
+    // exp(s - m) = exp2(s2 - m2) and the hardware exp2 serves every weight; m2 converts back to
+    // natural-log units for the split partials.
+    const float c2 = 1.4426950408889634f / sqrtf((float)HD);
+    float qf[G][EPL];
 #pragma unroll
-        for (int g = 0; g < G; g++)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int j = 0; j < EPL / 4; j++) {
-                const float4 t = *reinterpret_cast<const float4*>(&q_s[g][j * 64 + gl * 4]);
-                qr[g][j * 4] = t.x; qr[g][j * 4 + 1] = t.y; qr[g][j * 4 + 2] = t.z; qr[g][j * 4 + 3] = t.w;
-            }
-        const float scale = sqrtf((float)HD);
-        for (int base = t0; base < t1; base += PASS1) {
-            // the next pass's rows are in flight while this pass is scored
-            float kn[KU][EPL];
-            const bool more = base + PASS1 < t1;
-            if (more) load_k(kn, base + PASS1);
+        for (int e = 0; e < EPL; e += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(&q_s[g][16 * e + gl * 4]);
+            qf[g][e] = t.x * c2; qf[g][e + 1] = t.y * c2; qf[g][e + 2] = t.z * c2; qf[g][e + 3] = t.w * c2;
+        }
+    float m[G], l[G], acc[G][EPL];
 #pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int t = base + grp + NG * u;
-                if (has_pos && t == pos) {
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
 #pragma unroll
-                    for (int j = 0; j < EPL / 4; j++) {
-                        const float4 v = *reinterpret_cast<const float4*>(&k_new[j * 64 + gl * 4]);
-                        kr[u][j * 4] = v.x; kr[u][j * 4 + 1] = v.y; kr[u][j * 4 + 2] = v.z; kr[u][j * 4 + 3] = v.w;
+        for (int e = 0; e < EPL; e++) acc[g][e] = 0.f;
+    }
+    const int nch = (t1 - t0 + NGR * RU - 1) / (NGR * RU);
+    for (int c = 0; c < nch; c++) {
+        if (has_pos) {
+#pragma unroll
+            for (int j = 0; j < RU; j++)
+                if (t0 + grp + NGR * (c * RU + j) == pos)
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) {
+                        kr[j][e] = k_new[16 * (e & ~3) + gl * 4 + (e & 3)];
+                        vr[j][e] = v_new[16 * (e & ~3) + gl * 4 + (e & 3)];
                     }
-                }
+        }
+        // scores q . K[t] / sqrt(hd) of the chunk's rows (rows past the split: -inf)
+        float sc[G][RU];
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    float d = 0.f;
+        for (int j = 0; j < RU; j++) {
+            const bool valid = t0 + grp + NGR * (c * RU + j) < t1;
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) d = fmaf(qr[g][e], kr[u][e], d);
+            for (int g = 0; g < G; g++) {
+                float d = 0.f;
 #pragma unroll
-                    for (int off = 8; off > 0; off >>= 1) d += __shfl_xor(d, off, 16);
-                    if (gl == 0 && t < t1) s_s[g][t - t0] = d / scale;
-                }
+                for (int e = 0; e < EPL; e++) d = fmaf(qf[g][e], kr[j][e], d);
+#pragma unroll
+                for (int off = 8; off > 0; off >>= 1) d += __shfl_xor(d, off, 16);
+                sc[g][j] = valid ? d : -INFINITY;
             }
-            if (more)
+        }
+        if (c + 1 < nch) load_rows(kr, kc, c + 1);  // K of the next chunk, in flight from here
 #pragma unroll
-                for (int u = 0; u < KU; u++)
+        for (int g = 0; g < G; g++) {
+            float mc = sc[g][0];
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) kr[u][e] = kn[u][e];
+            for (int j = 1; j < RU; j++) mc = fmaxf(mc, sc[g][j]);
+            const float mn = fmaxf(m[g], mc);
+            if (mn == -INFINITY) continue;  // nothing valid yet for this group
+            const float alpha = (m[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);
+            l[g] *= alpha;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[g][e] *= alpha;
+#pragma unroll
+            for (int j = 0; j < RU; j++) {
+                const float pj = __builtin_amdgcn_exp2f(sc[g][j] - mn);  // masked: exp2(-inf) = 0
+                l[g] += pj;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(pj, vr[j][e], acc[g][e]);
+            }
+            m[g] = mn;
+        }
+        if (c + 1 < nch) load_rows(vr, vc, c + 1);  // V of the next chunk
+    }
+
+    // ---- merge the groups: the four of a wavefront by shuffles, the wavefronts through LDS ---
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float mo = __shfl_xor(m[g], off, 64), lo = __shfl_xor(l[g], off, 64);
+            const float mn = fmaxf(m[g], mo);
+            const float a = (m[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);
+            const float bo = (mo == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mo - mn);
+            l[g] = l[g] * a + lo * bo;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                const float ao = __shfl_xor(acc[g][e], off, 64);
+                acc[g][e] = acc[g][e] * a + ao * bo;
+            }
+            m[g] = mn;
         }
     }
-    __syncthreads();
-
-    // ---- split-local softmax statistics --------------------------------------------
-    const int len = t1 - t0;
-    for (int g = wave; g < G; g += NWV) {
-        float m = -INFINITY;
-        for (int i = lane; i < len; i += 64) m = fmaxf(m, s_s[g][i]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int i = lane; i < len; i += 64) {
-            const float e = expf(s_s[g][i] - m);
-            s_s[g][i] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) { m_s[g] = m; l_s[g] = l; }
-    }
-    __syncthreads();
-
-    // ---- phase 2: values -------------------------------------------------------------
-    {
-        float acc[G][VPL];
+    if (lane < 16) {
 #pragma unroll
-        for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++) {
 #pragma unroll
-            for (int j = 0; j < VPL; j++) acc[g][j] = 0.f;
-        for (int base = t0; base < t1; base += PASS2) {
-            float vn[VU][VPL];
-            const bool more = base + PASS2 < t1;
-            if (more) load_v(vn, base + PASS2);
-#pragma unroll
-            for (int u = 0; u < VU; u++) {
-                const int t = base + wave + NWV * u;
-                if (t < t1) {
-                    if (has_pos && t == pos) {
-#pragma unroll
-                        for (int j = 0; j < VPL; j++) vr[u][j] = v_new[lane * VPL + j];
-                    }
-#pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        const float a = s_s[g][t - t0];
-#pragma unroll
-                        for (int j = 0; j < VPL; j++) acc[g][j] = fmaf(a, vr[u][j], acc[g][j]);
-                    }
-                }
+            for (int e = 0; e < EPL; e++) red_acc[wave][g][16 * (e & ~3) + gl * 4 + (e & 3)] = acc[g][e];
+            if (lane == 0) {
+                red_m[wave][g] = m[g];
+                red_l[wave][g] = l[g];
             }
-            if (more)
-#pragma unroll
-                for (int u = 0; u < VU; u++)
-#pragma unroll
-                    for (int j = 0; j < VPL; j++) vr[u][j] = vn[u][j];
         }
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int j = 0; j < VPL; j++) red_s[wave][g][lane * VPL + j] = acc[g][j];
     }
     __syncthreads();
 
     const int hbase = kvh * G;
     for (int idx = tid; idx < G * HD; idx += NT) {
         const int g = idx / HD, i = idx - g * HD;
-        float o = 0.f;
+        float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NWV; w++) o += red_s[w][g][i];
+        for (int w = 0; w < NWV; w++) M = fmaxf(M, red_m[w][g]);
+        float L = 0.f, o = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWV; w++) {
+            const float wt = (red_m[w][g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(red_m[w][g] - M);
+            L = fmaf(red_l[w][g], wt, L);
+            o = fmaf(red_acc[w][g][i], wt, o);
+        }
         if (nsplit == 1) {
-            p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = o / l_s[g];
+            p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = o / L;
         } else {
             const size_t slot = ((size_t)b * heads + hbase + g) * p.max_splits + split;
             p.part_o[slot * HD + i] = o;
             if (i == 0) {
-                p.part_ml[slot * 2] = m_s[g];
-                p.part_ml[slot * 2 + 1] = l_s[g];
+                p.part_ml[slot * 2] = M * 0.6931471805599453f;  // back to natural-log units
+                p.part_ml[slot * 2 + 1] = L;
             }
         }
     }
@@ -414,7 +412,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
     __shared__ float red[HD / 64];
     const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
     const int lane = i & 63, wave = i >> 6;
-    const int pos = *p.pos;
+    const int pos = p.pos ? *p.pos : p.pos_value;
     if (pos < 0 || pos >= p.max_seq) return;
     int nsplit, tile;
     split_plan(pos + 1, p.max_splits, &nsplit, &tile);
@@ -461,16 +459,19 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
 template <int HD, int G>
 int launch_t(const AttnLaunch& a, hipStream_t stream) {
     AttnParams p;
-    p.qkv = a.qkv; p.qkv_stride = a.qkv_stride; p.q_norm = a.q_norm; p.k_norm = a.k_norm;
+    p.q = a.qkv ? a.qkv : a.q;
+    p.k = a.qkv ? a.qkv + (size_t)a.heads * a.head_dim : a.k;
+    p.v = a.qkv ? a.qkv + (size_t)(a.heads + a.kv_heads) * a.head_dim : a.v;
+    p.qkv_stride = a.qkv_stride; p.q_norm = a.q_norm; p.k_norm = a.k_norm;
     p.qk_eps = a.qk_eps; p.per_head_norm = a.per_head_norm; p.kcache = a.kcache; p.vcache = a.vcache;
-    p.max_seq = a.max_seq; p.pos = a.pos; p.heads = a.heads; p.kv_heads = a.kv_heads;
+    p.max_seq = a.max_seq; p.pos = a.pos; p.pos_value = a.pos_value; p.heads = a.heads; p.kv_heads = a.kv_heads;
     p.rope_c = -2.0 * log(a.rope_theta) / (double)HD;
     p.rope_tab = a.rope_tab;
     p.max_splits = a.max_splits; p.part_o = a.part_o; p.part_ml = a.part_ml;
     p.out = a.out; p.out_stride = a.out_stride;
     if (a.max_splits == 1 && a.max_seq <= kShortMax) {
-        // whole context in one block: 1024 threads (512 when 8 query heads share a KV head, for registers)
-        constexpr int NT = G <= 4 ? 1024 : 512;
+        // whole context in one block
+        constexpr int NT = 512;
         hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT>), dim3(1, a.kv_heads, a.batch), dim3(NT), 0, stream, p);
         AR_LAUNCH_CHECK();
         return AR_HIP_OK;
@@ -506,7 +507,9 @@ size_t attention_partial_floats(int batch, int heads, int max_splits, int hd) {
 int attention_max_splits(int max_seq, int kv_heads, int batch) {
     if (max_seq <= kShortMax) return 1;  // one block per (sequence, KV head), no combine launch
     const int need = (max_seq + kMaxTile - 1) / kMaxTile;      // rows per split <= kMaxTile
-    const int want = (1024 + kv_heads * batch - 1) / (kv_heads * batch);  // ~4 blocks per CU
+    // about one block per CU: each block then streams a tile long enough to amortise its prologue
+    // (C2, 4097 rows: 32 splits of 129 rows; 128 splits of 33 rows measured 2.4x slower)
+    const int want = (256 + kv_heads * batch - 1) / (kv_heads * batch);
     const int cap = (max_seq + 15) / 16;                       // splits of >= 16 rows
     int s = want < cap ? want : cap;
     if (s < need) s = need;
@@ -514,7 +517,9 @@ int attention_max_splits(int max_seq, int kv_heads, int batch) {
 }
 
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
-    AR_CHECK_ARG(a.qkv && a.kcache && a.vcache && a.pos && a.out, "attention: null pointer");
+    AR_CHECK_ARG((a.qkv || (a.q && a.k && a.v)) && a.kcache && a.vcache && a.out, "attention: null pointer");
+    AR_CHECK_ARG(a.pos || (a.pos_value >= 0 && a.pos_value < a.max_seq), "attention: position %d outside %d rows",
+                 a.pos_value, a.max_seq);
     AR_CHECK_ARG(a.heads > 0 && a.kv_heads > 0 && a.heads % a.kv_heads == 0, "attention: bad head counts %d/%d",
                  a.heads, a.kv_heads);
     AR_CHECK_ARG(a.max_splits <= kMaxSplits, "attention: %d splits exceed %d", a.max_splits, kMaxSplits);

@@ -38,14 +38,12 @@ extern "C" int ar_hip_index_of_max(ar_hip_ctx* ctx, const float* x, int rows, in
 }
 
 namespace {
-// Scratch the stand-alone attention op keeps between calls: packed q|k|v, the position and the
-// split partials.  Grown on demand; freed with the context's allocations.
+// Split partials the stand-alone attention op keeps between calls.  Grown on demand; freed with
+// the context's allocations.
 struct AttnScratch {
-    size_t qkv_floats = 0, part_floats = 0, ml_floats = 0;
-    float* qkv = nullptr;
+    size_t part_floats = 0, ml_floats = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
-    int* pos = nullptr;
 };
 std::mutex g_attn_mu;
 std::unordered_map<ar_hip_ctx*, AttnScratch> g_attn;
@@ -71,24 +69,16 @@ extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const fl
     AR_CHECK_ARG(qk_norm_mode == AR_QK_NORM_WHOLE || qk_norm_mode == AR_QK_NORM_PER_HEAD, "attention: bad qk-norm mode");
     std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnScratch& s = g_attn[ctx];
-    const int q_dim = heads * head_dim, kv_dim = kv_heads * head_dim;
     const int max_splits = attention_max_splits(max_seq, kv_heads, 1);
-    size_t dummy = 0;
-    AR_TRY(grow(ctx, (void**)&s.qkv, &s.qkv_floats, (size_t)q_dim + 2 * kv_dim, sizeof(float)));
     AR_TRY(grow(ctx, (void**)&s.part_o, &s.part_floats, attention_partial_floats(1, heads, max_splits, head_dim),
                 sizeof(float)));
     AR_TRY(grow(ctx, (void**)&s.part_ml, &s.ml_floats, (size_t)heads * max_splits * 2, sizeof(float)));
-    if (!s.pos) AR_TRY(grow(ctx, (void**)&s.pos, &dummy, 1, sizeof(int)));
-    AR_HIP_TRY(hipMemcpyAsync(s.qkv, q, sizeof(float) * q_dim, hipMemcpyDeviceToDevice, ctx->stream));
-    AR_HIP_TRY(hipMemcpyAsync(s.qkv + q_dim, k, sizeof(float) * kv_dim, hipMemcpyDeviceToDevice, ctx->stream));
-    AR_HIP_TRY(hipMemcpyAsync(s.qkv + q_dim + kv_dim, v, sizeof(float) * kv_dim, hipMemcpyDeviceToDevice, ctx->stream));
-    AR_TRY(launch_fill_i32(s.pos, pos, 1, ctx->stream));
     AttnLaunch a;
-    a.qkv = s.qkv; a.qkv_stride = q_dim + 2 * kv_dim; a.q_norm = q_norm; a.k_norm = k_norm; a.qk_eps = qk_eps;
+    a.q = q; a.k = k; a.v = v; a.qkv_stride = 0; a.q_norm = q_norm; a.k_norm = k_norm; a.qk_eps = qk_eps;
     a.per_head_norm = qk_norm_mode == AR_QK_NORM_PER_HEAD; a.kcache = k_cache; a.vcache = v_cache;
-    a.max_seq = max_seq; a.pos = s.pos; a.heads = heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
-    a.rope_theta = rope_theta; a.max_splits = max_splits; a.part_o = s.part_o; a.part_ml = s.part_ml;
-    a.out = out; a.out_stride = q_dim; a.batch = 1;
+    a.max_seq = max_seq; a.pos = nullptr; a.pos_value = pos; a.heads = heads; a.kv_heads = kv_heads;
+    a.head_dim = head_dim; a.rope_theta = rope_theta; a.max_splits = max_splits; a.part_o = s.part_o;
+    a.part_ml = s.part_ml; a.out = out; a.out_stride = heads * head_dim; a.batch = 1;
     return launch_attention_decode(a, ctx->stream);
 }
 

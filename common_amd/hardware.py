@@ -204,6 +204,10 @@ class HipContext:
     def to_device(self, a: np.ndarray) -> DeviceBuffer:
         return DeviceBuffer.from_array(self, a)
 
+    def copy(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int):
+        """Device-to-device copy on the context's stream."""
+        check(lib().ar_hip_memcpy_d2d(self.handle, dst.ptr, src.ptr, nbytes))
+
     # operators (see include/ar_hip.h for the reference each mirrors) ----------------
     def rmsnorm(self, x: DeviceBuffer, w: DeviceBuffer, y: DeviceBuffer, rows: int, n: int, eps: float):
         check(lib().ar_hip_rmsnorm(self.handle, x.ptr, w.ptr, y.ptr, rows, n, eps))
