@@ -13,10 +13,11 @@
 // 8 consecutive k values (l / 32) * 8 .. +7 of a 16-wide k slice; the 32x32 fp32 result lands in
 // 16 registers per lane, register r holding row (r/4)*8 + (l/32)*4 + r%4, column l % 32.
 //
-// Tiling: 128 x 128 block tile, BK = 64, 256 threads as 2 x 2 wavefronts of 64 x 64 (2 x 2 MFMA
-// tiles each).  Global tiles are loaded 16 bytes per lane into registers one k-step ahead and
-// stored into the other half of a double-buffered, row-padded LDS tile (row stride 72 bf16 =
-// 144 B, so the 16-byte fragment reads of consecutive rows fall in different bank groups).
+// Tiling: 256 x 128 block tile (128 x 128 when that leaves fewer than 256 blocks), BK = 64,
+// wavefronts of 64 x 64 (2 x 2 MFMA tiles each).  Global tiles are loaded 16 bytes per lane into
+// registers one k-step ahead and stored into a row-padded LDS tile (row stride 72 bf16 = 144 B, so
+// the 16-byte fragment reads of consecutive rows fall in different bank groups).  Blocks take
+// output tiles in an XCD-grouped order (tile_of).
 // Epilogues: fp32 store (+bias), fp32 residual add, and SwiGLU of two weight matrices written as
 // bf16 (the next GEMM's A operand).
 #include "ar_hip_internal.h"
@@ -26,6 +27,7 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 halfx8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // register staging (stays in VGPRs)
 
 // MFMA operand element: bf16 (v_mfma_f32_32x32x16_bf16) or fp16 (v_mfma_f32_32x32x16_f16); both
 // take 8 consecutive k values per lane in the same lane layout and accumulate in fp32.
@@ -56,9 +58,8 @@ struct Mfma<true> {
     }
 };
 
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BN = 128, BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row
-constexpr int kThreads = 256;
 
 struct GemmParams {
     const uint16_t* A;  // [M][lda] bf16
@@ -72,43 +73,66 @@ struct GemmParams {
     int ldo;
 };
 
-template <int NW>  // 1 weight matrix, or 2 for SwiGLU
+template <int NW, int BMT>  // 1 weight matrix, or 2 for SwiGLU; BMT rows of A per block
 struct Tiles {
-    uint16_t a[2][BM * LDS_STRIDE];
-    uint16_t w[NW][2][BN * LDS_STRIDE];
+    uint16_t a[1][BMT * LDS_STRIDE];
+    uint16_t w[NW][1][BN * LDS_STRIDE];
 };
 
-template <bool F16, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
+// Block -> output tile.  Blocks are dispatched round-robin over the 8 XCDs; consecutive tile indices
+// are given to one XCD, and tile indices walk groups of 8 m-tiles column by column, so the blocks
+// an XCD runs together share A row-tiles and W column-tiles in that XCD's L2.
+__device__ inline void tile_of(int bid, int mt, int nt, int* mi, int* ni) {
+    const int nblk = mt * nt;
+    int t = bid;
+    if (nblk % 8 == 0) t = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    constexpr int G = 8;
+    const int per_group = G * nt;
+    const int group = t / per_group, first_m = group * G;
+    const int gsize = min(mt - first_m, G);
+    const int r = t - group * per_group;
+    *mi = first_m + r % gsize;
+    *ni = r / gsize;
+}
+
+// BMT x 128 block tile, (BMT/64) x 2 wavefronts of 64 x 64.
+template <bool F16, int EPI, int BMT>
+__global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int nt) {
     using M = Mfma<F16>;
     using frag = typename M::frag;
     constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
-    __shared__ __attribute__((aligned(16))) Tiles<NW> t;
+    constexpr int NTHR = BMT * 2;
+    constexpr int RPP = NTHR / 8;         // tile rows per load pass (8 threads x 16 B per 64-wide row)
+    constexpr int AL = BMT / RPP, WL = BN / RPP;
+    __shared__ __attribute__((aligned(16))) Tiles<NW, BMT> t;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int mi, ni;
+    tile_of(blockIdx.x, mt, nt, &mi, &ni);
+    const int m0 = mi * BMT, n0 = ni * BN;
 
-    // global -> register staging: 4 x 16 B of A and of each W per thread per k-step
-    // element (row = tid/8 + 32*i, k chunk = (tid%8)*8)
+    // global -> register staging per k-step: AL x 16 B of A and WL x 16 B of each W per thread
+    // (element row = tid/8 + RPP*i, k chunk = (tid%8)*8)
     const int lrow = tid >> 3, lk = (tid & 7) * 8;
-    uint4 ra[4], rw[NW][4];
+    u32x4 ra[AL], rw[NW][WL];
 #define AR_GEMM_LOAD_GLOBAL(k0)                                                                          \
-    _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                      \
-        const int r = lrow + 32 * i;                                                                     \
-        const int am = min(m0 + r, p.M - 1);                                                             \
-        ra[i] = *reinterpret_cast<const uint4*>(p.A + (size_t)am * p.lda + (k0) + lk);                   \
-        rw[0][i] = *reinterpret_cast<const uint4*>(p.W + (size_t)(n0 + r) * p.ldw + (k0) + lk);          \
+    _Pragma("unroll") for (int i = 0; i < AL; i++) {                                                     \
+        const int am = min(m0 + lrow + RPP * i, p.M - 1);                                                \
+        ra[i] = *reinterpret_cast<const u32x4*>(p.A + (size_t)am * p.lda + (k0) + lk);                   \
+    }                                                                                                    \
+    _Pragma("unroll") for (int i = 0; i < WL; i++) {                                                     \
+        const int r = lrow + RPP * i;                                                                    \
+        rw[0][i] = *reinterpret_cast<const u32x4*>(p.W + (size_t)(n0 + r) * p.ldw + (k0) + lk);          \
         if constexpr (NW == 2)                                                                           \
-            rw[NW - 1][i] = *reinterpret_cast<const uint4*>(p.W2 + (size_t)(n0 + r) * p.ldw + (k0) + lk);\
+            rw[NW - 1][i] = *reinterpret_cast<const u32x4*>(p.W2 + (size_t)(n0 + r) * p.ldw + (k0) + lk);\
     }
 #define AR_GEMM_STORE_LDS(buf)                                                                           \
-    _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                      \
-        const int r = lrow + 32 * i;                                                                     \
-        *reinterpret_cast<uint4*>(&t.a[buf][r * LDS_STRIDE + lk]) = ra[i];                               \
+    _Pragma("unroll") for (int i = 0; i < AL; i++)                                                       \
+        *reinterpret_cast<u32x4*>(&t.a[buf][(lrow + RPP * i) * LDS_STRIDE + lk]) = ra[i];                \
+    _Pragma("unroll") for (int i = 0; i < WL; i++)                                                       \
         _Pragma("unroll") for (int w = 0; w < NW; w++)                                                   \
-            *reinterpret_cast<uint4*>(&t.w[w][buf][r * LDS_STRIDE + lk]) = rw[w][i];                     \
-    }
+            *reinterpret_cast<u32x4*>(&t.w[w][buf][(lrow + RPP * i) * LDS_STRIDE + lk]) = rw[w][i];
 
     floatx16 acc[NW][2][2];
 #pragma unroll
@@ -120,14 +144,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[w][i][j][r] = 0.f;
 
+    // One LDS buffer: the next k-tile's global loads are in flight in registers while the current
+    // tile is multiplied; then the tile is swapped under two barriers.  (Half the LDS of a double
+    // buffer, so two 256-row blocks fit on a CU.)
     const int nk = p.K / BK;
     AR_GEMM_LOAD_GLOBAL(0)
     AR_GEMM_STORE_LDS(0)
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
-        // next tile in flight during the MFMAs (the last step reloads its own tile: a cache hit
-        // into the idle buffer, kept unconditional so the staging stays in registers)
+        const int buf = 0;
+        // (the last step reloads its own tile: a cache hit, kept unconditional so the staging stays
+        // in registers)
         const int knext = (kt + 1 < nk ? kt + 1 : kt) * BK;
         AR_GEMM_LOAD_GLOBAL(knext)
 #pragma unroll
@@ -154,7 +181,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
                     for (int j = 0; j < 2; j++)
                         acc[w][i][j] = M::mac(af[i], bfr[w][j], acc[w][i][j]);
         }
-        AR_GEMM_STORE_LDS(buf ^ 1)
+        __syncthreads();  // every wave is done with the tile
+        AR_GEMM_STORE_LDS(0)  // (unconditional: a conditional store spills the staging registers)
         __syncthreads();
     }
 #undef AR_GEMM_LOAD_GLOBAL
@@ -185,15 +213,24 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
         }
 }
 
-template <int EPI>
-int launch_t(const GemmParams& p, bool f16, hipStream_t st) {
-    dim3 grid(p.N / BN, (p.M + BM - 1) / BM);
+template <int EPI, int BMT>
+int launch_bm(const GemmParams& p, bool f16, hipStream_t st) {
+    const int mt = (p.M + BMT - 1) / BMT, nt = p.N / BN;
+    const dim3 grid(mt * nt), block(BMT * 2);
     if (f16)
-        hipLaunchKernelGGL((gemm_kernel<true, EPI>), grid, dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((gemm_kernel<true, EPI, BMT>), grid, block, 0, st, p, mt, nt);
     else
-        hipLaunchKernelGGL((gemm_kernel<false, EPI>), grid, dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((gemm_kernel<false, EPI, BMT>), grid, block, 0, st, p, mt, nt);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
+}
+
+// 256-row block tiles halve the A/W tile loads per MFMA (measured: the 128 x 128 tile is bound by
+// L2 -> CU operand traffic); they are used while they still give at least 256 blocks.
+template <int EPI>
+int launch_t(const GemmParams& p, bool f16, hipStream_t st) {
+    if ((long long)((p.M + 255) / 256) * (p.N / BN) >= 256) return launch_bm<EPI, 256>(p, f16, st);
+    return launch_bm<EPI, 128>(p, f16, st);
 }
 
 }  // namespace
