@@ -172,6 +172,18 @@ struct AttnLaunch {
     int batch = 1;
 };
 
+// Split plan of a live context of n rows over at most max_splits splits of >= kAttnMinTile rows
+// (the last may be short); the attention and combine kernels evaluate it from the device position.
+constexpr int kAttnMinTile = 16;
+__host__ __device__ inline void attn_split_plan(int n, int max_splits, int* nsplit, int* tile) {
+    int ns = (n + kAttnMinTile - 1) / kAttnMinTile;
+    if (ns > max_splits) ns = max_splits;
+    if (ns < 1) ns = 1;
+    const int t = (n + ns - 1) / ns;
+    *tile = t;
+    *nsplit = (n + t - 1) / t;
+}
+
 // Attention partials + (when the context is split) the combine kernel.
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);

@@ -86,15 +86,6 @@ __device__ inline float block_sum(float v, float* scratch) {
     return t;
 }
 
-// Split plan for a live context of n rows: nsplit splits of `tile` rows (the last may be short).
-__device__ inline void split_plan(int n, int max_splits, int* nsplit, int* tile) {
-    int ns = min(max_splits, (n + 15) / 16);
-    if (ns < 1) ns = 1;
-    const int t = (n + ns - 1) / ns;
-    *tile = t;
-    *nsplit = (n + t - 1) / t;
-}
-
 // (cos, sin) of pos * exp(f * -2 ln(theta) / hd): from the table the model precomputes in
 // double on the host, or evaluated here in double when no table is given.
 __device__ inline void rope_cs(const float2* row, int pos, int f, double c, float* cs, float* sn) {
@@ -175,7 +166,7 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     if (pos < 0 || pos >= p.max_seq) return;
     const int n = pos + 1;
     int nsplit, tile;
-    split_plan(n, p.max_splits, &nsplit, &tile);
+    attn_split_plan(n, p.max_splits, &nsplit, &tile);
     if (split >= nsplit) return;
     const int t0 = split * tile;
     const int t1 = min(t0 + tile, n);
@@ -415,7 +406,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
     const int pos = p.pos ? *p.pos : p.pos_value;
     if (pos < 0 || pos >= p.max_seq) return;
     int nsplit, tile;
-    split_plan(pos + 1, p.max_splits, &nsplit, &tile);
+    attn_split_plan(pos + 1, p.max_splits, &nsplit, &tile);
     if (nsplit == 1) return;  // the attention kernel wrote the output itself
     const size_t slot0 = ((size_t)b * p.heads + h) * p.max_splits;
     float m_loc = -INFINITY;
@@ -510,7 +501,7 @@ int attention_max_splits(int max_seq, int kv_heads, int batch) {
     // about one block per CU: each block then streams a tile long enough to amortise its prologue
     // (C2, 4097 rows: 32 splits of 129 rows; 128 splits of 33 rows measured 2.4x slower)
     const int want = (256 + kv_heads * batch - 1) / (kv_heads * batch);
-    const int cap = (max_seq + 15) / 16;                       // splits of >= 16 rows
+    const int cap = (max_seq + kAttnMinTile - 1) / kAttnMinTile;  // splits of >= kAttnMinTile rows
     int s = want < cap ? want : cap;
     if (s < need) s = need;
     return s < 1 ? 1 : s;
