@@ -113,6 +113,8 @@ struct GemmLaunch {
     int ldo = 0;
     int epilogue = GEMV_EPI_STORE;
     bool f16 = false;
+    int ksplit = 1;  // > 1 (store epilogue): k-slice s of the product goes to C + s*M*ldc, for the
+                     // consumer to add up in a fixed order (more blocks for small M x N, no atomics)
 };
 int launch_gemm(const GemmLaunch& a, hipStream_t stream);
 
@@ -122,6 +124,12 @@ int launch_embed_rows(const void* table, int wdtype, int dim, const int* tokens,
                       float* x, hipStream_t stream);
 int launch_rmsnorm_rows_f16(const float* x, const float* w, uint16_t* out, int rows, int n, float eps,
                             hipStream_t stream);
+// x[r] += sum_s parts[s][r] (s in order; nparts may be 0), then out[r] = fp16 RMSNorm(x[r]) as above.
+int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const float* w, uint16_t* out, int rows,
+                                 int n, float eps, hipStream_t stream);
+// dst[b] = src[rows[b]] + sum_s parts[s][rows[b]] for b < count (rows of n floats).
+int launch_fold_rows(const float* src, const float* parts, int nparts, size_t part_rows, int first, int step,
+                     int count, int n, float* dst, hipStream_t stream);
 // fp16 copy of bf16 data (exact for |v| >= 2^-17 inside the fp16 range), for the prefill GEMMs.
 int launch_bf16_to_f16(const uint16_t* src, uint16_t* dst, size_t n, hipStream_t stream);
 struct PrefillPrep {

@@ -13,7 +13,7 @@
 // 8 consecutive k values (l / 32) * 8 .. +7 of a 16-wide k slice; the 32x32 fp32 result lands in
 // 16 registers per lane, register r holding row (r/4)*8 + (l/32)*4 + r%4, column l % 32.
 //
-// Tiling: 256 x 128 block tile (128 x 128 when that leaves fewer than 256 blocks), BK = 64,
+// Tiling: 256 x 128 block tile (128 x 128 when that leaves too few blocks), BK = 64,
 // wavefronts of 64 x 64 (2 x 2 MFMA tiles each).  Global tiles are loaded 16 bytes per lane into
 // registers one k-step ahead and stored into a row-padded LDS tile (row stride 72 bf16 = 144 B, so
 // the 16-byte fragment reads of consecutive rows fall in different bank groups).  Blocks take
@@ -71,6 +71,7 @@ struct GemmParams {
     int ldc;
     uint16_t* O;        // bf16 [M][ldo] (SWIGLU)
     int ldo;
+    int ksplit;         // > 1: block (tile, s) multiplies k-slice s and stores into C + s*M*ldc
 };
 
 template <int NW, int BMT>  // 1 weight matrix, or 2 for SwiGLU; BMT rows of A per block
@@ -109,7 +110,11 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     int mi, ni;
-    tile_of(blockIdx.x, mt, nt, &mi, &ni);
+    const int tiles = mt * nt;
+    const int ks = blockIdx.x / tiles;  // k-slice (0 unless split)
+    tile_of(blockIdx.x - ks * tiles, mt, nt, &mi, &ni);
+    const int kbase = ks * (p.K / p.ksplit);
+    float* const Cs = p.C ? p.C + (size_t)ks * p.M * p.ldc : nullptr;
     const int m0 = mi * BMT, n0 = ni * BN;
 
     // global -> register staging per k-step: AL x 16 B of A and WL x 16 B of each W per thread
@@ -147,15 +152,15 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
     // One LDS buffer: the next k-tile's global loads are in flight in registers while the current
     // tile is multiplied; then the tile is swapped under two barriers.  (Half the LDS of a double
     // buffer, so two 256-row blocks fit on a CU.)
-    const int nk = p.K / BK;
-    AR_GEMM_LOAD_GLOBAL(0)
+    const int nk = p.K / p.ksplit / BK;
+    AR_GEMM_LOAD_GLOBAL(kbase)
     AR_GEMM_STORE_LDS(0)
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
         const int buf = 0;
         // (the last step reloads its own tile: a cache hit, kept unconditional so the staging stays
         // in registers)
-        const int knext = (kt + 1 < nk ? kt + 1 : kt) * BK;
+        const int knext = kbase + (kt + 1 < nk ? kt + 1 : kt) * BK;
         AR_GEMM_LOAD_GLOBAL(knext)
 #pragma unroll
         for (int kk = 0; kk < BK / 16; kk++) {
@@ -200,9 +205,9 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
                 if (row >= p.M) continue;
                 const float v = acc[0][i][j][r];
                 if (EPI == GEMV_EPI_STORE) {
-                    p.C[(size_t)row * p.ldc + col] = p.bias ? v + p.bias[col] : v;
+                    Cs[(size_t)row * p.ldc + col] = p.bias ? v + p.bias[col] : v;
                 } else if (EPI == GEMV_EPI_RESIDUAL) {
-                    float* c = p.C + (size_t)row * p.ldc + col;
+                    float* c = Cs + (size_t)row * p.ldc + col;
                     *c = *c + v;
                 } else {
                     const float g = v, u = acc[NW - 1][i][j][r];
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
 template <int EPI, int BMT>
 int launch_bm(const GemmParams& p, bool f16, hipStream_t st) {
     const int mt = (p.M + BMT - 1) / BMT, nt = p.N / BN;
-    const dim3 grid(mt * nt), block(BMT * 2);
+    const dim3 grid(mt * nt * p.ksplit), block(BMT * 2);
     if (f16)
         hipLaunchKernelGGL((gemm_kernel<true, EPI, BMT>), grid, block, 0, st, p, mt, nt);
     else
@@ -226,10 +231,13 @@ int launch_bm(const GemmParams& p, bool f16, hipStream_t st) {
 }
 
 // 256-row block tiles halve the A/W tile loads per MFMA (measured: the 128 x 128 tile is bound by
-// L2 -> CU operand traffic); they are used while they still give at least 256 blocks.
+// L2 -> CU operand traffic); they are used while they still give two blocks per CU, or one for
+// SwiGLU (two weight tiles per block).  Measured at C4 (2048 rows): QKV 47 us with 128-row tiles vs
+// 51 us, gate/up 163 us with 256-row tiles vs 176 us.
 template <int EPI>
 int launch_t(const GemmParams& p, bool f16, hipStream_t st) {
-    if ((long long)((p.M + 255) / 256) * (p.N / BN) >= 256) return launch_bm<EPI, 256>(p, f16, st);
+    const long long blocks256 = (long long)((p.M + 255) / 256) * (p.N / BN) * p.ksplit;
+    if (blocks256 >= (EPI == GEMV_EPI_SWIGLU ? 256 : 512)) return launch_bm<EPI, 256>(p, f16, st);
     return launch_bm<EPI, 128>(p, f16, st);
 }
 
@@ -240,12 +248,14 @@ int launch_gemm(const GemmLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(a.M > 0 && a.N > 0 && a.K > 0, "GEMM: empty shape");
     AR_CHECK_ARG(a.N % BN == 0, "GEMM: N=%d must be a multiple of %d", a.N, BN);
     AR_CHECK_ARG(a.K % BK == 0, "GEMM: K=%d must be a multiple of %d", a.K, BK);
+    AR_CHECK_ARG(a.ksplit >= 1 && a.K % (BK * a.ksplit) == 0 && (a.ksplit == 1 || a.epilogue == GEMV_EPI_STORE),
+                 "GEMM: a k-split of %d needs K %% %d == 0 and the store epilogue", a.ksplit, BK * a.ksplit);
     AR_CHECK_ARG(a.lda >= a.K && a.ldw >= a.K && a.lda % 8 == 0 && a.ldw % 8 == 0, "GEMM: bad leading dims");
     AR_CHECK_ARG((reinterpret_cast<uintptr_t>(a.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.W) & 15) == 0,
                  "GEMM: operands must be 16-byte aligned");
     GemmParams p;
     p.A = a.A; p.W = a.W; p.W2 = a.W2; p.M = a.M; p.N = a.N; p.K = a.K; p.lda = a.lda; p.ldw = a.ldw;
-    p.bias = a.bias; p.C = a.C; p.ldc = a.ldc; p.O = a.O; p.ldo = a.ldo;
+    p.bias = a.bias; p.C = a.C; p.ldc = a.ldc; p.O = a.O; p.ldo = a.ldo; p.ksplit = a.ksplit;
     switch (a.epilogue) {
         case GEMV_EPI_STORE:
             AR_CHECK_ARG(a.C && a.ldc >= a.N, "GEMM: bad fp32 output");

@@ -65,6 +65,36 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_f16_kernel(const float* x, c
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = f2h((w[i] * xr[i]) * r);
 }
 
+// Residual fold of a split-k projection followed by the row RMSNorm: x[r] += sum_s parts[s][r] (in
+// slice order), written back, then out[r] = fp16((w * x[r]) * 1/sqrt(mean(x[r]^2) + eps)).
+__global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_kernel(float* x, const float* parts, int nparts,
+                                                                     size_t part_stride, const float* w,
+                                                                     uint16_t* out, int n, float eps) {
+    __shared__ float scratch[4];
+    float* xr = x + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = xr[i];
+        for (int s = 0; s < nparts; s++) v += parts[s * part_stride + (size_t)blockIdx.x * n + i];
+        if (nparts) xr[i] = v;
+        ss += v * v;
+    }
+    ss = block_sum(ss, scratch);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = f2h((w[i] * xr[i]) * r);
+}
+
+// dst[b] = src[first + b*step] + sum_s parts[s][first + b*step], rows of n floats.
+__global__ __launch_bounds__(256) void fold_rows_kernel(const float* src, const float* parts, int nparts,
+                                                        size_t part_stride, int first, int step, int n, float* dst) {
+    const size_t row = (size_t)first + (size_t)blockIdx.x * step;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = src[row * n + i];
+        for (int s = 0; s < nparts; s++) v += parts[s * part_stride + row * n + i];
+        dst[(size_t)blockIdx.x * n + i] = v;
+    }
+}
+
 struct PrepParams {
     const float* qkv;       // [R][qkv_stride] raw projections
     int qkv_stride;
@@ -380,6 +410,25 @@ int launch_rmsnorm_rows_f16(const float* x, const float* w, uint16_t* out, int r
                             hipStream_t stream) {
     AR_CHECK_ARG(x && w && out && rows > 0 && n > 0, "rmsnorm rows: bad arguments");
     hipLaunchKernelGGL(rmsnorm_rows_f16_kernel, dim3(rows), dim3(256), 0, stream, x, w, out, n, eps);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
+int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const float* w, uint16_t* out, int rows,
+                                 int n, float eps, hipStream_t stream) {
+    AR_CHECK_ARG(x && w && out && rows > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0),
+                 "fold rmsnorm rows: bad arguments");
+    hipLaunchKernelGGL(fold_rmsnorm_rows_f16_kernel, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                       (size_t)rows * n, w, out, n, eps);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
+int launch_fold_rows(const float* src, const float* parts, int nparts, size_t part_rows, int first, int step,
+                     int count, int n, float* dst, hipStream_t stream) {
+    AR_CHECK_ARG(src && dst && count > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0), "fold rows: bad arguments");
+    hipLaunchKernelGGL(fold_rows_kernel, dim3(count), dim3(256), 0, stream, src, parts, nparts, part_rows * n, first,
+                       step, n, dst);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -100,6 +100,8 @@ struct ar_qwen3 {
     float* pf_qkv = nullptr;     // [R][qkv_dim]
     uint16_t* pf_q = nullptr;    // [R][q_dim] fp16 normalised, rotated queries
     uint16_t* pf_act = nullptr;  // [R][F] fp16 SwiGLU output
+    float* pf_part = nullptr;    // [kMaxKSplit][R][dim] k-slices of split residual projections
+    size_t pf_part_rows = 0;
     uint16_t* pf_k16 = nullptr;  // [B][KV][Tp][hd] fp16 keys of the prompt rows
     uint16_t* pf_vt16 = nullptr; // [B][KV][hd][Tp] fp16 values, transposed (zeroed once: padded keys
                                  // get weight 0 and must not hold NaN bit patterns)
@@ -134,7 +136,7 @@ void release(ar_qwen3* m) {
     if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
                     m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
-                    m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_w16, m->pf_k16, m->pf_vt16};
+                    m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     delete m;
@@ -661,6 +663,16 @@ extern "C" int ar_hip_qwen3_use_prefetch(ar_qwen3* m, int blocks) {
 
 namespace {
 
+// k-slices for a prefill projection of N outputs over K inputs whose 128 x 128 output tiles would
+// not give every CU two blocks (C4's d = 2048 projections): more blocks, same weights read
+constexpr int kMaxKSplit = 4;
+int prefill_ksplit(const ar_qwen3* m, size_t rows, int N, int K) {
+    const long long tiles = (long long)((rows + 127) / 128) * (N / 128);
+    int s = 1;
+    while (s < kMaxKSplit && tiles * s < 2LL * m->ctx->num_cus && K % (64 * s * 2) == 0 && K / (s * 2) >= 512) s *= 2;
+    return s;
+}
+
 int ensure_prefill_buffers(ar_qwen3* m, size_t rows) {
     if (m->pf_rows >= rows) return AR_HIP_OK;
     void** bufs[] = {(void**)&m->pf_x, (void**)&m->pf_h, (void**)&m->pf_qkv, (void**)&m->pf_q, (void**)&m->pf_act};
@@ -734,6 +746,15 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
     const size_t per_layer16 = (size_t)m->qkv_dim * dd + dd * qd + 3 * FF * dd;
     AR_TRY(launch_embed_rows(m->embed, c.weight_dtype, d, m->tokens, m->S + 1, T, (int)R, m->pf_x, st));
     const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
+    const int so = prefill_ksplit(m, R, d, qd), sd = prefill_ksplit(m, R, d, F);
+    if ((so > 1 || sd > 1) && m->pf_part_rows < R) {
+        if (m->pf_part) AR_TRY(ar_ctx_free(m->ctx, m->pf_part));
+        m->pf_part = nullptr;
+        m->pf_part_rows = 0;
+        AR_TRY(ar_ctx_alloc(m->ctx, (size_t)kMaxKSplit * R * d * 4, (void**)&m->pf_part));
+        m->pf_part_rows = R;
+    }
+    int pending = 0;  // k-slices of the last residual projection not yet added into pf_x
     for (int l = 0; l < c.layer_count; l++) {
         const Layer& L = m->layers[l];
         const uint16_t* w16 = m->pf_w16 + per_layer16 * l;
@@ -742,7 +763,9 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         const uint16_t* w1_16 = wo16 + dd * qd;
         const uint16_t* w3_16 = w1_16 + FF * dd;
         const uint16_t* w2_16 = w3_16 + FF * dd;
-        AR_TRY(launch_rmsnorm_rows_f16(m->pf_x, L.attn_norm, m->pf_h, (int)R, d, (float)c.epsilon, st));
+        AR_TRY(launch_fold_rmsnorm_rows_f16(m->pf_x, m->pf_part, pending, L.attn_norm, m->pf_h, (int)R, d,
+                                            (float)c.epsilon, st));
+        pending = 0;
         GemmLaunch g;
         g.A = m->pf_h; g.lda = d; g.W = wqkv16; g.ldw = d; g.M = (int)R; g.N = m->qkv_dim; g.K = d;
         g.bias = L.bqkv; g.C = m->pf_qkv; g.ldc = m->qkv_dim; g.epilogue = GEMV_EPI_STORE; g.f16 = true;
@@ -759,8 +782,12 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         GemmLaunch o;
         o.A = m->pf_h; o.lda = qd; o.W = wo16; o.ldw = qd; o.M = (int)R; o.N = d; o.K = qd;
         o.C = m->pf_x; o.ldc = d; o.epilogue = GEMV_EPI_RESIDUAL; o.f16 = true;
+        if (so > 1) {  // k-slices into pf_part, added into pf_x by the next row RMSNorm
+            o.C = m->pf_part; o.epilogue = GEMV_EPI_STORE; o.ksplit = so;
+        }
         AR_TRY(launch_gemm(o, st));
-        AR_TRY(launch_rmsnorm_rows_f16(m->pf_x, L.ffn_norm, m->pf_h, (int)R, d, (float)c.epsilon, st));
+        AR_TRY(launch_fold_rmsnorm_rows_f16(m->pf_x, m->pf_part, so > 1 ? so : 0, L.ffn_norm, m->pf_h, (int)R, d,
+                                            (float)c.epsilon, st));
         GemmLaunch u;
         u.A = m->pf_h; u.lda = d; u.W = w1_16; u.W2 = w3_16; u.ldw = d; u.M = (int)R;
         u.N = F; u.K = d; u.O = m->pf_act; u.ldo = F; u.epilogue = GEMV_EPI_SWIGLU; u.f16 = true;
@@ -768,13 +795,15 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         GemmLaunch dn;
         dn.A = m->pf_act; dn.lda = F; dn.W = w2_16; dn.ldw = F; dn.M = (int)R; dn.N = d; dn.K = F;
         dn.C = m->pf_x; dn.ldc = d; dn.epilogue = GEMV_EPI_RESIDUAL; dn.f16 = true;
+        if (sd > 1) {
+            dn.C = m->pf_part; dn.epilogue = GEMV_EPI_STORE; dn.ksplit = sd;
+            pending = sd;
+        }
         AR_TRY(launch_gemm(dn, st));
     }
     // last prompt row of every sequence -> residual stream of the decode plan, then the final
     // RMSNorm + logits GEMV leaves the greedy keys for the next step
-    for (int b = 0; b < B; b++)
-        AR_HIP_TRY(hipMemcpyAsync(m->x + (size_t)b * d, m->pf_x + ((size_t)b * T + T - 1) * d, (size_t)d * 4,
-                                  hipMemcpyDeviceToDevice, st));
+    AR_TRY(launch_fold_rows(m->pf_x, m->pf_part, pending, R, T - 1, T, B, d, m->x, st));
     AR_HIP_TRY(hipMemsetAsync(m->am_keys, 0, (size_t)B * kArgmaxSlots * 8, st));
     GemvLaunch h;
     h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
