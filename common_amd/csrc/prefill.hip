@@ -108,7 +108,6 @@ struct PrepParams {
     int S, T, p0, heads, kv_heads, hd;
     uint16_t* qb;           // [R][heads*hd] fp16 normalised, rotated queries
     uint16_t* k16;          // [B][KV][Tp][hd] fp16 keys of the prompt rows (for the attention MFMAs)
-    uint16_t* vt16;         // [B][KV][hd][Tp] fp16 values, transposed
     int Tp;
 };
 
@@ -176,7 +175,28 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
     for (int idx = threadIdx.x; idx < kv_dim; idx += blockDim.x) {
         const int g = idx / hd, i = idx - g * hd;
         p.vcache[(((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i] = v[idx];
-        p.vt16[(((size_t)b * p.kv_heads + g) * hd + i) * p.Tp + t] = f2h(v[idx]);
+    }
+}
+
+// fp16 Vᵀ tiles of the prompt rows from the fp32 V cache: block (tile of 64 rows, KV head, sequence)
+// reads 64 contiguous cache rows and writes 64 contiguous keys per hd row through LDS (rows past
+// the prompt are written as 0).
+template <int HD>
+__global__ __launch_bounds__(256) void vt16_kernel(const float* vcache, int S, int p0, int T, int kv_heads,
+                                                   uint16_t* vt16, int Tp) {
+    __shared__ float tile[64][HD + 1];
+    const int t0 = blockIdx.x * 64, g = blockIdx.y, b = blockIdx.z;
+    const size_t head = (size_t)b * kv_heads + g;
+    const float* src = vcache + (head * S + p0) * HD;
+    for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
+        const int r = idx / HD, i = idx - r * HD;
+        tile[r][i] = t0 + r < T ? src[(size_t)(t0 + r) * HD + i] : 0.f;
+    }
+    __syncthreads();
+    uint16_t* dst = vt16 + head * HD * Tp + t0;
+    for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
+        const int i = idx / 64, r = idx - i * 64;
+        dst[(size_t)i * Tp + r] = f2h(tile[r][i]);
     }
 }
 
@@ -443,8 +463,21 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     p.qkv = a.qkv; p.qkv_stride = a.qkv_stride; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.eps = a.eps;
     p.per_head = a.per_head; p.rope_tab = a.rope_tab; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.S;
     p.T = a.T; p.p0 = a.p0; p.heads = a.heads; p.kv_heads = a.kv_heads; p.hd = a.hd; p.qb = a.qb;
-    p.k16 = a.k16; p.vt16 = a.vt16; p.Tp = a.Tp;
+    p.k16 = a.k16; p.Tp = a.Tp;
     hipLaunchKernelGGL(qk_prep_kernel, dim3(a.B * a.T), dim3(256), 0, stream, p);
+    AR_LAUNCH_CHECK();
+    AR_CHECK_ARG(a.Tp % 64 == 0 && a.Tp >= a.T, "qk prep: Vᵀ rows %d not a multiple of 64 covering %d", a.Tp, a.T);
+    const dim3 vgrid((a.T + 63) / 64, a.kv_heads, a.B);
+    if (a.hd == 128)
+        hipLaunchKernelGGL(vt16_kernel<128>, vgrid, dim3(256), 0, stream, a.vcache, a.S, a.p0, a.T, a.kv_heads, a.vt16,
+                           a.Tp);
+    else if (a.hd == 64)
+        hipLaunchKernelGGL(vt16_kernel<64>, vgrid, dim3(256), 0, stream, a.vcache, a.S, a.p0, a.T, a.kv_heads, a.vt16,
+                           a.Tp);
+    else {
+        ar_set_error("qk prep: head_dim %d not supported (64, 128)", a.hd);
+        return AR_HIP_ERR_INVALID;
+    }
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
