@@ -144,140 +144,74 @@ def c5_section(args):
     from common_amd.qwen3 import Qwen3
 
     B, T, n_dec = C.C5_BATCH, C.C5_PROMPT, C.C5_DECODE
-    cfg = dataclasses.replace(C.C5_4B, seq_len=T + n_dec + 8, max_batch=B)
-    prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=args.seed + 500 + b) for b in range(B)]
-    t0 = time.time()
-    model = Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed + 5))
-    log(f"[bench] C5 weights generated + uploaded in {time.time() - t0:.1f}s")
-    am = model.model
-    am.use_graph(not args.no_graph)
-
-    def start():
-        am.reset()
-        for b, p in enumerate(prompts):
-            am.set_prompt(p, seq=b)
-        model.ctx.synchronize()
-
-    start()
-    am.prefill()  # first call makes the fp16 weight copies and the prefill buffers
-    start()
-    tp = time.perf_counter()
-    am.prefill()
-    t_pre = time.perf_counter() - tp
-    flops = B * prefill_flops(cfg, T)
+    base = dataclasses.replace(C.C5_4B, seq_len=T + n_dec + 8, max_batch=B)
+    prompts = [synthetic.prompt_ids(T, base.vocab_size, seed=args.seed + 500 + b) for b in range(B)]
     warm = 4
-    am.run(warm)
-    model.ctx.synchronize()
-    td = time.perf_counter()
-    toks = am.run(n_dec - warm)
-    t_dec = time.perf_counter() - td
-    model.close()
     steps = n_dec - warm
-    step_bytes = float(np.mean([step_bytes_batch(cfg, p, B) for p in range(T + warm, T + n_dec)]))
+
+    def run(kv_dtype):
+        cfg = dataclasses.replace(base, kv_dtype=kv_dtype)
+        t0 = time.time()
+        model = Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed + 5))
+        log(f"[bench] C5 weights generated + uploaded in {time.time() - t0:.1f}s")
+        am = model.model
+        am.use_graph(not args.no_graph)
+
+        def start():
+            am.reset()
+            for b, p in enumerate(prompts):
+                am.set_prompt(p, seq=b)
+            model.ctx.synchronize()
+
+        start()
+        am.prefill()  # first call makes the fp16 weight copies and the prefill buffers
+        start()
+        tp = time.perf_counter()
+        am.prefill()
+        t_pre = time.perf_counter() - tp
+        am.run(warm)
+        model.ctx.synchronize()
+        td = time.perf_counter()
+        toks = am.run(steps)
+        t_dec = time.perf_counter() - td
+        model.close()
+        kv_b = 2 if kv_dtype == C.DTYPE_F16 else 4
+        step_bytes = float(np.mean([step_bytes_batch(cfg, p, B, kv_b) for p in range(T + warm, T + n_dec)]))
+        dec = {"steps": steps, "tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(1000 * t_dec / steps, 3),
+               "algorithmic_bytes_per_step": round(step_bytes),
+               "hbm_frac": round(step_bytes * steps / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+               "kv_cache": "fp16" if kv_dtype == C.DTYPE_F16 else "fp32"}
+        return t_pre, dec, toks
+
+    t_pre, dec, toks = run(C.DTYPE_F32)
+    flops = B * prefill_flops(base, T)
     out = {
         "workload": "C5: Qwen3-4B shape bf16 weights (d2560, 36L, 32Q/8KV, hd128, F9728, V151936), "
                     f"batch {B} x {T}-token prompts, greedy decode {n_dec}",
         "prefill": {"tokens": B * T, "ms": round(1000 * t_pre, 2), "tok_s": round(B * T / t_pre, 1),
                     "tflop": round(flops / 1e12, 2), "achieved_tflops": round(flops / t_pre / 1e12, 1),
                     "mfma_frac": round(flops / t_pre / 1e12 / MFMA_PEAK_TFLOPS, 4)},
-        "decode": {"steps": steps, "tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(1000 * t_dec / steps, 3),
-                   "algorithmic_bytes_per_step": round(step_bytes),
-                   "hbm_frac": round(step_bytes * steps / t_dec / 1e9 / HBM_PEAK_GBS, 4),
-                   "kv_cache": "fp32"},
+        "decode": dec,
         "distinct_sequences": int(len({tuple(t) for t in toks})),
     }
     log(f"[bench] C5 prefill {B}x{T} tokens: {1000 * t_pre:.1f} ms = {B * T / t_pre:.0f} tok/s, "
-        f"{flops / t_pre / 1e12:.0f} TFLOP/s; decode {out['decode']['tok_s']} tok/s aggregate, "
-        f"{out['decode']['ms_per_step']} ms/step ({100 * out['decode']['hbm_frac']:.1f}% of HBM)")
+        f"{flops / t_pre / 1e12:.0f} TFLOP/s; decode {dec['tok_s']} tok/s aggregate, "
+        f"{dec['ms_per_step']} ms/step ({100 * dec['hbm_frac']:.1f}% of HBM)")
+    if not args.no_fp16_kv:
+        _, dec16, toks16 = run(C.DTYPE_F16)
+        dec16["tokens_equal_fp32_cache"] = int(np.sum(toks16 == toks))
+        dec16["tokens_compared"] = int(toks.size)
+        out["decode_fp16_kv"] = dec16
+        log(f"[bench] C5 decode with an fp16 KV cache: {dec16['tok_s']} tok/s aggregate, {dec16['ms_per_step']} "
+            f"ms/step ({100 * dec16['hbm_frac']:.1f}% of HBM); {dec16['tokens_equal_fp32_cache']}/{toks.size} "
+            f"greedy tokens equal to the fp32-cache run")
     return out
 
 
-def c2_section(args):
-    """the decode-step GQA attention op (16 Q / 8 KV heads, hd 128, cache filled
-    to 4096 rows, query at position 4096) through ar_hip_attention_decode.  Eight caches are used in
-    turn (8 x 33.6 MB > the 256 MB Infinity Cache) so every call streams its cache from HBM."""
-    import numpy as np
-
-    from common_amd import hardware as hw
-
-    H, KV, HD, pos = 16, 8, 128, 4096
-    S = pos + 1
-    ncache, calls = 8, 200
-    r = np.random.default_rng(args.seed + 2)
-    with hw.HipContext() as ctx:
-        caches = []
-        for i in range(ncache):
-            kc = r.standard_normal(KV * S * HD, dtype=np.float32)
-            vc = r.standard_normal(KV * S * HD, dtype=np.float32)
-            caches.append((ctx.to_device(kc), ctx.to_device(vc)))
-        q = ctx.to_device(r.standard_normal(H * HD, dtype=np.float32))
-        k = ctx.to_device(r.standard_normal(KV * HD, dtype=np.float32))
-        v = ctx.to_device(r.standard_normal(KV * HD, dtype=np.float32))
-        qn = ctx.to_device((1 + 0.02 * r.standard_normal(H * HD)).astype(np.float32))
-        kn = ctx.to_device((1 + 0.02 * r.standard_normal(KV * HD)).astype(np.float32))
-        out = ctx.allocate(H * HD * 4)
-
-        def call(i):
-            kc, vc = caches[i % ncache]
-            ctx.attention_decode(q, k, v, qn, kn, 1e-6, 0, kc, vc, S, pos, H, KV, HD, 1e6, out)
-
-        for i in range(2 * ncache):
-            call(i)
-        ctx.synchronize()
-        t = time.perf_counter()
-        for i in range(calls):
-            call(i)
-        ctx.synchronize()
-        us = 1e6 * (time.perf_counter() - t) / calls
-    kv_bytes = 2 * KV * S * HD * 4
-    gbs = kv_bytes / us / 1e3
-    log(f"[bench] C2 attention op: {us:.2f} us/call, {gbs:.0f} GB/s of K/V ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
-    return {"workload": "C2: decode-step GQA attention op, 16Q/8KV heads, hd 128, cache 0..4095 + new row at 4096, fp32",
-            "us_per_call": round(us, 2), "kv_bytes": kv_bytes, "GBs": round(gbs, 1),
-            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "note": "wall time per C-ABI call, including the op's q/k/v staging copies and position upload"}
-
-
-def traffic_probe(args):
-    """Workload for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic: one plain
-    256 MiB device copy (the counter scale: known bytes), then a few eager C3 decode steps, so every
-    launch of the logits GEMV is its own dispatch."""
-    from common_amd import config as C
-    from common_amd import hardware as hw
-    from common_amd import synthetic
-    from common_amd.qwen3 import Qwen3
-
-    nbytes = 256 << 20
-    cfg = C.C3_0_6B
-    prompt = synthetic.prompt_ids(4, cfg.vocab_size, seed=args.seed)
-    with hw.HipContext() as ctx:
-        a, b = ctx.allocate(nbytes), ctx.allocate(nbytes)
-        ctx.copy(b, a, nbytes)
-        ctx.synchronize()
-        with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed), ctx) as model:
-            am = model.model
-            am.use_graph(False)
-            am.reset()
-            am.set_prompt(prompt)
-            am.run(8)
-            ctx.synchronize()
-    print(json.dumps({"traffic_probe": {"copy_bytes": nbytes, "decode_steps": 8}}), flush=True)
-
-
-def load_traffic():
-    """roofline.traffic from the committed rocprofv3 counter summary, when present."""
-    path = os.path.join(ROOT, "profiles", "logits_gemv_traffic.json")
-    try:
-        with open(path) as f:
-            return json.load(f)
-    except (OSError, ValueError):
-        return None
-
-
-def step_bytes_batch(cfg, pos, batch):
+def step_bytes_batch(cfg, pos, batch, kv_bytes=4):
     """Bytes one batched decode step must move at position `pos`: weights once, KV per sequence."""
-    one = algorithmic_bytes_per_token(cfg, pos)
-    kv = cfg.layer_count * 2 * cfg.kv_dim * 4 * (pos + 1)
+    kv = cfg.layer_count * 2 * cfg.kv_dim * kv_bytes * (pos + 1)
+    one = algorithmic_bytes_per_token(cfg, pos) - cfg.layer_count * 2 * cfg.kv_dim * 4 * (pos + 1) + kv
     return one + (batch - 1) * (kv + cfg.dim * 4)
 
 
@@ -293,6 +227,7 @@ def main():
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 prefill/decode section")
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 batch-8 long-context section")
     ap.add_argument("--no-c2", action="store_true", help="skip the config-2 attention-op section")
+    ap.add_argument("--no-fp16-kv", action="store_true", help="skip the config-5 decode run with an fp16 KV cache")
     ap.add_argument("--sections", default="c3,c4,c5,c2",
                     help="comma list of workloads to run (c3 is the headline; the others are extra fields)")
     ap.add_argument("--traffic-probe", action="store_true",

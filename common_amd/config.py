@@ -17,6 +17,7 @@ QK_NORM_PER_HEAD = 1  # one RMS per head (HF Qwen3 semantics)
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2  # KV-cache storage option (kv_dtype)
 
 
 @dataclasses.dataclass(frozen=True)
@@ -34,6 +35,7 @@ class Qwen3Config:
     epsilon: float = 1e-6     # Qwen3.java:397,402
     qk_norm_mode: int = QK_NORM_WHOLE
     weight_dtype: int = DTYPE_F32
+    kv_dtype: int = DTYPE_F32  # KV cache storage: DTYPE_F32 (reference) or DTYPE_F16
     max_batch: int = 1
     qkv_bias: bool = False
 

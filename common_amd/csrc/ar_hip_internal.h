@@ -140,8 +140,9 @@ struct PrefillPrep {
     float eps = 1e-6f;
     int per_head = 0;
     const float2* rope_tab = nullptr;
-    float* kcache = nullptr;
-    float* vcache = nullptr;
+    void* kcache = nullptr;    // [B][KV][S][hd] fp32, or fp16 when kv16
+    void* vcache = nullptr;
+    bool kv16 = false;
     int B = 1, S = 0, T = 0, p0 = 0, heads = 0, kv_heads = 0, hd = 0;
     uint16_t* qb = nullptr;
     uint16_t* k16 = nullptr;   // [B][KV][Tp][hd] fp16 keys of the prompt rows
@@ -163,8 +164,9 @@ struct AttnLaunch {
     const float* k_norm = nullptr;
     float qk_eps = 1e-6f;
     int per_head_norm = 0;
-    float* kcache = nullptr;      // [batch][kv_heads][max_seq][hd]
-    float* vcache = nullptr;
+    void* kcache = nullptr;       // [batch][kv_heads][max_seq][hd], fp32 or fp16 (kv16)
+    void* vcache = nullptr;
+    bool kv16 = false;
     int max_seq = 0;
     const int* pos = nullptr;     // device position (same for every sequence), or null: pos_value
     int pos_value = 0;

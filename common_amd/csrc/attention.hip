@@ -27,6 +27,8 @@
 // With one split the block writes the normalised output; otherwise it writes unnormalised
 // partials (o, max, sum) that attn_combine_kernel merges in the next launch (the kernel boundary
 // makes them visible, so no block needs a device-wide fence).
+#include <type_traits>
+
 #include "ar_hip_internal.h"
 
 namespace {
@@ -45,8 +47,8 @@ struct AttnParams {
     const float* k_norm;
     float qk_eps;
     int per_head_norm;
-    float* kcache;
-    float* vcache;
+    void* kcache;          // fp32, or fp16 for the KV16 instantiation
+    void* vcache;
     int max_seq;
     const int* pos;        // device position, or null: pos_value
     int pos_value;
@@ -102,13 +104,17 @@ __device__ inline void rope_cs(const float2* row, int pos, int f, double c, floa
 }
 
 // NT threads: 256 when the context is cut into splits across blocks, 512 for a context of at most
-// kShortMax rows handled by one block per (sequence, KV head) with no combine launch.
-template <int HD, int G, int NT>
+// kShortMax rows handled by one block per (sequence, KV head) with no combine launch.  KV16: the
+// cache holds fp16 rows (the new row is rounded before it is used, so every step sees exactly the
+// values the cache holds).
+template <int HD, int G, int NT, bool KV16>
 __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
+    using KVT = typename std::conditional<KV16, _Float16, float>::type;
     constexpr int FD = HD / 2;
-    constexpr int EPL = HD / 16;     // dims per lane: a 16-lane group holds one row; lane gl holds dims
-                                     // 64*(e/4) + 4*gl + e%4, so each 16-byte load of the group covers
-                                     // 256 contiguous bytes of the row
+    constexpr int EPL = HD / 16;     // dims per lane: a 16-lane group holds one row; fp32 rows: lane gl
+                                     // holds dims 64*(e/4) + 4*gl + e%4 (each 16-byte load of the group
+                                     // covers 256 contiguous bytes); fp16 rows: dims EPL*gl + e (one
+                                     // load per row)
     constexpr int NGR = NT / 16;     // 16-lane row groups
     constexpr int NWV = NT / 64;     // wavefronts
     constexpr int RU = G >= 8 ? 2 : 4;  // rows per group per chunk (registers: G query fragments)
@@ -171,8 +177,9 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     const int t0 = split * tile;
     const int t1 = min(t0 + tile, n);
     const size_t head_base = ((size_t)b * kvH + kvh) * (size_t)p.max_seq * HD;
-    float* kc = p.kcache + head_base;
-    float* vc = p.vcache + head_base;
+    KVT* kc = reinterpret_cast<KVT*>(p.kcache) + head_base;
+    KVT* vc = reinterpret_cast<KVT*>(p.vcache) + head_base;
+    auto dim_of = [&](int e) { return KV16 ? EPL * gl + e : 16 * (e & ~3) + gl * 4 + (e & 3); };
 
     // ---- rows of the split: group `grp` takes rows t0 + grp + NGR*i (neighbouring groups read
     // neighbouring rows), chunk c = rows i in [c*RU, c*RU + RU).  The first chunk's K and V rows are
@@ -180,14 +187,21 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     // scores are masked below); row `pos` is stale in the cache until this block writes it, so
     // that row is taken from LDS instead.
     float kr[RU][EPL], vr[RU][EPL];
-    auto load_rows = [&](float (&dst)[RU][EPL], const float* src, int c) {
+    auto load_rows = [&](float (&dst)[RU][EPL], const KVT* src, int c) {
 #pragma unroll
         for (int j = 0; j < RU; j++) {
             const int t = min(t0 + grp + NGR * (c * RU + j), t1 - 1);
+            if constexpr (KV16) {
+                typedef _Float16 halfv __attribute__((ext_vector_type(EPL)));
+                const halfv v = *reinterpret_cast<const halfv*>(src + (size_t)t * HD + EPL * gl);
 #pragma unroll
-            for (int e = 0; e < EPL; e += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(src + (size_t)t * HD + 16 * e + gl * 4);
-                dst[j][e] = v.x; dst[j][e + 1] = v.y; dst[j][e + 2] = v.z; dst[j][e + 3] = v.w;
+                for (int e = 0; e < EPL; e++) dst[j][e] = (float)v[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; e += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(src + (size_t)t * HD + 16 * e + gl * 4);
+                    dst[j][e] = v.x; dst[j][e + 1] = v.y; dst[j][e + 2] = v.z; dst[j][e + 3] = v.w;
+                }
             }
         }
     };
@@ -252,15 +266,16 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
                 x1 = (kg1 * x1) * rk_s;
                 x2 = (kg2 * x2) * rk_s;
             }
-            const float o1 = x1 * kcs.x - x2 * kcs.y, o2 = x2 * kcs.x + x1 * kcs.y;
-            k_new[tid] = o1;
-            k_new[tid + FD] = o2;
+            const KVT o1 = (KVT)(x1 * kcs.x - x2 * kcs.y), o2 = (KVT)(x2 * kcs.x + x1 * kcs.y);
+            k_new[tid] = (float)o1;
+            k_new[tid + FD] = (float)o2;
             kc[(size_t)pos * HD + tid] = o1;
             kc[(size_t)pos * HD + tid + FD] = o2;
         }
         if (tid < HD) {
-            v_new[tid] = vnew;
-            vc[(size_t)pos * HD + tid] = vnew;
+            const KVT vv = (KVT)vnew;
+            v_new[tid] = (float)vv;
+            vc[(size_t)pos * HD + tid] = vv;
         }
     }
     __syncthreads();
@@ -275,7 +290,7 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int e = 0; e < EPL; e += 4) {
-            const float4 t = *reinterpret_cast<const float4*>(&q_s[g][16 * e + gl * 4]);
+            const float4 t = *reinterpret_cast<const float4*>(&q_s[g][dim_of(e)]);
             qf[g][e] = t.x * c2; qf[g][e + 1] = t.y * c2; qf[g][e + 2] = t.z * c2; qf[g][e + 3] = t.w * c2;
         }
     float m[G], l[G], acc[G][EPL];
@@ -294,8 +309,8 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
                 if (t0 + grp + NGR * (c * RU + j) == pos)
 #pragma unroll
                     for (int e = 0; e < EPL; e++) {
-                        kr[j][e] = k_new[16 * (e & ~3) + gl * 4 + (e & 3)];
-                        vr[j][e] = v_new[16 * (e & ~3) + gl * 4 + (e & 3)];
+                        kr[j][e] = k_new[dim_of(e)];
+                        vr[j][e] = v_new[dim_of(e)];
                     }
         }
         // scores q . K[t] / sqrt(hd) of the chunk's rows (rows past the split: -inf)
@@ -359,7 +374,7 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
 #pragma unroll
-            for (int e = 0; e < EPL; e++) red_acc[wave][g][16 * (e & ~3) + gl * 4 + (e & 3)] = acc[g][e];
+            for (int e = 0; e < EPL; e++) red_acc[wave][g][dim_of(e)] = acc[g][e];
             if (lane == 0) {
                 red_m[wave][g] = m[g];
                 red_l[wave][g] = l[g];
@@ -447,7 +462,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
     p.out[(size_t)b * p.out_stride + (size_t)h * HD + i] = O / L;
 }
 
-template <int HD, int G>
+template <int HD, int G, bool KV16>
 int launch_t(const AttnLaunch& a, hipStream_t stream) {
     AttnParams p;
     p.q = a.qkv ? a.qkv : a.q;
@@ -463,11 +478,11 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
     if (a.max_splits == 1 && a.max_seq <= kShortMax) {
         // whole context in one block
         constexpr int NT = 512;
-        hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT>), dim3(1, a.kv_heads, a.batch), dim3(NT), 0, stream, p);
+        hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16>), dim3(1, a.kv_heads, a.batch), dim3(NT), 0, stream, p);
         AR_LAUNCH_CHECK();
         return AR_HIP_OK;
     }
-    hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads>), dim3(a.max_splits, a.kv_heads, a.batch),
+    hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16>), dim3(a.max_splits, a.kv_heads, a.batch),
                        dim3(kThreads), 0, stream, p);
     AR_LAUNCH_CHECK();
     if (a.max_splits > 1) {
@@ -477,13 +492,13 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
     return AR_HIP_OK;
 }
 
-template <int HD>
+template <int HD, bool KV16>
 int pick_g(const AttnLaunch& a, hipStream_t s) {
     switch (a.heads / a.kv_heads) {
-        case 1: return launch_t<HD, 1>(a, s);
-        case 2: return launch_t<HD, 2>(a, s);
-        case 4: return launch_t<HD, 4>(a, s);
-        case 8: return launch_t<HD, 8>(a, s);
+        case 1: return launch_t<HD, 1, KV16>(a, s);
+        case 2: return launch_t<HD, 2, KV16>(a, s);
+        case 4: return launch_t<HD, 4, KV16>(a, s);
+        case 8: return launch_t<HD, 8, KV16>(a, s);
     }
     ar_set_error("attention: heads/kv_heads = %d not in {1,2,4,8}", a.heads / a.kv_heads);
     return AR_HIP_ERR_INVALID;
@@ -521,8 +536,8 @@ int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(a.batch >= 1 && a.batch <= 65535, "attention: bad batch %d", a.batch);
     AR_CHECK_ARG((reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.vcache) & 15) == 0,
                  "attention: caches must be 16-byte aligned");
-    if (a.head_dim == 128) return pick_g<128>(a, stream);
-    if (a.head_dim == 64) return pick_g<64>(a, stream);
+    if (a.head_dim == 128) return a.kv16 ? pick_g<128, true>(a, stream) : pick_g<128, false>(a, stream);
+    if (a.head_dim == 64) return a.kv16 ? pick_g<64, true>(a, stream) : pick_g<64, false>(a, stream);
     ar_set_error("attention: head_dim %d not supported (64, 128)", a.head_dim);
     return AR_HIP_ERR_INVALID;
 }

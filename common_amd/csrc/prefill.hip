@@ -103,8 +103,9 @@ struct PrepParams {
     float eps;
     int per_head;
     const float2* rope_tab; // [S][hd/2]
-    float* kcache;          // [B][KV][S][hd]
-    float* vcache;
+    void* kcache;           // [B][KV][S][hd], fp32 or fp16 (kv16)
+    void* vcache;
+    int kv16;
     int S, T, p0, heads, kv_heads, hd;
     uint16_t* qb;           // [R][heads*hd] fp16 normalised, rotated queries
     uint16_t* k16;          // [B][KV][Tp][hd] fp16 keys of the prompt rows (for the attention MFMAs)
@@ -164,33 +165,42 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
             x2 = (p.k_norm[(size_t)g * hd + f + fd] * x2) * s;
         }
         const float2 cs = rope[f];
-        float* kc = p.kcache + (((size_t)b * p.kv_heads + g) * p.S + pos) * hd;
+        const size_t kofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd;
         const float o1 = x1 * cs.x - x2 * cs.y, o2 = x2 * cs.x + x1 * cs.y;
-        kc[f] = o1;
-        kc[f + fd] = o2;
+        if (p.kv16) {
+            reinterpret_cast<uint16_t*>(p.kcache)[kofs + f] = f2h(o1);
+            reinterpret_cast<uint16_t*>(p.kcache)[kofs + f + fd] = f2h(o2);
+        } else {
+            reinterpret_cast<float*>(p.kcache)[kofs + f] = o1;
+            reinterpret_cast<float*>(p.kcache)[kofs + f + fd] = o2;
+        }
         uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
         k16[f] = f2h(o1);
         k16[f + fd] = f2h(o2);
     }
     for (int idx = threadIdx.x; idx < kv_dim; idx += blockDim.x) {
         const int g = idx / hd, i = idx - g * hd;
-        p.vcache[(((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i] = v[idx];
+        const size_t vofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i;
+        if (p.kv16)
+            reinterpret_cast<uint16_t*>(p.vcache)[vofs] = f2h(v[idx]);
+        else
+            reinterpret_cast<float*>(p.vcache)[vofs] = v[idx];
     }
 }
 
 // fp16 Vᵀ tiles of the prompt rows from the fp32 V cache: block (tile of 64 rows, KV head, sequence)
 // reads 64 contiguous cache rows and writes 64 contiguous keys per hd row through LDS (rows past
 // the prompt are written as 0).
-template <int HD>
-__global__ __launch_bounds__(256) void vt16_kernel(const float* vcache, int S, int p0, int T, int kv_heads,
+template <int HD, typename KVT>
+__global__ __launch_bounds__(256) void vt16_kernel(const KVT* vcache, int S, int p0, int T, int kv_heads,
                                                    uint16_t* vt16, int Tp) {
     __shared__ float tile[64][HD + 1];
     const int t0 = blockIdx.x * 64, g = blockIdx.y, b = blockIdx.z;
     const size_t head = (size_t)b * kv_heads + g;
-    const float* src = vcache + (head * S + p0) * HD;
+    const KVT* src = vcache + (head * S + p0) * HD;
     for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
         const int r = idx / HD, i = idx - r * HD;
-        tile[r][i] = t0 + r < T ? src[(size_t)(t0 + r) * HD + i] : 0.f;
+        tile[r][i] = t0 + r < T ? (float)src[(size_t)(t0 + r) * HD + i] : 0.f;
     }
     __syncthreads();
     uint16_t* dst = vt16 + head * HD * Tp + t0;
@@ -462,22 +472,29 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     PrepParams p;
     p.qkv = a.qkv; p.qkv_stride = a.qkv_stride; p.q_norm = a.q_norm; p.k_norm = a.k_norm; p.eps = a.eps;
     p.per_head = a.per_head; p.rope_tab = a.rope_tab; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.S;
+    p.kv16 = a.kv16;
     p.T = a.T; p.p0 = a.p0; p.heads = a.heads; p.kv_heads = a.kv_heads; p.hd = a.hd; p.qb = a.qb;
     p.k16 = a.k16; p.Tp = a.Tp;
     hipLaunchKernelGGL(qk_prep_kernel, dim3(a.B * a.T), dim3(256), 0, stream, p);
     AR_LAUNCH_CHECK();
     AR_CHECK_ARG(a.Tp % 64 == 0 && a.Tp >= a.T, "qk prep: Vᵀ rows %d not a multiple of 64 covering %d", a.Tp, a.T);
     const dim3 vgrid((a.T + 63) / 64, a.kv_heads, a.B);
-    if (a.hd == 128)
-        hipLaunchKernelGGL(vt16_kernel<128>, vgrid, dim3(256), 0, stream, a.vcache, a.S, a.p0, a.T, a.kv_heads, a.vt16,
-                           a.Tp);
-    else if (a.hd == 64)
-        hipLaunchKernelGGL(vt16_kernel<64>, vgrid, dim3(256), 0, stream, a.vcache, a.S, a.p0, a.T, a.kv_heads, a.vt16,
-                           a.Tp);
-    else {
+#define AR_VT16(HDV, T_)                                                                                     \
+    hipLaunchKernelGGL((vt16_kernel<HDV, T_>), vgrid, dim3(256), 0, stream, reinterpret_cast<const T_*>(a.vcache), \
+                       a.S, a.p0, a.T, a.kv_heads, a.vt16, a.Tp)
+    if (a.hd != 128 && a.hd != 64) {
         ar_set_error("qk prep: head_dim %d not supported (64, 128)", a.hd);
         return AR_HIP_ERR_INVALID;
     }
+    if (a.hd == 128 && a.kv16)
+        AR_VT16(128, _Float16);
+    else if (a.hd == 128)
+        AR_VT16(128, float);
+    else if (a.kv16)
+        AR_VT16(64, _Float16);
+    else
+        AR_VT16(64, float);
+#undef AR_VT16
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

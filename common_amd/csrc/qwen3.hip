@@ -64,8 +64,9 @@ struct ar_qwen3 {
     float* attn = nullptr;    // [B][q_dim]
     float* act = nullptr;     // [B][F]
     float* logits = nullptr;  // [B][V]
-    float* kcache = nullptr;  // [L][B][KV][S][hd]
-    float* vcache = nullptr;
+    void* kcache = nullptr;   // [L][B][KV][S][hd], fp32 or fp16 (cfg.kv_dtype)
+    void* vcache = nullptr;
+    size_t kv_elem = 4;
     float* part_o = nullptr;
     float* part_ml = nullptr;
     unsigned long long* am_keys = nullptr;  // [B][kArgmaxSlots] greedy-token keys
@@ -213,7 +214,9 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         AttnLaunch a;
         a.qkv = m->qkv; a.qkv_stride = m->qkv_dim; a.q_norm = L.q_norm; a.k_norm = L.k_norm;
         a.qk_eps = (float)c.epsilon; a.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
-        a.kcache = m->kcache + l * layer_cache; a.vcache = m->vcache + l * layer_cache; a.max_seq = m->S;
+        a.kcache = (char*)m->kcache + l * layer_cache * m->kv_elem;
+        a.vcache = (char*)m->vcache + l * layer_cache * m->kv_elem;
+        a.kv16 = c.kv_dtype == AR_DTYPE_F16; a.max_seq = m->S;
         a.pos = m->state; a.heads = c.head_count; a.kv_heads = c.kv_head_count; a.head_dim = c.head_size;
         a.rope_theta = c.rope_theta; a.rope_tab = m->rope_tab; a.max_splits = m->max_splits; a.part_o = m->part_o;
         a.part_ml = m->part_ml; a.out = m->attn; a.out_stride = m->q_dim; a.batch = B;
@@ -329,6 +332,8 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     AR_CHECK_ARG(c.head_size == 64 || c.head_size == 128, "Qwen3: head size %d not in {64,128}", c.head_size);
     AR_CHECK_ARG(c.max_batch >= 1 && c.max_batch <= 8, "Qwen3: batch %d outside 1..8", c.max_batch);
     AR_CHECK_ARG(c.weight_dtype == AR_DTYPE_F32 || c.weight_dtype == AR_DTYPE_BF16, "Qwen3: bad weight dtype");
+    AR_CHECK_ARG(c.kv_dtype == AR_DTYPE_F32 || c.kv_dtype == AR_DTYPE_F16, "Qwen3: KV cache dtype %d not fp32 / fp16",
+                 c.kv_dtype);
     AR_CHECK_ARG(c.qk_norm_mode == AR_QK_NORM_WHOLE || c.qk_norm_mode == AR_QK_NORM_PER_HEAD, "Qwen3: bad qk-norm mode");
     AR_CHECK_ARG(c.dim % 8 == 0 && c.hidden_dim % 8 == 0, "Qwen3: dim and hidden dim must be multiples of 8");
     auto* m = new ar_qwen3();
@@ -340,6 +345,7 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     m->B = c.max_batch;
     m->S = c.seq_len;
     m->wbytes = c.weight_dtype == AR_DTYPE_BF16 ? 2 : 4;
+    m->kv_elem = c.kv_dtype == AR_DTYPE_F16 ? 2 : 4;
     m->layers.resize(c.layer_count);
     m->prompt_set.assign(m->B, 0);
     m->max_splits = attention_max_splits(m->S, c.kv_head_count, m->B);
@@ -428,8 +434,8 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     ALLOC(attn, B * m->q_dim * 4);
     ALLOC(act, B * F * 4);
     ALLOC(logits, B * V * 4);
-    ALLOC(kcache, cache * 4);
-    ALLOC(vcache, cache * 4);
+    ALLOC(kcache, cache * m->kv_elem);
+    ALLOC(vcache, cache * m->kv_elem);
     ALLOC(part_o, attention_partial_floats(m->B, c.head_count, m->max_splits, c.head_size) * 4);
     ALLOC(part_ml, B * c.head_count * m->max_splits * 2 * 4);
     ALLOC(am_keys, B * kArgmaxSlots * 8);
@@ -773,7 +779,9 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         PrefillPrep pp;
         pp.qkv = m->pf_qkv; pp.qkv_stride = m->qkv_dim; pp.q_norm = L.q_norm; pp.k_norm = L.k_norm;
         pp.eps = (float)c.epsilon; pp.per_head = c.qk_norm_mode == AR_QK_NORM_PER_HEAD; pp.rope_tab = m->rope_tab;
-        pp.kcache = m->kcache + l * layer_cache; pp.vcache = m->vcache + l * layer_cache; pp.B = B; pp.S = m->S;
+        pp.kcache = (char*)m->kcache + l * layer_cache * m->kv_elem;
+        pp.vcache = (char*)m->vcache + l * layer_cache * m->kv_elem;
+        pp.kv16 = c.kv_dtype == AR_DTYPE_F16; pp.B = B; pp.S = m->S;
         pp.T = T; pp.p0 = 0; pp.heads = c.head_count; pp.kv_heads = c.kv_head_count; pp.hd = c.head_size;
         pp.qb = m->pf_q; pp.k16 = m->pf_k16; pp.vt16 = m->pf_vt16; pp.Tp = m->pf_tp;
         AR_TRY(launch_qk_prep(pp, st));

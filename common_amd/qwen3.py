@@ -22,13 +22,13 @@ KT_NONE, KT_LOGITS, KT_GATE_UP, KT_QKV, KT_ATTENTION, KT_DOWN, KT_O = range(7)
 class _Cfg(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "dim", "hidden_dim", "layer_count", "head_count", "kv_head_count", "head_size", "vocab_size", "seq_len",
-        "max_batch", "weight_dtype", "qk_norm_mode", "shared_weights", "qkv_bias", "reserved")] + [
+        "max_batch", "weight_dtype", "qk_norm_mode", "shared_weights", "qkv_bias", "kv_dtype")] + [
         ("rope_theta", ctypes.c_double), ("epsilon", ctypes.c_double)]
 
 
 def native_cfg(c: Qwen3Config) -> _Cfg:
     return _Cfg(c.dim, c.hidden_dim, c.layer_count, c.head_count, c.kv_head_count, c.head_size, c.vocab_size,
-                c.seq_len, c.max_batch, c.weight_dtype, c.qk_norm_mode, int(c.shared_weights), int(c.qkv_bias), 0,
+                c.seq_len, c.max_batch, c.weight_dtype, c.qk_norm_mode, int(c.shared_weights), int(c.qkv_bias), c.kv_dtype,
                 c.rope_theta, c.epsilon)
 
 

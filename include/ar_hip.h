@@ -30,6 +30,7 @@ extern "C" {
 /* ---- element types ---------------------------------------------------------------- */
 #define AR_DTYPE_F32 0
 #define AR_DTYPE_BF16 1
+#define AR_DTYPE_F16 2   /* KV-cache storage option (ar_qwen3_cfg.kv_dtype) */
 
 /* ---- QK-norm grouping ------------------------------------------------------------- */
 #define AR_QK_NORM_WHOLE 0    /* one RMS over the whole q / k vector (AttentionFeatures.java:840-845, :886-891) */
@@ -145,7 +146,9 @@ typedef struct ar_qwen3_cfg {
     int32_t qk_norm_mode;  /* AR_QK_NORM_WHOLE (reference) or AR_QK_NORM_PER_HEAD */
     int32_t shared_weights;/* tied embeddings: logits use model.embed_tokens.weight */
     int32_t qkv_bias;      /* q/k/v projection biases present */
-    int32_t reserved;
+    int32_t kv_dtype;      /* KV-cache storage: AR_DTYPE_F32 (0, default: the reference keeps the cache at
+                              the context precision) or AR_DTYPE_F16 (half the per-step cache bytes of
+                              long-context decode; scores and softmax stay fp32) */
     double rope_theta;
     double epsilon;        /* RMSNorm eps (1e-6, Qwen3.java:397,402); QK-norm uses the same */
 } ar_qwen3_cfg;

@@ -197,3 +197,55 @@ def test_prefill_c5_shape_batch8_matches_sequential_decode(ctx):
         top = np.sort(ls[b])[-2:]
         if (top[1] - top[0]) / abs(top[1]) > BF16_TOL:
             assert after_prefill[b, 0] == after_seq[b, 0], b
+
+
+@pytest.mark.parametrize("prefill", [True, False])
+def test_fp16_kv_cache_matches_oracle(ctx, prefill):
+    """kv_dtype = fp16 (half the cache bytes): prompt by prefill or token by token, then greedy decode;
+    logits within the bf16 north-star tolerance of the FP64 oracle, continuations checked until
+    the oracle's top-2 margin falls inside the tolerance."""
+    cfg = _bf16_cfg(C.C1_TINY, head_count=8, kv_head_count=2, head_size=64, seq_len=120, max_batch=2,
+                    kv_dtype=C.DTYPE_F16)
+    sd = synthetic.state_dict(cfg, seed=9)
+    T, steps = 70, 6
+    prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=60 + b) for b in range(2)]
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        if prefill:
+            lp = am.prefill(return_logits=True)
+        else:
+            am.run(T - 1)
+            _, lp = am.next(return_logits=True)
+        toks = am.run(steps)
+    for b, p in enumerate(prompts):
+        rf, rl = oracle.OracleQwen3(cfg, sd, precision="fp64").generate(p, steps)
+        assert rel_err(lp[b], rl[T - 1]) <= BF16_TOL, b
+        for s in range(steps):
+            top = np.sort(rl[T - 1 + s])[-2:]
+            if (top[1] - top[0]) / abs(top[1]) < BF16_TOL:
+                break
+            assert toks[b, s] == rf[T + s], (b, s)
+
+
+def test_fp16_kv_cache_c5_layer_shape_close_to_fp32_cache(ctx):
+    """C5 layer shape (32 Q / 8 KV heads, hd 128), batch 8 decode after a 512-token prefill: the fp16
+    cache gives logits within the bf16 tolerance of the fp32 cache."""
+    T = 512
+    base = dataclasses.replace(C.C5_4B, layer_count=2, seq_len=T + 8, max_batch=8)
+    prompts = [synthetic.prompt_ids(T, base.vocab_size, seed=70 + b) for b in range(8)]
+    out = {}
+    for kv in (C.DTYPE_F32, C.DTYPE_F16):
+        cfg = dataclasses.replace(base, kv_dtype=kv)
+        with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=6), ctx) as m:
+            am = m.model
+            am.reset()
+            for b, p in enumerate(prompts):
+                am.set_prompt(p, seq=b)
+            am.prefill()
+            am.run(3)
+            _, out[kv] = am.next(return_logits=True)
+    for b in range(8):
+        assert rel_err(out[C.DTYPE_F16][b], out[C.DTYPE_F32][b]) <= BF16_TOL, b
