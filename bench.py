@@ -208,6 +208,88 @@ def c5_section(args):
     return out
 
 
+def c2_section(args):
+    """the decode-step GQA attention op (16 Q / 8 KV heads, hd 128, cache filled
+    to 4096 rows, query at position 4096) through ar_hip_attention_decode.  Eight caches are used in
+    turn (8 x 33.6 MB > the 256 MB Infinity Cache) so every call streams its cache from HBM."""
+    import numpy as np
+
+    from common_amd import hardware as hw
+
+    H, KV, HD, pos = 16, 8, 128, 4096
+    S = pos + 1
+    ncache, calls = 8, 200
+    r = np.random.default_rng(args.seed + 2)
+    with hw.HipContext() as ctx:
+        caches = []
+        for i in range(ncache):
+            kc = r.standard_normal(KV * S * HD, dtype=np.float32)
+            vc = r.standard_normal(KV * S * HD, dtype=np.float32)
+            caches.append((ctx.to_device(kc), ctx.to_device(vc)))
+        q = ctx.to_device(r.standard_normal(H * HD, dtype=np.float32))
+        k = ctx.to_device(r.standard_normal(KV * HD, dtype=np.float32))
+        v = ctx.to_device(r.standard_normal(KV * HD, dtype=np.float32))
+        qn = ctx.to_device((1 + 0.02 * r.standard_normal(H * HD)).astype(np.float32))
+        kn = ctx.to_device((1 + 0.02 * r.standard_normal(KV * HD)).astype(np.float32))
+        out = ctx.allocate(H * HD * 4)
+
+        def call(i):
+            kc, vc = caches[i % ncache]
+            ctx.attention_decode(q, k, v, qn, kn, 1e-6, 0, kc, vc, S, pos, H, KV, HD, 1e6, out)
+
+        for i in range(2 * ncache):
+            call(i)
+        ctx.synchronize()
+        t = time.perf_counter()
+        for i in range(calls):
+            call(i)
+        ctx.synchronize()
+        us = 1e6 * (time.perf_counter() - t) / calls
+    kv_bytes = 2 * KV * S * HD * 4
+    gbs = kv_bytes / us / 1e3
+    log(f"[bench] C2 attention op: {us:.2f} us/call, {gbs:.0f} GB/s of K/V ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+    return {"workload": "C2: decode-step GQA attention op, 16Q/8KV heads, hd 128, cache 0..4095 + new row at 4096, fp32",
+            "us_per_call": round(us, 2), "kv_bytes": kv_bytes, "GBs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "note": "wall time per C-ABI call, including the op's q/k/v staging copies and position upload"}
+
+
+def traffic_probe(args):
+    """Workload for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic: one plain
+    256 MiB device copy (the counter scale: known bytes), then a few eager C3 decode steps, so every
+    launch of the logits GEMV is its own dispatch."""
+    from common_amd import config as C
+    from common_amd import hardware as hw
+    from common_amd import synthetic
+    from common_amd.qwen3 import Qwen3
+
+    nbytes = 256 << 20
+    cfg = C.C3_0_6B
+    prompt = synthetic.prompt_ids(4, cfg.vocab_size, seed=args.seed)
+    with hw.HipContext() as ctx:
+        a, b = ctx.allocate(nbytes), ctx.allocate(nbytes)
+        ctx.copy(b, a, nbytes)
+        ctx.synchronize()
+        with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed), ctx) as model:
+            am = model.model
+            am.use_graph(False)
+            am.reset()
+            am.set_prompt(prompt)
+            am.run(8)
+            ctx.synchronize()
+    print(json.dumps({"traffic_probe": {"copy_bytes": nbytes, "decode_steps": 8}}), flush=True)
+
+
+def load_traffic():
+    """roofline.traffic from the committed rocprofv3 counter summary, when present."""
+    path = os.path.join(ROOT, "profiles", "logits_gemv_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def step_bytes_batch(cfg, pos, batch, kv_bytes=4):
     """Bytes one batched decode step must move at position `pos`: weights once, KV per sequence."""
     kv = cfg.layer_count * 2 * cfg.kv_dim * kv_bytes * (pos + 1)

@@ -379,8 +379,9 @@ inline Shape shape_for(int rows, int cols, int batch, int wdtype, int epi) {
     if (s.nb == 1) {
         // enough wavefronts to give each of 256 CUs several, then as many rows per wave as fit
         // (SwiGLU streams two matrices per row: one row pair per wave measured fastest below 8192
-        // rows, 7.0 vs 8.0 us at 2 x 3072 x 1024 fp32)
-        s.rpw = rows >= 8192 ? 4 : (rows >= 2048 && nmat == 1) ? 2 : 1;
+        // rows, 7.0 vs 8.0 us at 2 x 3072 x 1024 fp32; at 2048 rows one row per wave is faster too:
+        // bf16 2048 x 6144 7.8 vs 8.9 us, 2048 x 2048 4.4 vs 4.6 us)
+        s.rpw = rows >= 8192 ? 4 : (rows > 2048 && nmat == 1) ? 2 : 1;
         // ~16 loads in flight per lane: UNR chunks x RPW*NMAT rows
         const int budget = 16 / (s.rpw * nmat);
         const int want = nchunk < budget ? nchunk : budget;
