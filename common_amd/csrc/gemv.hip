@@ -26,6 +26,8 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
     if (a.batch >= 3 && a.wdtype == AR_DTYPE_BF16 && a.cols % 32 == 0)
         return gemv_launch_mfma(p, a.epilogue, stream);
     if (a.batch >= 3) return gemv_launch_batched(p, a.wdtype, a.epilogue, stream);
+    if (gemv_rx_fits(a.rows, a.cols, a.batch, a.wdtype, a.epilogue, a.norm_w != nullptr) && (a.cols * 4) % 16 == 0)
+        return gemv_launch_rx(p, a.wdtype, a.epilogue, stream);
     const gemv::Shape s = gemv::shape_for(a.rows, a.cols, a.batch, a.wdtype, a.epilogue);
     if (a.wdtype == AR_DTYPE_F32) return gemv_launch_f32(p, a.epilogue, s, stream);
     return gemv_launch_bf16(p, a.epilogue, s, stream);

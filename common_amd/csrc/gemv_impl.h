@@ -452,5 +452,8 @@ int gemv_launch_f32(const gemv::Params& p, int epi, const gemv::Shape& s, hipStr
 int gemv_launch_bf16(const gemv::Params& p, int epi, const gemv::Shape& s, hipStream_t st);
 // Batches of 3..8 sequences (gemv_batched.hip): input slices held in registers, 64/NB rows per block.
 int gemv_launch_batched(const gemv::Params& p, int wdtype, int epi, hipStream_t st);
+// Batch 1, no argmax, cols a multiple of the 64-lane chunk (gemv_rx.hip): input held in registers.
+bool gemv_rx_fits(int rows, int cols, int batch, int wdtype, int epi, bool norm);
+int gemv_launch_rx(const gemv::Params& p, int wdtype, int epi, hipStream_t st);
 // bf16 weights, batches of 3..16, cols % 32 == 0 (gemv_mfma.hip): 16-row tiles on the MFMA units.
 int gemv_launch_mfma(const gemv::Params& p, int epi, hipStream_t st);

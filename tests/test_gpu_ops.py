@@ -168,11 +168,22 @@ def test_attention_c2(ctx, per_head):
 
 @pytest.mark.parametrize("heads,kv,hd,max_seq,pos", [
     (4, 2, 64, 48, 0), (4, 2, 64, 48, 1), (4, 2, 64, 48, 47), (16, 8, 128, 384, 200), (32, 8, 128, 8256, 8192),
-    (8, 8, 128, 100, 63), (16, 2, 128, 700, 699)])
+    (8, 8, 128, 100, 63), (16, 2, 128, 700, 699), (8, 8, 128, 1000, 999), (4, 2, 64, 600, 599),
+    (8, 1, 128, 4096, 4000)])
 def test_attention_edges(ctx, heads, kv, hd, max_seq, pos):
+    """One-block form (caches <= 256 rows) and split form with G = 1, 2, 4, 8 query heads per KV
+    head, head_dim 64 and 128, up to 256 splits."""
     out, ref, kg, kr, vg, vr = _attention_case(ctx, heads, kv, hd, max_seq, pos, False, seed=pos + heads)
     assert rel_err(out, ref) <= TOL
     assert rel_err(kg, kr) <= 1e-6
+
+
+def test_attention_consecutive_calls(ctx):
+    """Consecutive calls with different split counts (positions 300, 3000, 17, 3000) reuse the op's
+    split buffers and all match the oracle."""
+    for i, pos in enumerate([300, 3000, 17, 3000]):
+        out, ref, *_ = _attention_case(ctx, 16, 8, 128, 4097, pos, False, seed=40 + i)
+        assert rel_err(out, ref) <= TOL, pos
 
 
 def test_attention_rejects_out_of_range_position(ctx):
