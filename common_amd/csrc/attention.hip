@@ -410,26 +410,29 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
 }
 
 // Merges the split partials of every query head: o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
-// The (m, l) pairs are loaded in parallel into LDS, the weights e^(m_s - M) computed once per
-// split, then every thread sums its column over the splits eight loads at a time.
+// Every load that does not depend on the position (the partial outputs of the first kMergeRegs
+// splits and this thread's (m, l) pair) is issued together with the position load, so the merge
+// costs one memory round trip; splits past kMergeRegs (long contexts) are read afterwards.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
+    constexpr int kMergeRegs = 32;
     __shared__ float w_s[kMaxSplits];
     __shared__ float red[HD / 64];
     const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
     const int lane = i & 63, wave = i >> 6;
+    const size_t slot0 = ((size_t)b * p.heads + h) * p.max_splits;
+    float ov[kMergeRegs];
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; s++) ov[s] = s < p.max_splits ? p.part_o[(slot0 + s) * HD + i] : 0.f;
+    const float2 ml = i < p.max_splits ? reinterpret_cast<const float2*>(p.part_ml)[slot0 + i]
+                                       : make_float2(-INFINITY, 0.f);
     const int pos = p.pos ? *p.pos : p.pos_value;
     if (pos < 0 || pos >= p.max_seq) return;
     int nsplit, tile;
     attn_split_plan(pos + 1, p.max_splits, &nsplit, &tile);
     if (nsplit == 1) return;  // the attention kernel wrote the output itself
-    const size_t slot0 = ((size_t)b * p.heads + h) * p.max_splits;
-    float m_loc = -INFINITY;
-    for (int s = i; s < nsplit; s += HD) {
-        const float m = p.part_ml[(slot0 + s) * 2];
-        w_s[s] = m;
-        m_loc = fmaxf(m_loc, m);
-    }
+    float m_loc = i < nsplit ? ml.x : -INFINITY;
+    for (int s = i + HD; s < nsplit; s += HD) m_loc = fmaxf(m_loc, p.part_ml[(slot0 + s) * 2]);
     m_loc = wave_max(m_loc);
     if (lane == 0) red[wave] = m_loc;
     __syncthreads();
@@ -437,8 +440,13 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
 #pragma unroll
     for (int w = 1; w < HD / 64; w++) M = fmaxf(M, red[w]);
     float l_loc = 0.f;
-    for (int s = i; s < nsplit; s += HD) {
-        const float w = expf(w_s[s] - M);
+    if (i < nsplit) {
+        const float w = expf(ml.x - M);
+        w_s[i] = w;
+        l_loc = fmaf(ml.y, w, l_loc);
+    }
+    for (int s = i + HD; s < nsplit; s += HD) {
+        const float w = expf(p.part_ml[(slot0 + s) * 2] - M);
         w_s[s] = w;
         l_loc = fmaf(p.part_ml[(slot0 + s) * 2 + 1], w, l_loc);
     }
@@ -450,15 +458,10 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
 #pragma unroll
     for (int w = 0; w < HD / 64; w++) L += red[w];
     float O = 0.f;
-    int s = 0;
-    for (; s + 8 <= nsplit; s += 8) {
-        float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = p.part_o[(slot0 + s + u) * HD + i];
-#pragma unroll
-        for (int u = 0; u < 8; u++) O = fmaf(v[u], w_s[s + u], O);
-    }
-    for (; s < nsplit; s++) O = fmaf(p.part_o[(slot0 + s) * HD + i], w_s[s], O);
+    for (int s = 0; s < kMergeRegs; s++)
+        if (s < nsplit) O = fmaf(ov[s], w_s[s], O);
+    for (int s = kMergeRegs; s < nsplit; s++) O = fmaf(p.part_o[(slot0 + s) * HD + i], w_s[s], O);
     p.out[(size_t)b * p.out_stride + (size_t)h * HD + i] = O / L;
 }
 
