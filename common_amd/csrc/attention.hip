@@ -74,20 +74,6 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
-// Block-wide sum of per-thread values; every thread gets the result.
-template <int NT>
-__device__ inline float block_sum(float v, float* scratch) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    v = wave_sum(v);
-    __syncthreads();
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    float t = 0.f;
-#pragma unroll
-    for (int w = 0; w < NT / 64; w++) t += scratch[w];
-    return t;
-}
-
 // (cos, sin) of pos * exp(f * -2 ln(theta) / hd): from the table the model precomputes in
 // double on the host, or evaluated here in double when no table is given.
 __device__ inline void rope_cs(const float2* row, int pos, int f, double c, float* cs, float* sn) {
@@ -106,8 +92,9 @@ __device__ inline void rope_cs(const float2* row, int pos, int f, double c, floa
 // NT threads: 256 when the context is cut into splits across blocks, 512 for a context of at most
 // kShortMax rows handled by one block per (sequence, KV head) with no combine launch.  KV16: the
 // cache holds fp16 rows (the new row is rounded before it is used, so every step sees exactly the
-// values the cache holds).
-template <int HD, int G, int NT, bool KV16>
+// values the cache holds).  TAB: the rotation angles come from the (cos, sin) table, else they
+// are evaluated in double.
+template <int HD, int G, int NT, bool KV16, bool TAB>
 __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     using KVT = typename std::conditional<KV16, _Float16, float>::type;
     constexpr int FD = HD / 2;
@@ -123,7 +110,7 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) float v_new[HD];
     __shared__ __attribute__((aligned(16))) float red_acc[NWV][G][HD];
     __shared__ float red_m[NWV][G], red_l[NWV][G];
-    __shared__ float scratch[NWV];
+    __shared__ float2 sq_s[NWV];
     __shared__ float rq_s[G], rk_s;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -155,17 +142,22 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     const float kg1 = p.k_norm ? p.k_norm[(size_t)kvh * HD + kf] : 1.f;
     const float kg2 = p.k_norm ? p.k_norm[(size_t)kvh * HD + kf + FD] : 1.f;
     const float vnew = v_raw[(size_t)kvh * HD + min(tid, HD - 1)];
-    float sq = 0.f, sk = 0.f;  // this thread's share of sum(q^2), sum(k^2) over the whole vectors
+    // whole-vector QK-norm: this thread's float4 slices of q and k, held in registers (straight-line
+    // loads, so no wait is needed before the position-dependent loads below are issued); vectors
+    // longer than the register slices are finished by a loop after those loads
+    constexpr int SQQ = (8192 / (NT * 4)) > 0 ? 8192 / (NT * 4) : 1;
+    constexpr int SQK = (2048 / (NT * 4)) > 0 ? 2048 / (NT * 4) : 1;
+    float4 wq[SQQ], wk[SQK];
     if (whole_norm) {
-#pragma unroll 4
-        for (int i = tid * 4; i < q_dim; i += NT * 4) {
-            const float4 v = *reinterpret_cast<const float4*>(q_raw + i);
-            sq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+#pragma unroll
+        for (int j = 0; j < SQQ; j++) {
+            const int i = (tid + j * NT) * 4;
+            wq[j] = i < q_dim ? *reinterpret_cast<const float4*>(q_raw + i) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-#pragma unroll 2
-        for (int i = tid * 4; i < kv_dim; i += NT * 4) {
-            const float4 v = *reinterpret_cast<const float4*>(k_raw + i);
-            sk += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+#pragma unroll
+        for (int j = 0; j < SQK; j++) {
+            const int i = (tid + j * NT) * 4;
+            wk[j] = i < kv_dim ? *reinterpret_cast<const float4*>(k_raw + i) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
 
@@ -182,10 +174,10 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     auto dim_of = [&](int e) { return KV16 ? EPL * gl + e : 16 * (e & ~3) + gl * 4 + (e & 3); };
 
     // ---- rows of the split: group `grp` takes rows t0 + grp + NGR*i (neighbouring groups read
-    // neighbouring rows), chunk c = rows i in [c*RU, c*RU + RU).  The first chunk's K and V rows are
-    // issued before anything that depends on the QKV kernel.  Rows are clamped to the split (their
-    // scores are masked below); row `pos` is stale in the cache until this block writes it, so
-    // that row is taken from LDS instead.
+    // neighbouring rows), chunk c = rows i in [c*RU, c*RU + RU).  The rotation row and the first
+    // chunk's K and V rows are issued as soon as the position is known, before anything waits for
+    // the loads above (loads complete in issue order: the rotation is needed first).  Rows are clamped to the split (their scores are masked below); row `pos` is
+    // stale in the cache until this block writes it, so that row is taken from LDS instead.
     float kr[RU][EPL], vr[RU][EPL];
     auto load_rows = [&](float (&dst)[RU][EPL], const KVT* src, int c) {
 #pragma unroll
@@ -205,27 +197,53 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
             }
         }
     };
+    float2 qcs[QPT], kcs;
+    if constexpr (TAB) {  // (cos, sin) row of the position from the table, ahead of the K/V rows
+        const float2* rope_row = p.rope_tab + (size_t)pos * FD;
+#pragma unroll
+        for (int j = 0; j < QPT; j++) qcs[j] = rope_row[min(tid + j * NT, G * FD - 1) % FD];
+        kcs = rope_row[kf];
+    }
     load_rows(kr, kc, 0);
     load_rows(vr, vc, 0);
-    const float2* rope_row = p.rope_tab ? p.rope_tab + (size_t)pos * FD : nullptr;
-    float2 qcs[QPT], kcs;
+    if constexpr (!TAB) {
 #pragma unroll
-    for (int j = 0; j < QPT; j++) {
-        const int idx = min(tid + j * NT, G * FD - 1);
-        rope_cs(rope_row, pos, idx % FD, p.rope_c, &qcs[j].x, &qcs[j].y);
+        for (int j = 0; j < QPT; j++) {
+            const int idx = min(tid + j * NT, G * FD - 1);
+            rope_cs(nullptr, pos, idx % FD, p.rope_c, &qcs[j].x, &qcs[j].y);
+        }
+        rope_cs(nullptr, pos, kf, p.rope_c, &kcs.x, &kcs.y);
     }
-    rope_cs(rope_row, pos, kf, p.rope_c, &kcs.x, &kcs.y);
 
     // ---- QK-norm factors ----------------------------------------------------------
+    float rq_w = 1.f, rk_w = 1.f;  // whole-vector factors (per-head factors go through LDS)
     if (p.q_norm || p.k_norm) {
         if (whole_norm) {
-            sq = block_sum<NT>(sq, scratch);
-            sk = block_sum<NT>(sk, scratch);
-            if (tid == 0) {
-                const float rq = 1.0f / sqrtf(sq / (float)q_dim + p.qk_eps);
-                for (int g = 0; g < G; g++) rq_s[g] = rq;
-                rk_s = 1.0f / sqrtf(sk / (float)kv_dim + p.qk_eps);
+            float sq = 0.f, sk = 0.f;  // this thread's share of sum(q^2), sum(k^2), in index order
+#pragma unroll
+            for (int j = 0; j < SQQ; j++) sq += wq[j].x * wq[j].x + wq[j].y * wq[j].y + wq[j].z * wq[j].z + wq[j].w * wq[j].w;
+            for (int i = (tid + SQQ * NT) * 4; i < q_dim; i += NT * 4) {
+                const float4 v = *reinterpret_cast<const float4*>(q_raw + i);
+                sq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
+#pragma unroll
+            for (int j = 0; j < SQK; j++) sk += wk[j].x * wk[j].x + wk[j].y * wk[j].y + wk[j].z * wk[j].z + wk[j].w * wk[j].w;
+            for (int i = (tid + SQK * NT) * 4; i < kv_dim; i += NT * 4) {
+                const float4 v = *reinterpret_cast<const float4*>(k_raw + i);
+                sk += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            sq = wave_sum(sq);
+            sk = wave_sum(sk);
+            if (lane == 0) sq_s[wave] = make_float2(sq, sk);
+            __syncthreads();
+            float tq = 0.f, tk = 0.f;
+#pragma unroll
+            for (int w = 0; w < NWV; w++) {
+                tq += sq_s[w].x;
+                tk += sq_s[w].y;
+            }
+            rq_w = 1.0f / sqrtf(tq / (float)q_dim + p.qk_eps);
+            rk_w = 1.0f / sqrtf(tk / (float)kv_dim + p.qk_eps);
         } else {
             // wave w reduces heads w, w+4, ...; the k head goes to the last slot
             for (int j = wave; j < G + 1; j += NWV) {
@@ -238,8 +256,8 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
                     if (j < G) rq_s[j] = r; else rk_s = r;
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
 
     // ---- normalised, rotated queries of this group -> LDS ---------------------------
@@ -250,8 +268,9 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
             const int g = idx / FD, f = idx - g * FD;
             float x1 = qx1[j], x2 = qx2[j];
             if (p.q_norm) {
-                x1 = (qg1[j] * x1) * rq_s[g];
-                x2 = (qg2[j] * x2) * rq_s[g];
+                const float r = whole_norm ? rq_w : rq_s[g];
+                x1 = (qg1[j] * x1) * r;
+                x2 = (qg2[j] * x2) * r;
             }
             q_s[g][f] = x1 * qcs[j].x - x2 * qcs[j].y;
             q_s[g][f + FD] = x2 * qcs[j].x + x1 * qcs[j].y;
@@ -263,8 +282,9 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
         if (tid < FD) {
             float x1 = kx1, x2 = kx2;
             if (p.k_norm) {
-                x1 = (kg1 * x1) * rk_s;
-                x2 = (kg2 * x2) * rk_s;
+                const float r = whole_norm ? rk_w : rk_s;
+                x1 = (kg1 * x1) * r;
+                x2 = (kg2 * x2) * r;
             }
             const KVT o1 = (KVT)(x1 * kcs.x - x2 * kcs.y), o2 = (KVT)(x2 * kcs.x + x1 * kcs.y);
             k_new[tid] = (float)o1;
@@ -481,12 +501,15 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
     if (a.max_splits == 1 && a.max_seq <= kShortMax) {
         // whole context in one block
         constexpr int NT = 512;
-        hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16>), dim3(1, a.kv_heads, a.batch), dim3(NT), 0, stream, p);
+        const dim3 grid(1, a.kv_heads, a.batch);
+        if (p.rope_tab) hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, true>), grid, dim3(NT), 0, stream, p);
+        else hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, false>), grid, dim3(NT), 0, stream, p);
         AR_LAUNCH_CHECK();
         return AR_HIP_OK;
     }
-    hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16>), dim3(a.max_splits, a.kv_heads, a.batch),
-                       dim3(kThreads), 0, stream, p);
+    const dim3 grid(a.max_splits, a.kv_heads, a.batch);
+    if (p.rope_tab) hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, false>), grid, dim3(kThreads), 0, stream, p);
     AR_LAUNCH_CHECK();
     if (a.max_splits > 1) {
         hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.heads, a.batch), dim3(HD), 0, stream, p);
