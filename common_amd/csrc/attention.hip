@@ -93,8 +93,8 @@ __device__ inline void rope_cs(const float2* row, int pos, int f, double c, floa
 // kShortMax rows handled by one block per (sequence, KV head) with no combine launch.  KV16: the
 // cache holds fp16 rows (the new row is rounded before it is used, so every step sees exactly the
 // values the cache holds).  TAB: the rotation angles come from the (cos, sin) table, else they
-// are evaluated in double.
-template <int HD, int G, int NT, bool KV16, bool TAB>
+// are evaluated in double.  RU0: K/V rows per 16-lane group per chunk.
+template <int HD, int G, int NT, bool KV16, bool TAB, int RU0>
 __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     using KVT = typename std::conditional<KV16, _Float16, float>::type;
     constexpr int FD = HD / 2;
@@ -104,7 +104,10 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
                                      // load per row)
     constexpr int NGR = NT / 16;     // 16-lane row groups
     constexpr int NWV = NT / 64;     // wavefronts
-    constexpr int RU = G >= 8 ? 2 : 4;  // rows per group per chunk (registers: G query fragments)
+    // rows per group per chunk: RU0, chosen from the longest split (a chunk of NGR * RU rows covers
+    // it; 16-row splits take one row per group, no clamped duplicate loads); at most 2 for G >= 8
+    // (registers: G query fragments)
+    constexpr int RU = (G >= 8 && RU0 > 2) ? 2 : RU0;
     __shared__ __attribute__((aligned(16))) float q_s[G][HD];
     __shared__ __attribute__((aligned(16))) float k_new[HD];
     __shared__ __attribute__((aligned(16))) float v_new[HD];
@@ -502,14 +505,31 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
         // whole context in one block
         constexpr int NT = 512;
         const dim3 grid(1, a.kv_heads, a.batch);
-        if (p.rope_tab) hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, true>), grid, dim3(NT), 0, stream, p);
-        else hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, false>), grid, dim3(NT), 0, stream, p);
+        if (p.rope_tab) hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, true, 4>), grid, dim3(NT), 0, stream, p);
+        else hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, false, 4>), grid, dim3(NT), 0, stream, p);
         AR_LAUNCH_CHECK();
         return AR_HIP_OK;
     }
     const dim3 grid(a.max_splits, a.kv_heads, a.batch);
-    if (p.rope_tab) hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true>), grid, dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, false>), grid, dim3(kThreads), 0, stream, p);
+    // longest split of this launch: of the live context when the position is given, else of any
+    // position the cache holds (attn_split_plan: splits of <= 16 rows until max_splits are in use)
+    int longest;
+    if (a.pos) {
+        longest = (a.max_seq + a.max_splits - 1) / a.max_splits;
+        if (longest < kAttnMinTile) longest = kAttnMinTile;
+    } else {
+        int ns;
+        attn_split_plan(a.pos_value + 1, a.max_splits, &ns, &longest);
+    }
+    constexpr int NGR = kThreads / 16;
+    if (p.rope_tab && longest <= NGR)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true, 1>), grid, dim3(kThreads), 0, stream, p);
+    else if (p.rope_tab && longest <= 2 * NGR)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true, 2>), grid, dim3(kThreads), 0, stream, p);
+    else if (p.rope_tab)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true, 4>), grid, dim3(kThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, false, 4>), grid, dim3(kThreads), 0, stream, p);
     AR_LAUNCH_CHECK();
     if (a.max_splits > 1) {
         hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.heads, a.batch), dim3(HD), 0, stream, p);

@@ -163,6 +163,23 @@ def test_c3_first_steps_vs_oracle(ctx):
     assert rel_err(logits[0], rl) <= LOGIT_TOL_F32
 
 
+@pytest.mark.parametrize("seq_len", [3000, 4500])
+def test_long_context_split_attention(ctx, seq_len):
+    """Caches long enough that the decode step cuts the context into up to 128 splits of up to 24 /
+    36 rows (two / four K-V rows per 16-lane group per chunk; the C3 cache takes one): the whole
+    cache is filled by a prompt of seq_len - 4 tokens, then 4 greedy steps, against the oracle."""
+    cfg = dataclasses.replace(C.C1_TINY, seq_len=seq_len)
+    sd = synthetic.state_dict(cfg, seed=7)
+    prompt = synthetic.prompt_ids(seq_len - 4, cfg.vocab_size, seed=7)
+    ref = oracle.OracleQwen3(cfg, sd, precision="fp32")
+    rf, rl = ref.generate(prompt, 4)
+    ref.close()
+    with Qwen3(cfg, sd, ctx) as m:
+        fed, logits = gpu_generate(m, prompt, 4)
+    assert compare_tokens(fed[0], rf, rl, len(prompt)) == len(rf)
+    assert rel_err(logits[0], rl) <= LOGIT_TOL_F32
+
+
 def test_model_state_errors(ctx, c1):
     cfg, sd, prompt = c1
     with Qwen3(cfg, sd, ctx) as m:
