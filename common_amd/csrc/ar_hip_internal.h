@@ -84,7 +84,35 @@ struct GemvLaunch {
     int epilogue = 0;              // GEMV_EPI_*
     // argmax epilogue: packed (value, index) maxima, [batch][kArgmaxSlots], zero before use
     unsigned long long* keys = nullptr;
+    // bf16 operand planes (MFMA path: batch >= 3, bf16 weights).  x_hi / x_lo [batch][x_stride]:
+    // hi = bf16(g*x), lo = bf16(g*x - hi) of the input (g = norm_w, or 1), written by the kernel
+    // that produced x, so the GEMV does not convert its input; null: converted from x.  y_hi / y_lo
+    // [batch][y_stride]: the same planes of this GEMV's output (the value stored to y) scaled by
+    // y_gain (the next GEMV's RMSNorm gain, or null for 1), for the next GEMV.
+    const uint16_t* x_hi = nullptr;
+    const uint16_t* x_lo = nullptr;
+    uint16_t* y_hi = nullptr;
+    uint16_t* y_lo = nullptr;
+    const float* y_gain = nullptr;
 };
+
+// Splits v into bf16 operand planes: hi = bf16(v) (round to nearest even), lo = bf16(v - hi), so
+// hi + lo keeps 16 significant bits of v.
+__host__ __device__ inline unsigned bf16_rne_bits(float f) {
+    unsigned u;
+    __builtin_memcpy(&u, &f, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u) return (u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__host__ __device__ inline void bf16_planes(float v, uint16_t* hi, uint16_t* lo) {
+    const unsigned h = bf16_rne_bits(v);
+    const unsigned hb = h << 16;
+    float hf;
+    __builtin_memcpy(&hf, &hb, 4);
+    *hi = (uint16_t)h;
+    *lo = (uint16_t)bf16_rne_bits(v - hf);
+}
 
 constexpr int kArgmaxSlots = 1024;
 
@@ -179,6 +207,8 @@ struct AttnLaunch {
     float* part_ml = nullptr;     // [batch][heads][max_splits][2]
     float* out = nullptr;         // [batch][out_stride]
     int out_stride = 0;
+    uint16_t* out_hi = nullptr;   // bf16 planes of out ([batch][out_stride], bf16_planes) for the
+    uint16_t* out_lo = nullptr;   // next GEMV's MFMA path, or null
     int batch = 1;
 };
 
@@ -205,9 +235,11 @@ int attention_max_splits(int max_seq, int kv_heads, int batch);
 // position}.  Position p = next: the token fed is the prompt token tokens[b][p] while p is inside
 // the prompt, else the greedy choice decoded from keys[b] (the previous step's logits), which is
 // also stored at tokens[b][p]; keys are then cleared, x[b] = E[token], current = p, next = p+1.
+// x_hi / x_lo (optional): bf16 planes of x_gain * x (bf16_planes) for the first GEMV's MFMA path.
 // AutoregressiveModel.next + the embedding copy (engine/ml/.../AutoregressiveModel.java:295-308,430).
 int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* tokens, int token_stride,
-                      unsigned long long* keys, int* state, int batch, float* x, int x_stride, hipStream_t stream);
+                      unsigned long long* keys, int* state, int batch, float* x, int x_stride,
+                      uint16_t* x_hi, uint16_t* x_lo, const float* x_gain, hipStream_t stream);
 int launch_rmsnorm(const float* x, const float* w, float* y, int rows, int n, float eps,
                    hipStream_t stream);
 int launch_rope(float* x, int heads, int hd, int pos, double theta, int rows, int row_stride,

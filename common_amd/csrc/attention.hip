@@ -60,6 +60,8 @@ struct AttnParams {
     float* part_ml;
     float* out;
     int out_stride;
+    uint16_t* out_hi;  // bf16 operand planes of out for the next GEMV, or null
+    uint16_t* out_lo;
 };
 
 __device__ inline float wave_sum(float v) {
@@ -420,7 +422,9 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
             o = fmaf(red_acc[w][g][i], wt, o);
         }
         if (nsplit == 1) {
-            p.out[(size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i] = o / L;
+            const size_t oi = (size_t)b * p.out_stride + (size_t)(hbase + g) * HD + i;
+            p.out[oi] = o / L;
+            if (p.out_hi) bf16_planes(o / L, p.out_hi + oi, p.out_lo + oi);
         } else {
             const size_t slot = ((size_t)b * heads + hbase + g) * p.max_splits + split;
             p.part_o[slot * HD + i] = o;
@@ -485,7 +489,9 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
     for (int s = 0; s < kMergeRegs; s++)
         if (s < nsplit) O = fmaf(ov[s], w_s[s], O);
     for (int s = kMergeRegs; s < nsplit; s++) O = fmaf(p.part_o[(slot0 + s) * HD + i], w_s[s], O);
-    p.out[(size_t)b * p.out_stride + (size_t)h * HD + i] = O / L;
+    const size_t oi = (size_t)b * p.out_stride + (size_t)h * HD + i;
+    p.out[oi] = O / L;
+    if (p.out_hi) bf16_planes(O / L, p.out_hi + oi, p.out_lo + oi);
 }
 
 template <int HD, int G, bool KV16>
@@ -500,7 +506,7 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
     p.rope_c = -2.0 * log(a.rope_theta) / (double)HD;
     p.rope_tab = a.rope_tab;
     p.max_splits = a.max_splits; p.part_o = a.part_o; p.part_ml = a.part_ml;
-    p.out = a.out; p.out_stride = a.out_stride;
+    p.out = a.out; p.out_stride = a.out_stride; p.out_hi = a.out_hi; p.out_lo = a.out_lo;
     if (a.max_splits == 1 && a.max_seq <= kShortMax) {
         // whole context in one block
         constexpr int NT = 512;

@@ -23,8 +23,12 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
     p.w = a.w; p.w2 = a.w2; p.rows = a.rows; p.cols = a.cols; p.batch = a.batch;
     p.x = a.x; p.x_stride = a.x_stride; p.norm_w = a.norm_w; p.eps = a.eps; p.bias = a.bias;
     p.y = a.y; p.y_stride = a.y_stride; p.keys = a.keys;
-    if (a.batch >= 3 && a.wdtype == AR_DTYPE_BF16 && a.cols % 32 == 0)
-        return gemv_launch_mfma(p, a.epilogue, stream);
+    p.x_hi = a.x_hi; p.x_lo = a.x_lo; p.y_hi = a.y_hi; p.y_lo = a.y_lo; p.y_gain = a.y_gain;
+    const bool mfma = a.batch >= 3 && a.wdtype == AR_DTYPE_BF16 && a.cols % 32 == 0;
+    AR_CHECK_ARG(mfma || (!a.x_hi && !a.y_hi), "GEMV: operand planes need the MFMA path (batch >= 3, bf16, cols %% 32)");
+    AR_CHECK_ARG(!a.x_hi == !a.x_lo && !a.y_hi == !a.y_lo, "GEMV: operand planes come in hi/lo pairs");
+    AR_CHECK_ARG(!a.y_hi || a.epilogue != GEMV_EPI_ARGMAX, "GEMV: no output planes for the argmax epilogue");
+    if (mfma) return gemv_launch_mfma(p, a.epilogue, stream);
     if (a.batch >= 3) return gemv_launch_batched(p, a.wdtype, a.epilogue, stream);
     if (gemv_rx_fits(a.rows, a.cols, a.batch, a.wdtype, a.epilogue, a.norm_w != nullptr) && (a.cols * 4) % 16 == 0)
         return gemv_launch_rx(p, a.wdtype, a.epilogue, stream);

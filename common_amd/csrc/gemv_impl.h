@@ -40,6 +40,11 @@ struct Params {
     float* y;
     int y_stride;
     unsigned long long* keys;  // argmax: [batch][kArgmaxSlots] packed (value, index) maxima
+    const uint16_t* x_hi;      // operand planes of the input / output (GemvLaunch), MFMA path only
+    const uint16_t* x_lo;
+    uint16_t* y_hi;
+    uint16_t* y_lo;
+    const float* y_gain;
 };
 
 template <typename WT>

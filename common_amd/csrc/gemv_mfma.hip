@@ -71,6 +71,13 @@ __device__ inline void make_planes(float4 a, float4 b, const float* gp, float& s
     lo = u32x4{l[0], l[1], l[2], l[3]};
 }
 
+// sum of squares of 8 inputs added to ss, in the order make_planes adds them
+__device__ inline void sumsq8(float4 a, float4 b, float& ss) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) ss = fmaf(v[j], v[j], ss);
+}
+
 __device__ inline float4 load4(const float* p, bool live) {
     return live ? *reinterpret_cast<const float4*>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
@@ -114,14 +121,20 @@ struct Finish {
         }
         if (!out) return;
         float* yp = p.y + (size_t)b * p.y_stride + row;
+        float val;
         if (EPI == GEMV_EPI_STORE) {
-            *yp = p.bias ? v[0] + p.bias[row] : v[0];
+            val = p.bias ? v[0] + p.bias[row] : v[0];
         } else if (EPI == GEMV_EPI_RESIDUAL) {
-            *yp = *yp + v[0];
+            val = *yp + v[0];
         } else {  // SwiGLU: u * (g * 1/(exp(-g)+1))
             const float g = v[0], u = v[NMAT - 1];
             const float sg = 1.0f / (expf(-g) + 1.0f);
-            *yp = u * (g * sg);
+            val = u * (g * sg);
+        }
+        *yp = val;
+        if (p.y_hi) {  // operand planes of the next GEMV's input
+            const size_t o = (size_t)b * p.y_stride + row;
+            bf16_planes(p.y_gain ? val * p.y_gain[row] : val, p.y_hi + o, p.y_lo + o);
         }
     }
     __device__ static inline void argmax(const gemv::Params& p, const float* tot, int row0, int tile, int tid) {
@@ -169,17 +182,35 @@ __global__ __launch_bounds__(kPersistWaves * 64) void gemv_mfma_persist_kernel(g
     } while (0)
     int t = blockIdx.x;
     if (t < tiles) AR_MFMA_LOAD_TILE(t);  // weights do not depend on x: their latency overlaps the planes
-    // input planes of this wavefront's k-steps, once for all tiles
+    // input planes of this wavefront's k-steps, once for all tiles: read as written by the kernel
+    // that produced the input (the RMSNorm sum of squares still comes from the fp32 input), or
+    // converted here
     u32x4 hv[KS], lv[KS];
     float ss = 0.f;
     {
         const float* xp = p.x + (size_t)min(r, p.batch - 1) * p.x_stride + (size_t)s0 * 32 + 8 * q;
-        const float* gp = norm ? p.norm_w + (size_t)s0 * 32 + 8 * q : nullptr;
+        if (p.x_hi) {
+            const size_t po = (size_t)min(r, p.batch - 1) * p.x_stride + (size_t)s0 * 32 + 8 * q;
+            const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < KS; i++)
-            if (i < ns)
-                make_planes(load4(xp + i * 32, live), load4(xp + i * 32 + 4, live), gp ? gp + i * 32 : nullptr, ss,
-                            hv[i], lv[i]);
+            for (int i = 0; i < KS; i++)
+                if (i < ns) {
+                    hv[i] = live ? *reinterpret_cast<const u32x4*>(p.x_hi + po + i * 32) : zero;
+                    lv[i] = live ? *reinterpret_cast<const u32x4*>(p.x_lo + po + i * 32) : zero;
+                }
+            if (norm) {
+#pragma unroll
+                for (int i = 0; i < KS; i++)
+                    if (i < ns) sumsq8(load4(xp + i * 32, live), load4(xp + i * 32 + 4, live), ss);
+            }
+        } else {
+            const float* gp = norm ? p.norm_w + (size_t)s0 * 32 + 8 * q : nullptr;
+#pragma unroll
+            for (int i = 0; i < KS; i++)
+                if (i < ns)
+                    make_planes(load4(xp + i * 32, live), load4(xp + i * 32 + 4, live), gp ? gp + i * 32 : nullptr,
+                                ss, hv[i], lv[i]);
+        }
     }
     if (norm) {
         ss += __shfl_xor(ss, 16, 64);
@@ -239,19 +270,36 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemv_mfma_stream_kernel(gem
     // two chunk buffers: the next chunk's loads are in flight while the current one is multiplied
     u32x4 wv[2][NMAT][KC];
     float4 xa[2][KC], xb[2][KC];
+    u32x4 ph[2][KC], pl[2][KC];  // operand planes read as written by the input's producer
+    const bool planes = p.x_hi != nullptr;
+    const uint16_t* phs = planes ? p.x_hi + (size_t)min(r, p.batch - 1) * p.x_stride + 8 * q : nullptr;
+    const uint16_t* pls = planes ? p.x_lo + (size_t)min(r, p.batch - 1) * p.x_stride + 8 * q : nullptr;
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
 #define AR_MFMA_LOAD_CHUNK(buf_, sb_)                                                    \
     _Pragma("unroll") for (int i = 0; i < KC; i++) {                                     \
         const int k = min((sb_) + i, s1 - 1) * 32;                                       \
         wv[buf_][0][i] = *reinterpret_cast<const u32x4*>(wa + k);                        \
         if (NMAT == 2) wv[buf_][NMAT - 1][i] = *reinterpret_cast<const u32x4*>(wb + k);  \
-        xa[buf_][i] = load4(xp + k, live);                                               \
-        xb[buf_][i] = load4(xp + k + 4, live);                                           \
+        if (planes) {                                                                    \
+            ph[buf_][i] = live ? *reinterpret_cast<const u32x4*>(phs + k) : zero4;       \
+            pl[buf_][i] = live ? *reinterpret_cast<const u32x4*>(pls + k) : zero4;       \
+        }                                                                                \
+        if (!planes || norm) {                                                           \
+            xa[buf_][i] = load4(xp + k, live);                                           \
+            xb[buf_][i] = load4(xp + k + 4, live);                                       \
+        }                                                                                \
     }
 #define AR_MFMA_MUL_CHUNK(buf_, sb_)                                                                     \
     _Pragma("unroll") for (int i = 0; i < KC; i++) {                                                     \
         if ((sb_) + i < s1) { /* uniform over the wavefront */                                           \
             u32x4 hi, lo;                                                                                \
-            make_planes(xa[buf_][i], xb[buf_][i], gp ? gp + ((sb_) + i) * 32 : nullptr, ss, hi, lo);     \
+            if (planes) {                                                                                \
+                hi = ph[buf_][i];                                                                        \
+                lo = pl[buf_][i];                                                                        \
+                if (norm) sumsq8(xa[buf_][i], xb[buf_][i], ss);                                         \
+            } else {                                                                                     \
+                make_planes(xa[buf_][i], xb[buf_][i], gp ? gp + ((sb_) + i) * 32 : nullptr, ss, hi, lo); \
+            }                                                                                            \
             _Pragma("unroll") for (int m = 0; m < NMAT; m++) acc[m] = mac2(wv[buf_][m][i], hi, lo, acc[m]); \
         }                                                                                                \
     }

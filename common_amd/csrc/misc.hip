@@ -20,7 +20,8 @@ __device__ inline bool better(float v1, int i1, float v2, int i2) {
 template <typename WT>
 __global__ __launch_bounds__(1024) void step_begin_kernel(const WT* table, int dim, int vocab, int* tokens,
                                                          int token_stride, unsigned long long* keys, int* state,
-                                                         int batch, float* x, int x_stride) {
+                                                         int batch, float* x, int x_stride, uint16_t* x_hi,
+                                                         uint16_t* x_lo, const float* x_gain) {
     __shared__ int tok_s[8];
     __shared__ unsigned long long red[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -58,6 +59,7 @@ __global__ __launch_bounds__(1024) void step_begin_kernel(const WT* table, int d
             if constexpr (sizeof(WT) == 2) v = __uint_as_float((unsigned)row[i] << 16);
             else v = row[i];
             x[(size_t)b * x_stride + i] = v;
+            if (x_hi) bf16_planes(x_gain ? v * x_gain[i] : v, x_hi + (size_t)b * x_stride + i, x_lo + (size_t)b * x_stride + i);
         }
     }
     if (tid == 0) {
@@ -178,15 +180,17 @@ int grid_for(size_t n, int threads, int cap = 4096) {
 }  // namespace
 
 int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* tokens, int token_stride,
-                      unsigned long long* keys, int* state, int batch, float* x, int x_stride, hipStream_t stream) {
+                      unsigned long long* keys, int* state, int batch, float* x, int x_stride, uint16_t* x_hi,
+                      uint16_t* x_lo, const float* x_gain, hipStream_t stream) {
     AR_CHECK_ARG(table && tokens && keys && state && x && dim > 0, "step begin: bad arguments");
+    AR_CHECK_ARG(!x_hi == !x_lo, "step begin: operand planes come in hi/lo pairs");
     AR_CHECK_ARG(batch >= 1 && batch <= 8, "step begin: batch %d outside 1..8", batch);
     if (wdtype == AR_DTYPE_BF16)
         hipLaunchKernelGGL(step_begin_kernel<uint16_t>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)table, dim,
-                           vocab, tokens, token_stride, keys, state, batch, x, x_stride);
+                           vocab, tokens, token_stride, keys, state, batch, x, x_stride, x_hi, x_lo, x_gain);
     else
         hipLaunchKernelGGL(step_begin_kernel<float>, dim3(1), dim3(1024), 0, stream, (const float*)table, dim, vocab,
-                           tokens, token_stride, keys, state, batch, x, x_stride);
+                           tokens, token_stride, keys, state, batch, x, x_stride, x_hi, x_lo, x_gain);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

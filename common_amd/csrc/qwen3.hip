@@ -69,6 +69,12 @@ struct ar_qwen3 {
     size_t kv_elem = 4;
     float* part_o = nullptr;
     float* part_ml = nullptr;
+    // bf16 operand planes (hi then lo, [B][width] each) of the inputs of the MFMA-path GEMVs
+    // (batch >= 3, bf16 weights), written by the kernel producing each input: residual stream x
+    // (scaled by the next RMSNorm gain), attention output, SwiGLU output
+    uint16_t* pl_x = nullptr;
+    uint16_t* pl_attn = nullptr;
+    uint16_t* pl_act = nullptr;
     unsigned long long* am_keys = nullptr;  // [B][kArgmaxSlots] greedy-token keys
     float2* rope_tab = nullptr;             // [S][hd/2] (cos, sin), computed in double on the host
     int* tokens = nullptr;    // [B][S+1]
@@ -136,7 +142,7 @@ void release(ar_qwen3* m) {
     if (m->join_ev) hipEventDestroy(m->join_ev);
     if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
+                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
@@ -194,8 +200,15 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         return launch_prefetch(m->arena + r.first, r.second - r.first, m->sink, m->prefetch_blocks, m->pstream);
     };
     if (pf) AR_TRY(prefetch_layer(0, 0));
+    // operand planes: x (width dim), attention output (q_dim), SwiGLU output (F); hi then lo
+    uint16_t* const xh = m->pl_x;
+    uint16_t* const xl = xh ? xh + (size_t)B * dim : nullptr;
+    uint16_t* const ah = m->pl_attn;
+    uint16_t* const al = ah ? ah + (size_t)B * m->q_dim : nullptr;
+    uint16_t* const hh = m->pl_act;
+    uint16_t* const hl = hh ? hh + (size_t)B * F : nullptr;
     AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys, m->state,
-                             B, m->x, dim, st));
+                             B, m->x, dim, xh, xl, m->layers[0].attn_norm, st));
     const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
     for (int l = 0; l < c.layer_count; l++) {
         const Layer& L = m->layers[l];
@@ -207,6 +220,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         // QKV projection with the pre-attention RMSNorm fused in (AttentionFeatures.java:830-900)
         g.w = L.wqkv; g.rows = m->qkv_dim; g.cols = dim; g.x = m->x; g.x_stride = dim; g.norm_w = L.attn_norm;
         g.bias = L.bqkv; g.y = m->qkv; g.y_stride = m->qkv_dim; g.epilogue = GEMV_EPI_STORE;
+        g.x_hi = xh; g.x_lo = xl;
         AR_TRY(timed_begin(AR_KT_QKV));
         AR_TRY(launch_gemv(g, st));
         AR_TRY(timed_end(AR_KT_QKV));
@@ -220,6 +234,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         a.pos = m->state; a.heads = c.head_count; a.kv_heads = c.kv_head_count; a.head_dim = c.head_size;
         a.rope_theta = c.rope_theta; a.rope_tab = m->rope_tab; a.max_splits = m->max_splits; a.part_o = m->part_o;
         a.part_ml = m->part_ml; a.out = m->attn; a.out_stride = m->q_dim; a.batch = B;
+        a.out_hi = ah; a.out_lo = al;
         AR_TRY(timed_begin(AR_KT_ATTENTION));
         AR_TRY(launch_attention_decode(a, st));
         AR_TRY(timed_end(AR_KT_ATTENTION));
@@ -228,6 +243,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         GemvLaunch o;
         o.wdtype = c.weight_dtype; o.batch = B; o.w = L.wo; o.rows = dim; o.cols = m->q_dim; o.x = m->attn;
         o.x_stride = m->q_dim; o.y = m->x; o.y_stride = dim; o.epilogue = GEMV_EPI_RESIDUAL;
+        o.x_hi = ah; o.x_lo = al; o.y_hi = xh; o.y_lo = xl; o.y_gain = L.ffn_norm;
         AR_TRY(timed_begin(AR_KT_O));
         AR_TRY(launch_gemv(o, st));
         AR_TRY(timed_end(AR_KT_O));
@@ -237,6 +253,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         u.wdtype = c.weight_dtype; u.batch = B; u.eps = (float)c.epsilon; u.w = L.w1; u.w2 = L.w3; u.rows = F;
         u.cols = dim; u.x = m->x; u.x_stride = dim; u.norm_w = L.ffn_norm; u.y = m->act; u.y_stride = F;
         u.epilogue = GEMV_EPI_SWIGLU;
+        u.x_hi = xh; u.x_lo = xl; u.y_hi = hh; u.y_lo = hl;
         AR_TRY(timed_begin(AR_KT_GATE_UP));
         AR_TRY(launch_gemv(u, st));
         AR_TRY(timed_end(AR_KT_GATE_UP));
@@ -245,6 +262,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         GemvLaunch d;
         d.wdtype = c.weight_dtype; d.batch = B; d.w = L.w2; d.rows = dim; d.cols = F; d.x = m->act; d.x_stride = F;
         d.y = m->x; d.y_stride = dim; d.epilogue = GEMV_EPI_RESIDUAL;
+        d.x_hi = hh; d.x_lo = hl; d.y_hi = xh; d.y_lo = xl;
+        d.y_gain = l + 1 < c.layer_count ? m->layers[l + 1].attn_norm : m->final_norm;
         AR_TRY(timed_begin(AR_KT_DOWN));
         AR_TRY(launch_gemv(d, st));
         AR_TRY(timed_end(AR_KT_DOWN));
@@ -254,6 +273,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
     h.cols = dim; h.x = m->x; h.x_stride = dim; h.norm_w = m->final_norm; h.y = store_logits ? m->logits : nullptr;
     h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.keys = m->am_keys;
+    h.x_hi = xh; h.x_lo = xl;
     AR_TRY(timed_begin(AR_KT_LOGITS));
     AR_TRY(launch_gemv(h, st));
     AR_TRY(timed_end(AR_KT_LOGITS));
@@ -438,6 +458,11 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     ALLOC(vcache, cache * m->kv_elem);
     ALLOC(part_o, attention_partial_floats(m->B, c.head_count, m->max_splits, c.head_size) * 4);
     ALLOC(part_ml, B * c.head_count * m->max_splits * 2 * 4);
+    if (B >= 3 && c.weight_dtype == AR_DTYPE_BF16 && d % 32 == 0 && m->q_dim % 32 == 0 && F % 32 == 0) {
+        ALLOC(pl_x, (size_t)2 * B * d * 2);
+        ALLOC(pl_attn, (size_t)2 * B * m->q_dim * 2);
+        ALLOC(pl_act, (size_t)2 * B * F * 2);
+    }
     ALLOC(am_keys, B * kArgmaxSlots * 8);
     ALLOC(rope_tab, (size_t)m->S * (c.head_size / 2) * sizeof(float2));
     ALLOC(tokens, B * (m->S + 1) * 4);
