@@ -94,6 +94,13 @@ struct GemvLaunch {
     uint16_t* y_hi = nullptr;
     uint16_t* y_lo = nullptr;
     const float* y_gain = nullptr;
+    // workspace of the MFMA path's k-split form (fewer 16-row tiles than CUs, no RMSNorm, no argmax):
+    // k-slice partial tiles (kpart_floats floats) and one arrival counter per tile (zero between
+    // launches: the block that completes a tile resets it); null: no split
+    float* kpart = nullptr;
+    int kpart_floats = 0;
+    unsigned* kcount = nullptr;
+    int kcount_n = 0;
 };
 
 // Splits v into bf16 operand planes: hi = bf16(v) (round to nearest even), lo = bf16(v - hi), so

@@ -24,6 +24,8 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
     p.x = a.x; p.x_stride = a.x_stride; p.norm_w = a.norm_w; p.eps = a.eps; p.bias = a.bias;
     p.y = a.y; p.y_stride = a.y_stride; p.keys = a.keys;
     p.x_hi = a.x_hi; p.x_lo = a.x_lo; p.y_hi = a.y_hi; p.y_lo = a.y_lo; p.y_gain = a.y_gain;
+    p.kpart = a.kpart; p.kpart_floats = a.kpart_floats; p.kcount = a.kcount; p.kcount_n = a.kcount_n;
+    AR_CHECK_ARG(!a.kpart == !a.kcount, "GEMV: k-split workspace needs both partials and counters");
     const bool mfma = a.batch >= 3 && a.wdtype == AR_DTYPE_BF16 && a.cols % 32 == 0;
     AR_CHECK_ARG(mfma || (!a.x_hi && !a.y_hi), "GEMV: operand planes need the MFMA path (batch >= 3, bf16, cols %% 32)");
     AR_CHECK_ARG(!a.x_hi == !a.x_lo && !a.y_hi == !a.y_lo, "GEMV: operand planes come in hi/lo pairs");

@@ -45,6 +45,10 @@ struct Params {
     uint16_t* y_hi;
     uint16_t* y_lo;
     const float* y_gain;
+    float* kpart;              // k-split workspace of the MFMA streaming form (GemvLaunch), or null
+    int kpart_floats;
+    unsigned* kcount;
+    int kcount_n;
 };
 
 template <typename WT>

@@ -37,6 +37,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kPersistWaves = 8;
 constexpr int kStreamWaves = 16;
 constexpr int kStreamChunk = 2;  // k-steps per load chunk (two chunks in flight)
+constexpr int kMaxKSplit = 4;    // k-slices per tile in the split streaming form
 
 __device__ inline unsigned bf16_bits(float f) {  // round to nearest even; NaN stays NaN
     unsigned u = __float_as_uint(f);
@@ -93,11 +94,7 @@ __device__ inline floatx4 mac2(const u32x4& w, const u32x4& hi, const u32x4& lo,
 // to `tot`, and after a barrier one thread per sequence scans the tile's 16 rows.
 template <int NW, int NMAT, int EPI>
 struct Finish {
-    __device__ static inline void outputs(const gemv::Params& p, float (*cpart)[NMAT][256], float (*ssw)[16],
-                                          bool norm, int row0, int tid, float* tot) {
-        if (tid >= 256) return;
-        const int ri = tid >> 4, b = tid & 15, row = row0 + ri;
-        float v[NMAT];
+    __device__ static inline void sum(float (*cpart)[NMAT][256], int tid, float (&v)[NMAT]) {
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             float t = 0.f;
@@ -105,6 +102,13 @@ struct Finish {
             for (int w = 0; w < NW; w++) t += cpart[w][m][tid];
             v[m] = t;
         }
+    }
+    __device__ static inline void outputs(const gemv::Params& p, float (*cpart)[NMAT][256], float (*ssw)[16],
+                                          bool norm, int row0, int tid, float* tot) {
+        if (tid >= 256) return;
+        const int b = tid & 15;
+        float v[NMAT];
+        sum(cpart, tid, v);
         if (norm) {
             float s = 0.f;
 #pragma unroll
@@ -113,6 +117,11 @@ struct Finish {
 #pragma unroll
             for (int m = 0; m < NMAT; m++) v[m] *= rn;
         }
+        emit(p, v, row0, tid, tot);
+    }
+    // epilogue of output (row0 + tid/16, sequence tid%16) given its finished dot products
+    __device__ static inline void emit(const gemv::Params& p, float (&v)[NMAT], int row0, int tid, float* tot) {
+        const int ri = tid >> 4, b = tid & 15, row = row0 + ri;
         const bool out = row < p.rows && b < p.batch;
         if (EPI == GEMV_EPI_ARGMAX) {
             if (p.y && out) p.y[(size_t)b * p.y_stride + row] = v[0];
@@ -243,18 +252,27 @@ __global__ __launch_bounds__(kPersistWaves * 64) void gemv_mfma_persist_kernel(g
 #undef AR_MFMA_LOAD_TILE
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kStreamWaves * 64) void gemv_mfma_stream_kernel(gemv::Params p, int kpw) {
-    constexpr int NW = kStreamWaves, NMAT = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1, KC = kStreamChunk;
+// NWS wavefronts per block; ks blocks per 16-row tile (block = tile * ks + k-slice), each taking
+// a contiguous share of the k-steps.  With ks > 1 the blocks store their partial tiles in the
+// workspace and the last one to arrive adds the ks partials in k-slice order and applies the
+// epilogue (partials through agent-scope atomic accesses, as the attention merge would need; no
+// device-wide fence).
+template <int EPI, int NWS>
+__global__ __launch_bounds__(NWS * 64, NWS == 8 ? 4 : 1) void gemv_mfma_stream_kernel(gemv::Params p, int kpw, int ks) {
+    constexpr int NW = NWS, NMAT = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1, KC = kStreamChunk;
     using F = Finish<NW, NMAT, EPI>;
     __shared__ float cpart[NW][NMAT][256];
     __shared__ float ssw[NW][16];
     __shared__ float tot[256];
+    __shared__ int last_s;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, q = lane >> 4;
-    const int row0 = blockIdx.x * 16;
+    const int tile = blockIdx.x / ks, kh = blockIdx.x - tile * ks;
+    const int row0 = tile * 16;
     const int nsteps = p.cols / 32;
-    const int s0 = w * kpw, s1 = min(s0 + kpw, nsteps);
+    const int per = (nsteps + ks - 1) / ks;  // k-steps of this block: [kh*per, min((kh+1)*per, nsteps))
+    const int kend = min((kh + 1) * per, nsteps);
+    const int s0 = kh * per + w * kpw, s1 = min(s0 + kpw, kend);
     const bool live = r < p.batch;
     const bool norm = p.norm_w != nullptr;
     const size_t wrow = (size_t)min(row0 + r, p.rows - 1) * p.cols + 8 * q;
@@ -322,11 +340,43 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemv_mfma_stream_kernel(gem
         if (q == 0) ssw[w][r] = ss;
     }
     __syncthreads();
-    F::outputs(p, cpart, ssw, norm, row0, tid, tot);
-    if (EPI == GEMV_EPI_ARGMAX) {
-        __syncthreads();
-        F::argmax(p, tot, row0, blockIdx.x, tid);
+    if (ks == 1) {
+        F::outputs(p, cpart, ssw, norm, row0, tid, tot);
+        if (EPI == GEMV_EPI_ARGMAX) {
+            __syncthreads();
+            F::argmax(p, tot, row0, tile, tid);
+        }
+        return;
     }
+    // k-split (no RMSNorm, no argmax): partial tile -> workspace; the last block of the tile folds
+    float v[NMAT];
+    if (tid < 256) {
+        F::sum(cpart, tid, v);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+            __hip_atomic_store(p.kpart + ((size_t)blockIdx.x * NMAT + m) * 256 + tid, v[m], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+    __syncthreads();
+    if (tid == 0) {
+        unsigned* c = p.kcount + tile;
+        const unsigned prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (unsigned)(ks - 1);
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = last;
+    }
+    __syncthreads();
+    if (!last_s || tid >= 256) return;
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        float t = 0.f;
+        for (int j = 0; j < ks; j++)
+            t += __hip_atomic_load(p.kpart + ((size_t)(tile * ks + j) * NMAT + m) * 256 + tid, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        v[m] = t;
+    }
+    F::emit(p, v, row0, tid, tot);
 }
 
 int persist_blocks() {
@@ -364,8 +414,22 @@ int launch_epi(const gemv::Params& p, hipStream_t st) {
             hipLaunchKernelGGL((gemv_mfma_persist_kernel<EPI, (NMAT == 2 ? 12 : 16)>), grid, block, 0, st, p, kpw_p,
                                tiles);
     } else {
-        const int kpw = (nsteps + kStreamWaves - 1) / kStreamWaves;
-        hipLaunchKernelGGL(gemv_mfma_stream_kernel<EPI>, dim3(tiles), dim3(64 * kStreamWaves), 0, st, p, kpw);
+        // fewer tiles than CUs and nothing that needs the whole row in one block: split k over
+        // ks = 2*CUs / tiles blocks of 8 wavefronts (two per CU), partials folded in order
+        int ks = 1;
+        if (p.kpart && p.kcount && tiles <= p.kcount_n && !p.norm_w && EPI != GEMV_EPI_ARGMAX &&
+            tiles < persist_blocks()) {
+            ks = std::min(kMaxKSplit, std::max(1, 2 * persist_blocks() / tiles));
+            while (ks > 1 && ((long long)tiles * ks * NMAT * 256 > p.kpart_floats || nsteps < ks * 8)) ks--;
+        }
+        if (ks > 1) {
+            const int per = (nsteps + ks - 1) / ks, kpw = (per + 7) / 8;
+            hipLaunchKernelGGL((gemv_mfma_stream_kernel<EPI, 8>), dim3(tiles * ks), dim3(64 * 8), 0, st, p, kpw, ks);
+        } else {
+            const int kpw = (nsteps + kStreamWaves - 1) / kStreamWaves;
+            hipLaunchKernelGGL((gemv_mfma_stream_kernel<EPI, kStreamWaves>), dim3(tiles), dim3(64 * kStreamWaves), 0, st,
+                               p, kpw, 1);
+        }
     }
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;

@@ -75,6 +75,11 @@ struct ar_qwen3 {
     uint16_t* pl_x = nullptr;
     uint16_t* pl_attn = nullptr;
     uint16_t* pl_act = nullptr;
+    // k-split workspace of the batch >= 3 MFMA GEMVs with few row tiles (O, down): partial tiles and
+    // one arrival counter per 16-row tile of the residual stream (kept zero between launches)
+    float* gv_part = nullptr;
+    int gv_part_floats = 0;
+    unsigned* gv_count = nullptr;
     unsigned long long* am_keys = nullptr;  // [B][kArgmaxSlots] greedy-token keys
     float2* rope_tab = nullptr;             // [S][hd/2] (cos, sin), computed in double on the host
     int* tokens = nullptr;    // [B][S+1]
@@ -142,7 +147,7 @@ void release(ar_qwen3* m) {
     if (m->join_ev) hipEventDestroy(m->join_ev);
     if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
+                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
@@ -244,6 +249,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         o.wdtype = c.weight_dtype; o.batch = B; o.w = L.wo; o.rows = dim; o.cols = m->q_dim; o.x = m->attn;
         o.x_stride = m->q_dim; o.y = m->x; o.y_stride = dim; o.epilogue = GEMV_EPI_RESIDUAL;
         o.x_hi = ah; o.x_lo = al; o.y_hi = xh; o.y_lo = xl; o.y_gain = L.ffn_norm;
+        o.kpart = m->gv_part; o.kpart_floats = m->gv_part_floats; o.kcount = m->gv_count;
+        o.kcount_n = m->gv_count ? (dim + 15) / 16 : 0;
         AR_TRY(timed_begin(AR_KT_O));
         AR_TRY(launch_gemv(o, st));
         AR_TRY(timed_end(AR_KT_O));
@@ -264,6 +271,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         d.y = m->x; d.y_stride = dim; d.epilogue = GEMV_EPI_RESIDUAL;
         d.x_hi = hh; d.x_lo = hl; d.y_hi = xh; d.y_lo = xl;
         d.y_gain = l + 1 < c.layer_count ? m->layers[l + 1].attn_norm : m->final_norm;
+        d.kpart = m->gv_part; d.kpart_floats = m->gv_part_floats; d.kcount = m->gv_count;
+        d.kcount_n = m->gv_count ? (dim + 15) / 16 : 0;
         AR_TRY(timed_begin(AR_KT_DOWN));
         AR_TRY(launch_gemv(d, st));
         AR_TRY(timed_end(AR_KT_DOWN));
@@ -462,6 +471,9 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
         ALLOC(pl_x, (size_t)2 * B * d * 2);
         ALLOC(pl_attn, (size_t)2 * B * m->q_dim * 2);
         ALLOC(pl_act, (size_t)2 * B * F * 2);
+        m->gv_part_floats = ((d + 15) / 16) * 4 * 256;  // up to 4 k-slices of every tile
+        ALLOC(gv_part, (size_t)m->gv_part_floats * 4);
+        ALLOC(gv_count, (size_t)((d + 15) / 16) * 4);
     }
     ALLOC(am_keys, B * kArgmaxSlots * 8);
     ALLOC(rope_tab, (size_t)m->S * (c.head_size / 2) * sizeof(float2));
