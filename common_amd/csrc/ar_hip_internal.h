@@ -234,9 +234,9 @@ __host__ __device__ inline void attn_split_plan(int n, int max_splits, int* nspl
 // Attention partials + (when the context is split) the combine kernel.
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);
-// Splits for a cache of max_seq rows: about one block per CU, rows per split <= 256 (one split,
-// no combine, for caches of at most 256 rows).
-int attention_max_splits(int max_seq, int kv_heads, int batch);
+// Splits for a cache of max_seq rows: about one block per CU, rows per split <= 256 (1040 for an
+// fp16 cache; one split, no combine, for caches of at most 256 rows).
+int attention_max_splits(int max_seq, int kv_heads, int batch, bool kv16);
 
 // Start of a decode step (one block).  state = device {current position, prompt length, next
 // position}.  Position p = next: the token fed is the prompt token tokens[b][p] while p is inside

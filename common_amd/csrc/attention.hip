@@ -34,7 +34,10 @@
 namespace {
 
 constexpr int kThreads = 256;   // threads of the split (multi-block) form
-constexpr int kMaxTile = 256;   // rows per split in that form
+constexpr int kMaxTile = 256;   // rows per split in that form (fp32 cache)
+constexpr int kMaxTile16 = 1040; // fp16 cache: the per-row work (fp16 -> fp32 conversions) makes
+                                 // longer splits pay (C5, 8 x 8 KV heads x 8256 rows: 8 splits of
+                                 // 1032 rows 5.55 ms/step vs 33 of 251 rows 6.32)
 constexpr int kShortMax = 256;  // caches up to this many rows: one block per (sequence, KV head)
 constexpr int kMaxSplits = 1024;
 
@@ -562,9 +565,10 @@ size_t attention_partial_floats(int batch, int heads, int max_splits, int hd) {
     return (size_t)batch * heads * max_splits * (size_t)hd;
 }
 
-int attention_max_splits(int max_seq, int kv_heads, int batch) {
+int attention_max_splits(int max_seq, int kv_heads, int batch, bool kv16) {
     if (max_seq <= kShortMax) return 1;  // one block per (sequence, KV head), no combine launch
-    const int need = (max_seq + kMaxTile - 1) / kMaxTile;      // rows per split <= kMaxTile
+    const int tmax = kv16 ? kMaxTile16 : kMaxTile;
+    const int need = (max_seq + tmax - 1) / tmax;                // rows per split <= tmax
     // about one block per CU: each block then streams a tile long enough to amortise its prologue
     // (C2, 4097 rows: 32 splits of 129 rows; 128 splits of 33 rows measured 2.4x slower)
     const int want = (256 + kv_heads * batch - 1) / (kv_heads * batch);
@@ -581,9 +585,10 @@ int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(a.heads > 0 && a.kv_heads > 0 && a.heads % a.kv_heads == 0, "attention: bad head counts %d/%d",
                  a.heads, a.kv_heads);
     AR_CHECK_ARG(a.max_splits <= kMaxSplits, "attention: %d splits exceed %d", a.max_splits, kMaxSplits);
-    AR_CHECK_ARG(a.max_splits >= 1 && ((long long)a.max_splits * kMaxTile >= a.max_seq ||
+    const int tmax = a.kv16 ? kMaxTile16 : kMaxTile;
+    AR_CHECK_ARG(a.max_splits >= 1 && ((long long)a.max_splits * tmax >= a.max_seq ||
                                        (a.max_splits == 1 && a.max_seq <= kShortMax)),
-                 "attention: %d splits of at most %d rows do not cover %d rows", a.max_splits, kMaxTile, a.max_seq);
+                 "attention: %d splits of at most %d rows do not cover %d rows", a.max_splits, tmax, a.max_seq);
     AR_CHECK_ARG(a.max_splits == 1 || (a.part_o && a.part_ml), "attention: missing split buffers");
     AR_CHECK_ARG(a.batch >= 1 && a.batch <= 65535, "attention: bad batch %d", a.batch);
     AR_CHECK_ARG((reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.vcache) & 15) == 0,

@@ -69,7 +69,7 @@ extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const fl
     AR_CHECK_ARG(qk_norm_mode == AR_QK_NORM_WHOLE || qk_norm_mode == AR_QK_NORM_PER_HEAD, "attention: bad qk-norm mode");
     std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnScratch& s = g_attn[ctx];
-    const int max_splits = attention_max_splits(max_seq, kv_heads, 1);
+    const int max_splits = attention_max_splits(max_seq, kv_heads, 1, false);
     AR_TRY(grow(ctx, (void**)&s.part_o, &s.part_floats, attention_partial_floats(1, heads, max_splits, head_dim),
                 sizeof(float)));
     AR_TRY(grow(ctx, (void**)&s.part_ml, &s.ml_floats, (size_t)heads * max_splits * 2, sizeof(float)));

@@ -377,7 +377,7 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     m->kv_elem = c.kv_dtype == AR_DTYPE_F16 ? 2 : 4;
     m->layers.resize(c.layer_count);
     m->prompt_set.assign(m->B, 0);
-    m->max_splits = attention_max_splits(m->S, c.kv_head_count, m->B);
+    m->max_splits = attention_max_splits(m->S, c.kv_head_count, m->B, c.kv_dtype == AR_DTYPE_F16);
 
     // ---- weight arena: every tensor 256-byte aligned --------------------------------
     const size_t d = c.dim, F = c.hidden_dim, V = c.vocab_size, wb = m->wbytes;
