@@ -1,6 +1,6 @@
 """Builds the native libraries in-tree (common_amd/lib/), for gfx950 only.
 
-  libar_hip.so    HIP kernels + C-ABI (hipcc, --offload-arch=gfx950)
+  libar_hip.so    HIP kernels + C-ABI (hipcc, --offload-arch=gfx950) + host-only C++ (g++)
   libar_synth.so  seeded synthetic-input generator (gcc, host only)
 
 Every HIP translation unit is compiled with packed-FP32 instructions disabled.
@@ -53,8 +53,16 @@ def build_hip(jobs: int = 8):
         _run([HIPCC, *HIP_FLAGS, "-I", os.path.join(HERE, "..", "include"), "-c", src, "-o", obj])
         return obj
 
+    def compile_host(src):
+        # host-only C++ (no device code): the host compiler, as its own objects in the library
+        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+        _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(HERE, "..", "include"), "-c", src,
+              "-o", obj])
+        return obj
+
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, srcs))
+        objs += list(ex.map(compile_host, sorted(glob.glob(os.path.join(CSRC, "*.cpp")))))
     out = os.path.join(LIB, "libar_hip.so")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", *objs])
     os.replace(out + ".tmp", out)

@@ -9,6 +9,7 @@ is no Python or CPU fallback, and a missing library raises ``NativeLibraryMissin
 from __future__ import annotations
 
 import ctypes
+import glob
 import os
 import re
 
@@ -25,6 +26,8 @@ AR_HIP_ERR_NOT_FOUND = 5
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
+DTYPE_F64 = 3
 
 GEMM_STORE, GEMM_RESIDUAL, GEMM_SWIGLU = 0, 1, 2
 
@@ -82,6 +85,25 @@ _SIGS = {
     "ar_hip_qwen3_use_prefetch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_gemm_bf16": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4),
+    # include/ar_state_dict.h
+    "ar_hip_state_dict_open": (ctypes.c_int, [ctypes.c_char_p, _c_void_pp]),
+    "ar_hip_state_dict_create": (ctypes.c_int, [_c_void_pp]),
+    "ar_hip_state_dict_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_state_dict_size": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
+    "ar_hip_state_dict_key": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]),
+    "ar_hip_state_dict_contains": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, _c_int_p]),
+    "ar_hip_state_dict_files": (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_int_p]),
+    "ar_hip_state_dict_info": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, _c_int_p,
+                                              ctypes.POINTER(ctypes.c_int32), _c_int_p, _c_int_p,
+                                              ctypes.POINTER(ctypes.c_int64)]),
+    "ar_hip_state_dict_read": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int, ctypes.c_void_p,
+                                              ctypes.c_int64]),
+    "ar_hip_state_dict_put": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32),
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                             ctypes.c_int64]),
+    "ar_hip_state_dict_save": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int]),
+    "ar_hip_qwen3_infer_config": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_qwen3_load_state_dict": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
 }
 
 
@@ -110,11 +132,17 @@ def check(code: int):
 
 
 def declared_symbols(header: str | None = None) -> list[str]:
-    """Names of every function include/ar_hip.h declares."""
+    """Names of every function the C-ABI headers (include/*.h, or one given header) declare."""
     if header is None:
-        header = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "ar_hip.h")
-    text = open(header).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ar_hip_\w+)\s*\(", text, flags=re.M)))
+        inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+        headers = sorted(glob.glob(os.path.join(inc, "*.h")))
+    else:
+        headers = [header]
+    names = set()
+    for h in headers:
+        text = open(h).read()
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ar_hip_\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
 
 
 def device_count() -> int:

@@ -10,6 +10,7 @@ All work happens in the native library (include/ar_hip.h).
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 
 import numpy as np
 
@@ -109,11 +110,29 @@ class Qwen3:
         cfg = native_cfg(config)
         hw.check(hw.lib().ar_hip_qwen3_create(self.ctx.handle, ctypes.byref(cfg), ctypes.byref(h)))
         self.handle = h.value
-        items = state_dict.items() if isinstance(state_dict, dict) else state_dict
-        for key, t in items:
-            self.set_weight(key, t)
+        from .state_dict import StateDictionary
+        if isinstance(state_dict, StateDictionary):
+            # protobuf weights: packed fp32 payloads go from the mapped files to the device
+            hw.check(hw.lib().ar_hip_qwen3_load_state_dict(self.handle, state_dict.handle))
+        else:
+            items = state_dict.items() if isinstance(state_dict, dict) else state_dict
+            for key, t in items:
+                self.set_weight(key, t)
         hw.check(hw.lib().ar_hip_qwen3_finalize(self.handle))
         self.model = AutoregressiveModel(self)
+
+    @classmethod
+    def from_weights_directory(cls, path, config: Qwen3Config | None = None, ctx: hw.HipContext | None = None,
+                               **config_fields) -> "Qwen3":
+        """Qwen3(String weightsDirectory, tokenizerPath, config) (Qwen3.java:154-190): reads the
+        protobuf weights with StateDictionary and, without a config, infers one from the weight
+        shapes (Qwen3.inferConfigFromWeights); ``config_fields`` override fields of the inferred
+        config (e.g. seq_len, max_batch, weight_dtype)."""
+        from .state_dict import StateDictionary
+        with StateDictionary(path) as sd:
+            if config is None:
+                config = dataclasses.replace(sd.infer_config(), **config_fields)
+            return cls(config, sd, ctx)
 
     def set_weight(self, key: str, t: np.ndarray):
         t = np.ascontiguousarray(t, dtype=np.float32)

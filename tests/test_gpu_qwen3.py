@@ -111,6 +111,29 @@ def test_c1_run_matches_next(ctx, c1):
     np.testing.assert_array_equal(toks[0], fed[0])
 
 
+@pytest.mark.parametrize("wdtype", [C.DTYPE_F32, C.DTYPE_BF16])
+def test_c1_from_protobuf_weights_directory(ctx, c1, tmp_path, wdtype):
+    """Qwen3(weightsDirectory) path: weights written in the reference's protobuf layout (one file
+    per layer group, one tensor stored as doubles, an extra key the model does not use), config
+    inferred from the shapes; the run must equal the model built from the same arrays bitwise."""
+    from common_amd.state_dict import DTYPE_F64, StateDictionary, save_split
+    cfg, sd, prompt = c1
+    cfg = dataclasses.replace(cfg, weight_dtype=wdtype)
+    if wdtype == C.DTYPE_BF16:
+        sd = synthetic.state_dict(cfg, seed=0)
+    save_split({k: v for k, v in sd.items() if k != "model.norm.weight"}, tmp_path)
+    with StateDictionary({"model.norm.weight": sd["model.norm.weight"].astype(np.float64),
+                          "unused.extra.weight": np.ones((2, 2))}) as extra:
+        extra.save(tmp_path / "extra", DTYPE_F64)
+    with Qwen3.from_weights_directory(tmp_path, ctx=ctx, seq_len=cfg.seq_len, weight_dtype=wdtype) as m:
+        assert m.config == cfg
+        fed_p, lg_p = gpu_generate(m, prompt, 8)
+    with Qwen3(cfg, sd, ctx) as m:
+        fed_d, lg_d = gpu_generate(m, prompt, 8)
+    np.testing.assert_array_equal(fed_p, fed_d)
+    np.testing.assert_array_equal(lg_p, lg_d)
+
+
 def test_c1_batch_sequences_are_independent(ctx, c1):
     cfg, sd, prompt = c1
     cfg2 = dataclasses.replace(cfg, max_batch=3)
