@@ -257,4 +257,26 @@ int launch_fill_i32(int* dst, int value, size_t n, hipStream_t stream);
 // Reads [p, p+bytes) (16-byte aligned) with `blocks` x 256 threads so it lands in the Infinity Cache.
 int launch_prefetch(const void* p, size_t bytes, unsigned* sink, int blocks, hipStream_t stream);
 
+// Token sampling (sample.hip): AR_SAMPLE_TOKEN = AutoregressiveModel.sampleToken(logits, V,
+// temperature, top_p, random), AR_SAMPLE_MODEL = the sample function of AutoregressiveModel.of.
+// Each of `rows` rows draws once from its java.util.Random state rng[row] (advanced in place);
+// with `state` set (the model's loop state) nothing is drawn unless the next step is past the
+// prompt.  The drawn index goes to out[row] and/or to keys[row * keys_stride] as a key above
+// every greedy key (step_begin feeds it).  `work` holds sample_workspace_bytes(rows, vocab).
+struct SampleLaunch {
+    const float* logits = nullptr;
+    int logits_stride = 0, rows = 0, vocab = 0;
+    int mode = AR_SAMPLE_MODEL;
+    double temperature = 0.0, top_p = 1.0;
+    void* work = nullptr;
+    unsigned long long* rng = nullptr;
+    const int* state = nullptr;
+    unsigned long long* keys = nullptr;
+    int keys_stride = 0;
+    int* out = nullptr;
+};
+bool sample_is_greedy(int mode, double temperature);
+size_t sample_workspace_bytes(int rows, int vocab);
+int launch_sample(const SampleLaunch& s, hipStream_t stream);
+
 void ar_ops_release(ar_hip_ctx* ctx);

@@ -38,12 +38,13 @@ extern "C" int ar_hip_index_of_max(ar_hip_ctx* ctx, const float* x, int rows, in
 }
 
 namespace {
-// Split partials the stand-alone attention op keeps between calls.  Grown on demand; freed with
-// the context's allocations.
+// Workspace the stand-alone ops keep between calls (attention split partials, the sampler's
+// passes).  Grown on demand; freed with the context's allocations.
 struct AttnScratch {
-    size_t part_floats = 0, ml_floats = 0;
+    size_t part_floats = 0, ml_floats = 0, smp_bytes = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
+    void* smp = nullptr;
 };
 std::mutex g_attn_mu;
 std::unordered_map<ar_hip_ctx*, AttnScratch> g_attn;
@@ -80,6 +81,23 @@ extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const fl
     a.head_dim = head_dim; a.rope_theta = rope_theta; a.max_splits = max_splits; a.part_o = s.part_o;
     a.part_ml = s.part_ml; a.out = out; a.out_stride = heads * head_dim; a.batch = 1;
     return launch_attention_decode(a, ctx->stream);
+}
+
+extern "C" int ar_hip_sample(ar_hip_ctx* ctx, const float* logits, int rows, int n, int mode, double temperature,
+                             double top_p, uint64_t* rng_state, int32_t* out) {
+    AR_CHECK_ARG(ctx && logits && out, "sample: null pointer");
+    AR_CHECK_ARG(rows > 0 && n > 0, "sample: empty input");
+    AR_CHECK_ARG(mode == AR_SAMPLE_TOKEN || mode == AR_SAMPLE_MODEL, "sample: unknown mode %d", mode);
+    if (sample_is_greedy(mode, temperature))  // first maximum, no draw (AutoregressiveModel.java:327-337,419-420)
+        return launch_index_of_max(logits, rows, n, out, ctx->stream);
+    AR_CHECK_ARG(rng_state, "sample: null generator state");
+    std::lock_guard<std::mutex> lk(g_attn_mu);
+    AttnScratch& s = g_attn[ctx];
+    AR_TRY(grow(ctx, &s.smp, &s.smp_bytes, sample_workspace_bytes(rows, n), 1));
+    SampleLaunch l;
+    l.logits = logits; l.logits_stride = n; l.rows = rows; l.vocab = n; l.mode = mode; l.temperature = temperature;
+    l.top_p = top_p; l.work = s.smp; l.rng = (unsigned long long*)rng_state; l.out = out;
+    return launch_sample(l, ctx->stream);
 }
 
 // Called from ar_hip_destroy's owner before the context goes away.

@@ -81,6 +81,12 @@ struct ar_qwen3 {
     int gv_part_floats = 0;
     unsigned* gv_count = nullptr;
     unsigned long long* am_keys = nullptr;  // [B][kArgmaxSlots] greedy-token keys
+    // token selection: greedy unless a sampling temperature is set (AR_SAMPLE_*); one
+    // java.util.Random state per sequence, the sampler's workspace allocated on first use
+    int smp_mode = AR_SAMPLE_MODEL;
+    double smp_temperature = 0.0, smp_top_p = 1.0;
+    unsigned long long* smp_rng = nullptr;  // [B]
+    void* smp_work = nullptr;
     float2* rope_tab = nullptr;             // [S][hd/2] (cos, sin), computed in double on the host
     int* tokens = nullptr;    // [B][S+1]
     int* state = nullptr;     // {current position, prompt length, next position}
@@ -147,7 +153,7 @@ void release(ar_qwen3* m) {
     if (m->join_ev) hipEventDestroy(m->join_ev);
     if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
+                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->smp_rng, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
@@ -175,6 +181,16 @@ int invalidate_graphs(ar_qwen3* m) {
 }
 
 // One decode step on the model's stream.
+// The sampler over this step's logits: its draw replaces the greedy key that the next step feeds
+// (only when that step is past the prompt, which the kernel reads from the loop state).
+int enqueue_sample(ar_qwen3* m) {
+    SampleLaunch s;
+    s.logits = m->logits; s.logits_stride = m->cfg.vocab_size; s.rows = m->B; s.vocab = m->cfg.vocab_size;
+    s.mode = m->smp_mode; s.temperature = m->smp_temperature; s.top_p = m->smp_top_p; s.work = m->smp_work;
+    s.rng = m->smp_rng; s.state = m->state; s.keys = m->am_keys; s.keys_stride = kArgmaxSlots;
+    return launch_sample(s, m->ctx->stream);
+}
+
 int enqueue_step(ar_qwen3* m, bool store_logits) {
     const ar_qwen3_cfg& c = m->cfg;
     hipStream_t st = m->ctx->stream;
@@ -280,12 +296,15 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     // final RMSNorm + tied logits + greedy token + advance (Qwen3.java:401-405; AutoregressiveModel.java:412-421)
     GemvLaunch h;
     h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
-    h.cols = dim; h.x = m->x; h.x_stride = dim; h.norm_w = m->final_norm; h.y = store_logits ? m->logits : nullptr;
+    const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
+    h.cols = dim; h.x = m->x; h.x_stride = dim; h.norm_w = m->final_norm;
+    h.y = (store_logits || sampling) ? m->logits : nullptr;
     h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.keys = m->am_keys;
     h.x_hi = xh; h.x_lo = xl;
     AR_TRY(timed_begin(AR_KT_LOGITS));
     AR_TRY(launch_gemv(h, st));
     AR_TRY(timed_end(AR_KT_LOGITS));
+    if (sampling) AR_TRY(enqueue_sample(m));
     if (pf) {  // join the prefetch branch back into the compute stream
         AR_HIP_TRY(hipEventRecord(m->join_ev, m->pstream));
         AR_HIP_TRY(hipStreamWaitEvent(st, m->join_ev, 0));
@@ -476,6 +495,18 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
         ALLOC(gv_count, (size_t)((d + 15) / 16) * 4);
     }
     ALLOC(am_keys, B * kArgmaxSlots * 8);
+    ALLOC(smp_rng, B * 8);
+    {
+        // every sequence starts with new Random(0)
+        std::vector<unsigned long long> st0(B, 0x5DEECE66DULL & ((1ULL << 48) - 1));
+        hipError_t e = hipMemcpyAsync(m->smp_rng, st0.data(), (size_t)B * 8, hipMemcpyHostToDevice, m->ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
+        if (e != hipSuccess) {
+            release(m);
+            ar_set_error("hipMemcpy: %s", hipGetErrorString(e));
+            return AR_HIP_ERR_HIP;
+        }
+    }
     ALLOC(rope_tab, (size_t)m->S * (c.head_size / 2) * sizeof(float2));
     ALLOC(tokens, B * (m->S + 1) * 4);
     ALLOC(state, 64);
@@ -695,6 +726,30 @@ extern "C" int ar_hip_qwen3_use_graph(ar_qwen3* m, int enable) {
     return AR_HIP_OK;
 }
 
+extern "C" int ar_hip_qwen3_set_sampling(ar_qwen3* m, int mode, double temperature, double top_p,
+                                         const int64_t* seeds) {
+    AR_CHECK_ARG(m, "null model");
+    AR_CHECK_ARG(mode == AR_SAMPLE_MODEL || mode == AR_SAMPLE_TOKEN, "unknown sampling mode %d", mode);
+    AR_CHECK_ARG(temperature == temperature && top_p == top_p, "temperature and top_p must not be NaN");
+    hipStream_t st = m->ctx->stream;
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    if (seeds) {
+        std::vector<unsigned long long> states(m->B);
+        for (int b = 0; b < m->B; b++)  // new Random(seed): (seed ^ 0x5DEECE66D) mod 2^48
+            states[b] = ((unsigned long long)seeds[b] ^ 0x5DEECE66DULL) & ((1ULL << 48) - 1);
+        AR_HIP_TRY(hipMemcpyAsync(m->smp_rng, states.data(), states.size() * 8, hipMemcpyHostToDevice, st));
+        AR_HIP_TRY(hipStreamSynchronize(st));
+    }
+    if (!sample_is_greedy(mode, temperature) && !m->smp_work)
+        AR_TRY(ar_ctx_alloc(m->ctx, sample_workspace_bytes(m->B, m->cfg.vocab_size), &m->smp_work));
+    if (mode != m->smp_mode || temperature != m->smp_temperature || top_p != m->smp_top_p)
+        AR_TRY(invalidate_graphs(m));  // the captured step holds the sampler's launches and arguments
+    m->smp_mode = mode;
+    m->smp_temperature = temperature;
+    m->smp_top_p = top_p;
+    return AR_HIP_OK;
+}
+
 extern "C" int ar_hip_qwen3_use_prefetch(ar_qwen3* m, int blocks) {
     AR_CHECK_ARG(m, "null model");
     AR_CHECK_ARG(blocks >= 0 && blocks <= 4096, "prefetch blocks %d outside 0..4096", blocks);
@@ -852,11 +907,14 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
     AR_HIP_TRY(hipMemsetAsync(m->am_keys, 0, (size_t)B * kArgmaxSlots * 8, st));
     GemvLaunch h;
     h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
-    h.cols = d; h.x = m->x; h.x_stride = d; h.norm_w = m->final_norm; h.y = logits_out ? m->logits : nullptr;
+    const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
+    h.cols = d; h.x = m->x; h.x_stride = d; h.norm_w = m->final_norm;
+    h.y = (logits_out || sampling) ? m->logits : nullptr;
     h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.keys = m->am_keys;
     AR_TRY(launch_gemv(h, st));
     const int state[3] = {T - 1, T, T};
     AR_HIP_TRY(hipMemcpyAsync(m->state, state, sizeof(state), hipMemcpyHostToDevice, st));
+    if (sampling) AR_TRY(enqueue_sample(m));  // the first generated token
     if (logits_out)
         AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)B * c.vocab_size * 4, hipMemcpyDeviceToHost, st));
     AR_HIP_TRY(hipStreamSynchronize(st));

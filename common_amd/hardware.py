@@ -30,6 +30,7 @@ DTYPE_F16 = 2
 DTYPE_F64 = 3
 
 GEMM_STORE, GEMM_RESIDUAL, GEMM_SWIGLU = 0, 1, 2
+SAMPLE_MODEL, SAMPLE_TOKEN = 0, 1  # AutoregressiveModel.of's sample function / AutoregressiveModel.sampleToken
 
 _c_void_pp = ctypes.POINTER(ctypes.c_void_p)
 _c_int_p = ctypes.POINTER(ctypes.c_int)
@@ -85,6 +86,10 @@ _SIGS = {
     "ar_hip_qwen3_use_prefetch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_gemm_bf16": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4),
+    "ar_hip_sample": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_double, ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_qwen3_set_sampling": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_double, ctypes.c_double,
+                                                 ctypes.c_void_p]),
     # include/ar_state_dict.h
     "ar_hip_state_dict_open": (ctypes.c_int, [ctypes.c_char_p, _c_void_pp]),
     "ar_hip_state_dict_create": (ctypes.c_int, [_c_void_pp]),
@@ -257,6 +262,12 @@ class HipContext:
     def index_of_max(self, x: DeviceBuffer, rows: int, n: int, out: DeviceBuffer):
         check(lib().ar_hip_index_of_max(self.handle, x.ptr, rows, n, out.ptr))
 
+    def sample(self, logits: DeviceBuffer, rows: int, n: int, mode: int, temperature: float, top_p: float,
+               rng_state: DeviceBuffer | None, out: DeviceBuffer):
+        """One draw per row (ar_hip_sample): rng_state holds rows java.util.Random states (u64)."""
+        check(lib().ar_hip_sample(self.handle, logits.ptr, rows, n, mode, temperature, top_p,
+                                  rng_state.ptr if rng_state else None, out.ptr))
+
     def gemm_bf16(self, A: DeviceBuffer, W: DeviceBuffer, M: int, N: int, K: int, epilogue: int = GEMM_STORE,
                   W2: DeviceBuffer | None = None, bias: DeviceBuffer | None = None, C: DeviceBuffer | None = None,
                   O: DeviceBuffer | None = None):
@@ -268,3 +279,8 @@ class HipContext:
         check(lib().ar_hip_attention_decode(
             self.handle, q.ptr, k.ptr, v.ptr, q_norm.ptr if q_norm else None, k_norm.ptr if k_norm else None,
             qk_eps, qk_norm_mode, k_cache.ptr, v_cache.ptr, max_seq, pos, heads, kv_heads, head_dim, theta, out.ptr))
+
+
+def java_random_state(seed: int) -> int:
+    """The 48-bit state of java.util.Random(seed): (seed ^ 0x5DEECE66D) mod 2^48."""
+    return (int(seed) ^ 0x5DEECE66D) & ((1 << 48) - 1)

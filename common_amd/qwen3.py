@@ -82,6 +82,21 @@ class AutoregressiveModel:
         hw.check(hw.lib().ar_hip_qwen3_hidden(self.handle, out.ctypes.data))
         return out
 
+    def set_temperature(self, temperature: float):
+        """AutoregressiveModel.setTemperature (AutoregressiveModel.java:258-260): 0 is greedy, any
+        other value samples with the sample function of AutoregressiveModel.of (:413-425)."""
+        hw.check(hw.lib().ar_hip_qwen3_set_sampling(self.handle, hw.SAMPLE_MODEL, float(temperature), 1.0, None))
+
+    def set_sampling(self, mode: int, temperature: float, top_p: float = 1.0, seeds=None):
+        """Token selection: hw.SAMPLE_MODEL (the reference model's sample function) or
+        hw.SAMPLE_TOKEN (AutoregressiveModel.sampleToken with top_p); ``seeds`` (one per sequence)
+        reseed the per-sequence java.util.Random generators."""
+        sd = None
+        if seeds is not None:
+            sd = np.ascontiguousarray(np.broadcast_to(np.asarray(seeds, dtype=np.int64), (self.batch,)))
+        hw.check(hw.lib().ar_hip_qwen3_set_sampling(self.handle, int(mode), float(temperature), float(top_p),
+                                                    sd.ctypes.data if sd is not None else None))
+
     def use_graph(self, enable: bool):
         hw.check(hw.lib().ar_hip_qwen3_use_graph(self.handle, int(enable)))
 

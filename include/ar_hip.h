@@ -115,6 +115,24 @@ int ar_hip_attention_decode(ar_hip_ctx *ctx, const float *q, const float *k, con
                             float *k_cache, float *v_cache, int max_seq, int pos, int heads,
                             int kv_heads, int head_dim, double rope_theta, float *out);
 
+/* Token sampling, one draw per row of `rows` logit vectors of n (device, fp32), in double:
+ *   AR_SAMPLE_TOKEN: AutoregressiveModel.sampleToken(logits, n, temperature, top_p, random)
+ *     (engine/ml/.../AutoregressiveModel.java:323-386): softmax of logits / temperature, nucleus
+ *     filtering when top_p < 1 (shortest prefix in descending order, ties by index, whose sum
+ *     reaches top_p; renormalised), then the first index whose running sum exceeds
+ *     r = random.nextDouble();
+ *   AR_SAMPLE_MODEL: the sample function AutoregressiveModel.of installs (:413-425): logits /
+ *     temperature, DistributionFeatures.softmax (compute/stats/.../DistributionFeatures.java:129-141;
+ *     a value equal to 0 stays 0), then sampleToken(probabilities, n, 1.0, 1.0, random); top_p unused.
+ * rng_state (device, rows entries) holds java.util.Random states, (seed ^ 0x5DEECE66D) mod 2^48 for
+ * new Random(seed), and is advanced by the draw; out (device) receives the indices.  Greedy
+ * temperatures (sampleToken: <= 0; the model's function: == 0) take the first maximum
+ * (AggregationFeatures.indexOfMax) and draw nothing, as the reference does. */
+#define AR_SAMPLE_MODEL 0
+#define AR_SAMPLE_TOKEN 1
+int ar_hip_sample(ar_hip_ctx *ctx, const float *logits, int rows, int n, int mode, double temperature, double top_p,
+                  uint64_t *rng_state, int32_t *out);
+
 /* Multi-token projection on the MFMA units: C[M x N] = A[M x K] . W[N x K]^T, A and W bf16
  * (raw uint16 bits, K contiguous), fp32 accumulation.  N % 128 == 0, K % 64 == 0.
  *   AR_GEMM_STORE:    C (fp32, [M][N]) = result (+ bias[N] if non-null)
@@ -183,6 +201,15 @@ int ar_hip_qwen3_run(ar_qwen3 *m, int steps, int32_t *tokens_out);
  * row.  logits_out (optional, batch x vocab, host) receives the last prompt row's logits.
  * AutoregressiveModel.next over the prompt (AutoregressiveModel.java:295-299), batched. */
 int ar_hip_qwen3_prefill(ar_qwen3 *m, float *logits_out);
+/* Token selection of next / run / prefill.  Default: AR_SAMPLE_MODEL at temperature 0, i.e. greedy,
+ * as a new AutoregressiveModel starts.  AR_SAMPLE_MODEL with another temperature is
+ * AutoregressiveModel.setTemperature (AutoregressiveModel.java:258-260) with the sample function of
+ * AutoregressiveModel.of; AR_SAMPLE_TOKEN applies sampleToken(logits, V, temperature, top_p, random)
+ * instead (see ar_hip_sample).  seeds (host, max_batch values, or NULL to keep the generators) seed
+ * one java.util.Random per sequence; a draw happens only for steps past the prompt, so each
+ * sequence's draws match a reference model driven with new Random(seed).  Tokens sampled on the
+ * device are fed without a host round trip, like the greedy ones. */
+int ar_hip_qwen3_set_sampling(ar_qwen3 *m, int mode, double temperature, double top_p, const int64_t *seeds);
 /* Current position (AutoregressiveModel.getCurrentStep). */
 int ar_hip_qwen3_position(ar_qwen3 *m, int *pos);
 /* Residual-stream vector after the last step (batch x dim floats, host) for activation checks. */

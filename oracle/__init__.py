@@ -270,14 +270,72 @@ class OracleQwen3:
         _fn("oracle_model_hidden", self.precision)(self.h, out.ctypes.data)
         return out
 
-    def generate(self, prompt, n_decode, want_logits=True):
-        """AutoregressiveModel semantics: returns (tokens fed at each step, logits per step)."""
+    def generate(self, prompt, n_decode, want_logits=True, sampler=None):
+        """AutoregressiveModel semantics: returns (tokens fed at each step, logits per step).
+        ``sampler(logits) -> token`` replaces the greedy choice past the prompt (it is called only
+        there, as AutoregressiveModel.next applies its sample function, :295-308)."""
         fed, all_logits = [], []
-        prev_next = None
+        prev_next, prev_logits = None, None
         for s in range(len(prompt) + n_decode):
-            tok = int(prompt[s]) if s < len(prompt) else prev_next
-            prev_next, lg = self.step(tok, want_logits)
+            if s < len(prompt):
+                tok = int(prompt[s])
+            else:
+                tok = int(sampler(prev_logits)) if sampler is not None else prev_next
+            prev_next, lg = self.step(tok, want_logits or sampler is not None)
+            prev_logits = lg
             fed.append(tok)
             if want_logits:
                 all_logits.append(lg)
         return np.array(fed, dtype=np.int32), (np.stack(all_logits) if want_logits else None)
+
+
+# ---- token sampling (oracle/sample_oracle.c) ----------------------------------------
+class JavaRandom:
+    """java.util.Random(seed) state; draws advance it exactly as the Java class does."""
+
+    def __init__(self, seed: int):
+        lib().oracle_jrandom_seed.restype = ctypes.c_uint64
+        lib().oracle_jrandom_seed.argtypes = [ctypes.c_int64]
+        self.state = ctypes.c_uint64(lib().oracle_jrandom_seed(int(seed)))
+
+    def next_int(self) -> int:
+        lib().oracle_jrandom_next_int.restype = ctypes.c_int32
+        lib().oracle_jrandom_next_int.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        return lib().oracle_jrandom_next_int(ctypes.byref(self.state))
+
+    def next_double(self) -> float:
+        lib().oracle_jrandom_next_double.restype = ctypes.c_double
+        lib().oracle_jrandom_next_double.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        return lib().oracle_jrandom_next_double(ctypes.byref(self.state))
+
+
+def _sample_call(name, values, args, rng):
+    v = np.ascontiguousarray(values, dtype=np.float64)
+    r, margin = ctypes.c_double(-1.0), ctypes.c_double(np.inf)
+    fn = getattr(lib(), name)
+    fn.restype = ctypes.c_int
+    fn.argtypes = ([ctypes.c_void_p, ctypes.c_int] + [ctypes.c_double] * len(args) +
+                   [ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)])
+    k = fn(v.ctypes.data, v.size, *args, ctypes.byref(rng.state) if rng is not None else None, ctypes.byref(r),
+           ctypes.byref(margin))
+    return k, r.value, margin.value
+
+
+def sample_token(values, temperature, top_p, rng: JavaRandom | None):
+    """AutoregressiveModel.sampleToken (AutoregressiveModel.java:323-386).  Returns (index, r,
+    margin): r is the uniform draw (-1 when greedy), margin its distance to the nearest boundary
+    of the chosen index's cumulative interval."""
+    return _sample_call("oracle_sample_token", values, (temperature, top_p), rng)
+
+
+def model_sample(logits, temperature, rng: JavaRandom):
+    """The sample function of AutoregressiveModel.of (AutoregressiveModel.java:413-425)."""
+    return _sample_call("oracle_model_sample", logits, (temperature,), rng)
+
+
+def softmax_ignore_zero(x):
+    """DistributionFeatures.softmax(x, true) in FP64 (DistributionFeatures.java:129-141)."""
+    x = np.ascontiguousarray(x, dtype=np.float64).copy()
+    lib().oracle_softmax_ignore_zero.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    lib().oracle_softmax_ignore_zero(x.ctypes.data, x.size)
+    return x
