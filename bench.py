@@ -17,6 +17,9 @@ Extra fields on the JSON line:
   c5            BASELINE config 5 (Qwen3-4B shape, bf16 weights): 8 sequences x 8192-token prompts
                 prefilled together, then 64 greedy steps of all 8 (aggregate tok/s, HBM fraction)
   c2            BASELINE config 2: the decode-step attention op at a 4096-row cache (us per call)
+  sampled_c3    the C3 decode with on-device sampling instead of greedy selection: sampleToken
+                at temperature 0.8 / top-p 0.9, and the sample function of AutoregressiveModel.of
+                at temperature 0.7 (tok/s)
 """
 from __future__ import annotations
 
@@ -411,6 +414,27 @@ def main():
                     "traffic": tr.get("hbm_bytes_per_launch") if tr else None,
                     "traffic_source": "profiles/logits_gemv_traffic.md" if tr else None,
                     "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": kd["avg_us"]}
+
+    # ---- the same decode with on-device sampling instead of greedy selection ----------------
+    sampled = {}
+    for name, mode, temp, top_p in (("top_p", q.hw.SAMPLE_TOKEN, 0.8, 0.9), ("model_of", q.hw.SAMPLE_MODEL, 0.7, 1.0)):
+        am.set_temperature(0.0)
+        am.reset()
+        am.set_prompt(prompt)
+        am.run(n_prompt + args.warmup)
+        am.set_sampling(mode, temp, top_p, seeds=[args.seed])
+        n_s = min(args.steps, cfg.seq_len - (n_prompt + args.warmup))
+        model.ctx.synchronize()
+        ts = time.perf_counter()
+        am.run(n_s)
+        el = time.perf_counter() - ts
+        sampled[name] = {"tok_s": round(n_s / el, 1), "ms_per_step": round(1000.0 * el / n_s, 4), "steps": n_s,
+                         "temperature": temp, "top_p": top_p,
+                         "fn": "AutoregressiveModel.sampleToken" if mode == q.hw.SAMPLE_TOKEN
+                         else "AutoregressiveModel.of sample function"}
+        log(f"[bench] decode with sampling ({name}, T={temp}, top_p={top_p}): {sampled[name]['ms_per_step']} ms/token, "
+            f"{sampled[name]['tok_s']} tok/s")
+    am.set_temperature(0.0)
     model.close()
 
     # ---- CPU baseline: the oracle (reference semantics, fp32) on this host -------------
@@ -456,6 +480,7 @@ def main():
                    "prefetch_blocks": args.prefetch},
         "hbm": {"algorithmic_bytes_per_token": round(mean_bytes), "achieved_GBs": round(e2e_gbs, 1),
                 "frac_of_peak": round(e2e_gbs / HBM_PEAK_GBS, 4)},
+        "sampled_c3": sampled,
         "prompt_c3": {"tok_s": round(n_prompt / prefill_s, 1), "tokens": n_prompt,
                       "path": "fp32 weights: token by token through the decode step (reference semantics)"},
         "c4": c4_section(args) if "c4" in sections and not args.no_c4 else None,

@@ -277,6 +277,9 @@ struct SampleLaunch {
 };
 bool sample_is_greedy(int mode, double temperature);
 size_t sample_workspace_bytes(int rows, int vocab);
+// Zeroes the part of the workspace that must start at zero (row histograms, arrival counters);
+// launches keep it zero afterwards, so a workspace used with one (rows, vocab) is cleared once.
+int sample_workspace_clear(void* work, int rows, int vocab, hipStream_t stream);
 int launch_sample(const SampleLaunch& s, hipStream_t stream);
 
 void ar_ops_release(ar_hip_ctx* ctx);

@@ -94,6 +94,7 @@ extern "C" int ar_hip_sample(ar_hip_ctx* ctx, const float* logits, int rows, int
     std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnScratch& s = g_attn[ctx];
     AR_TRY(grow(ctx, &s.smp, &s.smp_bytes, sample_workspace_bytes(rows, n), 1));
+    AR_TRY(sample_workspace_clear(s.smp, rows, n, ctx->stream));  // the layout depends on (rows, n)
     SampleLaunch l;
     l.logits = logits; l.logits_stride = n; l.rows = rows; l.vocab = n; l.mode = mode; l.temperature = temperature;
     l.top_p = top_p; l.work = s.smp; l.rng = (unsigned long long*)rng_state; l.out = out;

@@ -740,8 +740,10 @@ extern "C" int ar_hip_qwen3_set_sampling(ar_qwen3* m, int mode, double temperatu
         AR_HIP_TRY(hipMemcpyAsync(m->smp_rng, states.data(), states.size() * 8, hipMemcpyHostToDevice, st));
         AR_HIP_TRY(hipStreamSynchronize(st));
     }
-    if (!sample_is_greedy(mode, temperature) && !m->smp_work)
+    if (!sample_is_greedy(mode, temperature) && !m->smp_work) {
         AR_TRY(ar_ctx_alloc(m->ctx, sample_workspace_bytes(m->B, m->cfg.vocab_size), &m->smp_work));
+        AR_TRY(sample_workspace_clear(m->smp_work, m->B, m->cfg.vocab_size, st));
+    }
     if (mode != m->smp_mode || temperature != m->smp_temperature || top_p != m->smp_top_p)
         AR_TRY(invalidate_graphs(m));  // the captured step holds the sampler's launches and arguments
     m->smp_mode = mode;

@@ -6,7 +6,7 @@
 // (48-bit LCG, nextDouble = ((next(26) << 27) + next(27)) * 2^-53) kept per sequence on the device.
 //
 // Everything after the fp32 logits is double, the reference's precision.  A row of V values is cut
-// into kBlocks chunks; each pass is one grid of (kBlocks, rows) 256-thread blocks whose per-block
+// into kBlocks chunks; each pass is one grid of (kBlocks, rows) 1024-thread blocks whose per-block
 // maxima / sums go to the workspace and are combined by the next kernel in a fixed order (a
 // wavefront butterfly over the 64 chunk values), so every result is deterministic.
 //
@@ -15,10 +15,13 @@
 // reaches top_p.  With p* the smallest kept value, that is every value > p* plus the first c
 // (by index) of the values == p*; p* is the largest key t with sum(p >= t) >= top_p.  It is found
 // by a radix descent over the 64-bit patterns of the probabilities (non-negative doubles order as
-// their bit patterns): 8 passes of 8-bit digits, each a per-chunk histogram of (count, sum) and a
-// one-block select of the digit.  Bucket sums are 2^-60 fixed point in u64 (exact, associative:
-// the histograms are independent of timing); the kept set agrees with the reference's sequential
-// double sums except when top_p lies within ~1e-13 of a partial sum.
+// their bit patterns): 8 passes of 8-bit digits.  Each pass is one kernel: every chunk builds its
+// histogram of (count, sum) in LDS and adds it into the row's histogram with device-scope integer
+// atomics; the last chunk to finish (an arrival counter) picks the digit and clears the row's
+// histogram and counter for the next pass.  Bucket sums are 2^-60 fixed point in u64, so the
+// atomics are exact and associative (the result does not depend on arrival order); the kept set
+// agrees with the reference's sequential double sums except when top_p lies within ~1e-13 of a
+// partial sum.
 //
 // The draw mirrors the reference's loop `cumulative += probs[i]; if (r < cumulative) return i`:
 // chunk masses locate the chunk whose interval holds r, then per-thread sums of contiguous index
@@ -30,7 +33,8 @@
 namespace {
 
 constexpr int kBlocks = 64;   // chunks per row (one wavefront of partials)
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
 constexpr double kFix = 1152921504606846976.0;     // 2^60
 constexpr double kEps64 = 2.220446049250313e-16;   // FP64 machine epsilon (Precision.java:110-121)
 
@@ -41,14 +45,17 @@ struct Ws {
     double* pemax;
     double* psum2;
     double* pmass;
-    unsigned* hcnt;             // [rows][kBlocks][256]
-    unsigned long long* hsum;   // [rows][kBlocks][256]
-    unsigned long long* sel;    // [rows][8]: prefix, above, done, take, -, -, -, -
+    unsigned* hcnt;             // [rows][kBlocks][256] per-chunk counts of the last pass
+    unsigned* gcnt;             // [rows][256] row histogram of the current pass (zero between passes)
+    unsigned long long* gsum;   // [rows][256]
+    unsigned* arrived;          // [rows] chunks done with the current pass (zero between passes)
+    unsigned long long* sel;    // [rows][8]: prefix, above, done, take
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-Ws carve(void* base, int rows, int V, size_t* total) {
+// The zero-initialised part (gcnt, gsum, arrived) comes first so that it can be cleared once.
+Ws carve(void* base, int rows, int V, size_t* total, size_t* zero_bytes) {
     Ws w{};
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -56,6 +63,10 @@ Ws carve(void* base, int rows, int V, size_t* total) {
         off += align256(bytes);
         return reinterpret_cast<void*>(p);
     };
+    w.gcnt = (unsigned*)take((size_t)rows * 256 * 4);
+    w.gsum = (unsigned long long*)take((size_t)rows * 256 * 8);
+    w.arrived = (unsigned*)take((size_t)rows * 4);
+    if (zero_bytes) *zero_bytes = off;
     w.buf = (double*)take((size_t)rows * V * 8);
     w.pmax = (double*)take((size_t)rows * kBlocks * 8);
     w.psum = (double*)take((size_t)rows * kBlocks * 8);
@@ -63,7 +74,6 @@ Ws carve(void* base, int rows, int V, size_t* total) {
     w.psum2 = (double*)take((size_t)rows * kBlocks * 8);
     w.pmass = (double*)take((size_t)rows * kBlocks * 8);
     w.hcnt = (unsigned*)take((size_t)rows * kBlocks * 256 * 4);
-    w.hsum = (unsigned long long*)take((size_t)rows * kBlocks * 256 * 8);
     w.sel = (unsigned long long*)take((size_t)rows * 8 * 8);
     if (total) *total = off;
     return w;
@@ -92,12 +102,24 @@ __device__ inline double wave_sum_d(double v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
-// block reductions (256 threads): butterfly per wavefront, then the 4 wavefront values in order
+// inclusive prefix over the lanes of a wavefront (Hillis-Steele; a fixed order of additions)
+template <typename T>
+__device__ inline T wave_incl_scan(T v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const T u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+// block reductions: butterfly per wavefront, then the wavefront values in order
 __device__ inline double block_max_d(double v, double* red) {
     v = wave_max_d(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    const double r = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+    double r = red[0];
+    for (int w = 1; w < kWaves; w++) r = fmax(r, red[w]);
     __syncthreads();
     return r;
 }
@@ -105,9 +127,23 @@ __device__ inline double block_sum_d(double v, double* red) {
     v = wave_sum_d(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    const double r = ((red[0] + red[1]) + red[2]) + red[3];
+    double r = red[0];
+    for (int w = 1; w < kWaves; w++) r += red[w];
     __syncthreads();
     return r;
+}
+// inclusive prefix over the block's threads in thread order (wavefront scans + the wavefront
+// totals in order)
+template <typename T>
+__device__ inline T block_incl_scan(T v, T* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    v = wave_incl_scan(v);
+    if (lane == 63) red[w] = v;
+    __syncthreads();
+    T base = 0;
+    for (int k = 0; k < w; k++) base += red[k];
+    __syncthreads();
+    return base + v;
 }
 // combine one row's 64 chunk partials (every thread gets the value; same order in every block)
 __device__ inline double row_max(const double* p) { return wave_max_d(p[threadIdx.x & 63]); }
@@ -123,7 +159,7 @@ __device__ inline double scaled(const Args& a, int b, int i) { return (double)a.
 
 // 1. maximum of logits / temperature per chunk
 __global__ __launch_bounds__(kThreads) void smp_max_kernel(Args a) {
-    __shared__ double red[4];
+    __shared__ double red[kWaves];
     const int blk = blockIdx.x, b = blockIdx.y;
     int c0, c1;
     chunk_of(a.V, blk, &c0, &c1);
@@ -136,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void smp_max_kernel(Args a) {
 // 2. exponentials: sampleToken's exp(x - max), or the softmax-ignoring-zero of the model's sample
 //    function (a value equal to 0 stays 0; the maximum itself gets exp(epsilon))
 __global__ __launch_bounds__(kThreads) void smp_exp_kernel(Args a) {
-    __shared__ double red[4];
+    __shared__ double red[kWaves];
     const int blk = blockIdx.x, b = blockIdx.y;
     int c0, c1;
     chunk_of(a.V, blk, &c0, &c1);
@@ -167,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void smp_exp_kernel(Args a) {
 // 3. (model sample function) sampleToken's own softmax of the probabilities p = e / S1 at
 //    temperature 1: f = exp(p - max p); max p = fl(max e / S1), division being monotone
 __global__ __launch_bounds__(kThreads) void smp_exp2_kernel(Args a) {
-    __shared__ double red[4];
+    __shared__ double red[kWaves];
     const int blk = blockIdx.x, b = blockIdx.y;
     int c0, c1;
     chunk_of(a.V, blk, &c0, &c1);
@@ -188,14 +224,66 @@ __device__ inline double denom(const Args& a, int b) {
     return row_sum((a.mode == AR_SAMPLE_TOKEN ? a.w.psum : a.w.psum2) + b * kBlocks);
 }
 
+// The digit choice of one pass (wavefront 0 of the last chunk): the highest non-empty bucket d
+// with above + sum(buckets >= d) >= target, scanning buckets in descending order, 4 per lane.
+__device__ void select_digit(const Args& a, int b, int level, unsigned long long target, const unsigned* cnt,
+                             const unsigned long long* sm) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long* sel = a.w.sel + b * 8;
+    // state left by the previous pass (nothing before the first)
+    const unsigned long long prefix0 = level ? sel[0] : 0ull;
+    const unsigned long long above = level ? sel[1] : 0ull;
+    unsigned long long lsum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) lsum += sm[255 - 4 * lane - k];
+    const unsigned long long before = wave_incl_scan(lsum) - lsum;  // buckets above this lane's four
+    unsigned long long acc = above + before;
+    int hit = -1;
+    unsigned long long acc_hit = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int d = 255 - 4 * lane - k;
+        if (hit < 0 && cnt[d] && acc + sm[d] >= target) {
+            hit = d;
+            acc_hit = acc;
+        }
+        acc += sm[d];
+    }
+    const unsigned long long hits = __ballot(hit >= 0);
+    if (!hits) {  // the whole row sums to less than top_p: the reference keeps every value
+        if (lane == 0) sel[2] = 1;
+        return;
+    }
+    if (lane != __builtin_ctzll(hits)) return;
+    const int shift = 56 - 8 * level;
+    const unsigned long long prefix = prefix0 | ((unsigned long long)hit << shift);
+    sel[0] = prefix;  // prefix
+    sel[1] = acc_hit; // fixed-point sum of the values above the prefix range
+    unsigned long long done = 0, take = 0;  // done: 0 searching, 1 keep everything, 2 cut found
+    if (level == 7) {
+        const double pstar = __longlong_as_double((long long)prefix);
+        const unsigned long long pf = (unsigned long long)(pstar * kFix);
+        const unsigned long long ties = cnt[hit];
+        take = 1;
+        if (target > acc_hit) take = pf ? (target - acc_hit + pf - 1) / pf : ties;
+        take = take < 1 ? 1 : (take > ties ? ties : take);
+        done = 2;
+    }
+    sel[2] = done;
+    sel[3] = take;  // values == p* kept
+}
+
 // 4. nucleus search, pass `level`: histogram of digit (key >> shift) & 255 over the keys that match
-//    the prefix chosen so far
-__global__ __launch_bounds__(kThreads) void smp_hist_kernel(Args a, int level) {
+//    the prefix chosen so far; the last chunk to arrive picks the digit
+__global__ __launch_bounds__(kThreads) void smp_hist_kernel(Args a, int level, unsigned long long target) {
     __shared__ unsigned cnt[256];
     __shared__ unsigned long long sm[256];
+    __shared__ int last_s;
     const int blk = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-    cnt[t] = 0;
-    sm[t] = 0;
+    if (t < 256) {
+        cnt[t] = 0;
+        sm[t] = 0;
+    }
     __syncthreads();
     int c0, c1;
     chunk_of(a.V, blk, &c0, &c1);
@@ -203,76 +291,50 @@ __global__ __launch_bounds__(kThreads) void smp_hist_kernel(Args a, int level) {
     const int shift = 56 - 8 * level;
     const int hs = level ? shift + 8 : 0;  // bits above the current digit (none at level 0)
     const unsigned long long want = level ? a.w.sel[b * 8 + 0] >> hs : 0ull;
+    const bool searching = level == 0 || a.w.sel[b * 8 + 2] == 0;
     const double* buf = a.w.buf + (size_t)b * a.V;
-    for (int i = c0 + t; i < c1; i += kThreads) {
-        const double p = buf[i] / D;
-        const unsigned long long key = (unsigned long long)__double_as_longlong(p);
-        if (level == 0 || (key >> hs) == want) {
-            const int d = (int)((key >> shift) & 255);
-            atomicAdd(&cnt[d], 1u);
-            atomicAdd(&sm[d], (unsigned long long)(p * kFix));
+    if (searching) {
+        for (int i = c0 + t; i < c1; i += kThreads) {
+            const double p = buf[i] / D;
+            const unsigned long long key = (unsigned long long)__double_as_longlong(p);
+            if (level == 0 || (key >> hs) == want) {
+                const int d = (int)((key >> shift) & 255);
+                atomicAdd(&cnt[d], 1u);
+                atomicAdd(&sm[d], (unsigned long long)(p * kFix));
+            }
         }
     }
     __syncthreads();
-    const size_t o = ((size_t)b * kBlocks + blk) * 256 + t;
-    a.w.hcnt[o] = cnt[t];
-    a.w.hsum[o] = sm[t];
-}
-
-// 5. one block per row: add the chunk histograms (fixed order), pick the digit
-__global__ __launch_bounds__(kThreads) void smp_select_kernel(Args a, int level, unsigned long long target) {
-    __shared__ unsigned cnt[256];
-    __shared__ unsigned long long sm[256];
-    const int b = blockIdx.x, t = threadIdx.x;
-    unsigned long long* sel = a.w.sel + b * 8;
-    unsigned c = 0;
-    unsigned long long s = 0;
-    for (int j = 0; j < kBlocks; j++) {
-        const size_t o = ((size_t)b * kBlocks + j) * 256 + t;
-        c += a.w.hcnt[o];
-        s += a.w.hsum[o];
-    }
-    cnt[t] = c;
-    sm[t] = s;
-    __syncthreads();
-    if (t != 0) return;
-    if (level == 0) {
-        sel[0] = 0;  // prefix
-        sel[1] = 0;  // fixed-point sum of the values above the prefix range
-        sel[2] = 0;  // 0 searching, 1 keep everything, 2 cut found
-        sel[3] = 0;  // values == p* kept
-    }
-    if (sel[2] == 1) return;
-    const int shift = 56 - 8 * level;
-    unsigned long long acc = sel[1];
-    int dstar = -1;
-    for (int d = 255; d >= 0; d--) {
-        if (cnt[d] && acc + sm[d] >= target) {
-            dstar = d;
-            break;
+    if (t < 256) {
+        a.w.hcnt[((size_t)b * kBlocks + blk) * 256 + t] = cnt[t];
+        if (cnt[t]) {
+            __hip_atomic_fetch_add(a.w.gcnt + b * 256 + t, cnt[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(a.w.gsum + b * 256 + t, sm[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        acc += sm[d];
     }
-    if (dstar < 0) {  // the whole row sums to less than top_p: the reference keeps every value
-        sel[2] = 1;
-        return;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's histogram atomics have completed
+    __syncthreads();
+    if (t == 0) {
+        unsigned* c = a.w.arrived + b;
+        const unsigned prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (unsigned)(kBlocks - 1);
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = last;
     }
-    sel[0] |= (unsigned long long)dstar << shift;
-    sel[1] = acc;
-    if (level == 7) {
-        const double pstar = __longlong_as_double((long long)sel[0]);
-        const unsigned long long pf = (unsigned long long)(pstar * kFix);
-        const unsigned long long ties = cnt[dstar];
-        unsigned long long take = 1;
-        if (target > acc) take = pf ? (target - acc + pf - 1) / pf : ties;
-        take = take < 1 ? 1 : (take > ties ? ties : take);
-        sel[3] = take;
-        sel[2] = 2;
+    __syncthreads();
+    if (!last_s) return;
+    // the row histogram, read once and cleared for the next pass
+    if (t < 256) {
+        cnt[t] = __hip_atomic_load(a.w.gcnt + b * 256 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm[t] = __hip_atomic_load(a.w.gsum + b * 256 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.w.gcnt + b * 256 + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.w.gsum + b * 256 + t, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    __syncthreads();
+    if (t < 64 && searching) select_digit(a, b, level, target, cnt, sm);
 }
 
-// Membership of the nucleus for the contiguous index range of one thread: `rank` is the number of
-// values == p* before the range (a block-level scan of per-thread tie counts).
+// Membership of the nucleus: values > p* and the first `take` (by index) of the values == p*.
 struct Nucleus {
     int mode;                   // 0: everything (no top-p), 1: everything (top-p kept all), 2: cut
     unsigned long long pstar, take;
@@ -292,34 +354,32 @@ __device__ inline Nucleus nucleus_of(const Args& a, int b) {
     return n;
 }
 
-// Per-thread range inside chunk [c0, c1) and the number of p* ties before it.
+__device__ inline void thread_range(int c0, int c1, int* r0, int* r1) {
+    const int per = (c1 - c0 + kThreads - 1) / kThreads;
+    *r0 = min(c1, c0 + (int)threadIdx.x * per);
+    *r1 = min(c1, *r0 + per);
+}
+
+// Number of values == p* before this thread's contiguous range: earlier chunks (their last-pass
+// histograms) plus earlier threads of this chunk (a block scan).
 __device__ inline unsigned long long tie_base(const Args& a, const Nucleus& n, int b, int blk, int r0, int r1,
-                                              double D, unsigned long long* scan) {
-    const int t = threadIdx.x;
+                                              double D, unsigned long long* red) {
     unsigned long long mine = 0;
     if (n.mode == 2) {
         const double* buf = a.w.buf + (size_t)b * a.V;
         for (int i = r0; i < r1; i++)
             mine += (unsigned long long)__double_as_longlong(buf[i] / D) == n.pstar;
     }
-    scan[t] = mine;
-    __syncthreads();
-    if (t == 0) {
-        unsigned long long before = 0;
-        if (n.mode == 2) {
-            const int d = (int)(n.pstar & 255);
-            for (int j = 0; j < blk; j++) before += a.w.hcnt[((size_t)b * kBlocks + j) * 256 + d];
-        }
-        for (int k = 0; k < kThreads; k++) {
-            const unsigned long long v = scan[k];
-            scan[k] = before;
-            before += v;
-        }
+    unsigned long long before_chunk = 0;
+    if (n.mode == 2) {
+        const int lane = threadIdx.x & 63;
+        const int d = (int)(n.pstar & 255);
+        unsigned long long v = lane < blk ? a.w.hcnt[((size_t)b * kBlocks + lane) * 256 + d] : 0ull;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        before_chunk = v;
     }
-    __syncthreads();
-    const unsigned long long base = scan[t];
-    __syncthreads();
-    return base;
+    return before_chunk + block_incl_scan(mine, red) - mine;
 }
 
 __device__ inline double kept(const Nucleus& n, double q, unsigned long long* rank) {
@@ -330,23 +390,17 @@ __device__ inline double kept(const Nucleus& n, double q, unsigned long long* ra
     return 0.0;
 }
 
-__device__ inline void thread_range(int c0, int c1, int* r0, int* r1) {
-    const int per = (c1 - c0 + kThreads - 1) / kThreads;
-    *r0 = min(c1, c0 + (int)threadIdx.x * per);
-    *r1 = min(c1, *r0 + per);
-}
-
-// 6. kept probability mass per chunk (before the nucleus renormalisation)
+// 5. kept probability mass per chunk (before the nucleus renormalisation)
 __global__ __launch_bounds__(kThreads) void smp_mass_kernel(Args a) {
-    __shared__ unsigned long long scan[kThreads];
-    __shared__ double red[4];
+    __shared__ unsigned long long ured[kWaves];
+    __shared__ double red[kWaves];
     const int blk = blockIdx.x, b = blockIdx.y;
     int c0, c1, r0, r1;
     chunk_of(a.V, blk, &c0, &c1);
     thread_range(c0, c1, &r0, &r1);
     const double D = denom(a, b);
     const Nucleus n = nucleus_of(a, b);
-    unsigned long long rank = tie_base(a, n, b, blk, r0, r1, D, scan);
+    unsigned long long rank = tie_base(a, n, b, blk, r0, r1, D, ured);
     const double* buf = a.w.buf + (size_t)b * a.V;
     double s = 0.0;
     for (int i = r0; i < r1; i++) s += kept(n, buf[i] / D, &rank);
@@ -365,41 +419,37 @@ __device__ inline double java_next_double(unsigned long long* s) {
     return (double)((hi << 27) + lo) * 0x1.0p-53;
 }
 
-// 7. one block per row: the uniform draw and the index whose cumulative interval holds it
+// 6. one block per row: the uniform draw and the index whose cumulative interval holds it
 __global__ __launch_bounds__(kThreads) void smp_draw_kernel(Args a) {
-    __shared__ unsigned long long scan[kThreads];
-    __shared__ double tsum[kThreads];
-    __shared__ int tlast[kThreads];
+    __shared__ unsigned long long ured[kWaves];
+    __shared__ double dred[kWaves];
+    __shared__ int ifirst[kWaves], ilast[kWaves];
     __shared__ double sh_r, sh_c, sh_Z;
-    __shared__ int sh_blk, sh_t, sh_idx;
-    const int b = blockIdx.x, t = threadIdx.x;
+    __shared__ int sh_blk, sh_idx;
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
     // The model draws only when the next step feeds a sampled token (past the prompt), as
     // AutoregressiveModel.next applies its sample function (AutoregressiveModel.java:295-308).
     if (a.state && a.state[2] < a.state[1]) return;
     const double D = denom(a, b);
     const Nucleus n = nucleus_of(a, b);
-    if (t == 0) {
-        const double r = java_next_double(a.rng + b);
-        double Z = 1.0;
-        if (a.topp) {
-            Z = 0.0;
-            for (int j = 0; j < kBlocks; j++) Z += a.w.pmass[b * kBlocks + j];
+    if (t < 64) {
+        // chunk masses in index order; the first chunk whose running total exceeds r
+        const double pm = a.w.pmass[b * kBlocks + lane];
+        const double Z = a.topp ? wave_sum_d(pm) : 1.0;
+        const double m = a.topp ? pm / Z : pm;
+        const double incl = wave_incl_scan(m);
+        const double excl = __shfl_up(incl, 1, 64);
+        double r = 0.0;
+        if (lane == 0) r = java_next_double(a.rng + b);
+        r = __shfl(r, 0, 64);
+        const unsigned long long hits = __ballot(r < incl);
+        if (lane == 0) {
+            sh_r = r;
+            sh_Z = Z;
+            sh_blk = hits ? __builtin_ctzll(hits) : -1;
+            sh_idx = a.V - 1;  // the reference's result when no running sum exceeds r
         }
-        double c = 0.0;
-        int blk = -1;
-        for (int j = 0; j < kBlocks; j++) {
-            const double m = a.topp ? a.w.pmass[b * kBlocks + j] / Z : a.w.pmass[b * kBlocks + j];
-            if (r < c + m) {
-                blk = j;
-                break;
-            }
-            c += m;
-        }
-        sh_r = r;
-        sh_c = c;
-        sh_Z = Z;
-        sh_blk = blk;
-        sh_idx = a.V - 1;  // the reference's result when no running sum exceeds r
+        if (hits && lane == __builtin_ctzll(hits)) sh_c = lane ? excl : 0.0;
     }
     __syncthreads();
     const int blk = sh_blk;
@@ -407,9 +457,9 @@ __global__ __launch_bounds__(kThreads) void smp_draw_kernel(Args a) {
         int c0, c1, r0, r1;
         chunk_of(a.V, blk, &c0, &c1);
         thread_range(c0, c1, &r0, &r1);
-        unsigned long long rank0 = tie_base(a, n, b, blk, r0, r1, D, scan);
+        const unsigned long long rank0 = tie_base(a, n, b, blk, r0, r1, D, ured);
         const double* buf = a.w.buf + (size_t)b * a.V;
-        const double Z = sh_Z;
+        const double Z = sh_Z, r = sh_r, c = sh_c;
         double s = 0.0;
         int last = -1;
         unsigned long long rank = rank0;
@@ -419,45 +469,43 @@ __global__ __launch_bounds__(kThreads) void smp_draw_kernel(Args a) {
             s += q;
             if (q > 0.0) last = i;
         }
-        tsum[t] = s;
-        tlast[t] = last;
-        __syncthreads();
-        if (t == 0) {
-            double c = sh_c;
-            const double r = sh_r;
-            int tc = -1, lastpos = -1;
-            for (int k = 0; k < kThreads; k++) {
-                if (tlast[k] >= 0) lastpos = tlast[k];
-                if (r < c + tsum[k]) {
-                    tc = k;
-                    break;
-                }
-                c += tsum[k];
-            }
-            sh_t = tc;
-            sh_c = c;
-            // rounding of the grouped sums left r past this chunk's total: its last positive value
-            if (tc < 0) sh_idx = lastpos >= 0 ? lastpos : c1 - 1;
+        const double incl = block_incl_scan(s, dred);
+        // first thread whose running total exceeds r (thread order = index order), and the last
+        // positive value of the chunk: the fallback when rounding of the grouped sums leaves r
+        // past the chunk's total
+        const unsigned long long wh = __ballot(r < c + incl);
+        int wl = last;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) wl = max(wl, __shfl_xor(wl, o, 64));
+        if (lane == 0) {
+            ifirst[t >> 6] = wh ? (t & ~63) + __builtin_ctzll(wh) : 0x7FFFFFFF;
+            ilast[t >> 6] = wl;
         }
         __syncthreads();
-        if (t == sh_t) {
-            double c = sh_c;
-            const double r = sh_r;
+        int first = 0x7FFFFFFF, lastpos = -1;
+        for (int w = 0; w < kWaves; w++) {
+            first = min(first, ifirst[w]);
+            lastpos = max(lastpos, ilast[w]);
+        }
+        if (first == 0x7FFFFFFF) {
+            if (t == 0) sh_idx = lastpos >= 0 ? lastpos : c1 - 1;
+        } else if (t == first) {
+            double cc = c + (incl - s);
             rank = rank0;
             int idx = last >= 0 ? last : r1 - 1;
             for (int i = r0; i < r1; i++) {
                 double q = kept(n, buf[i] / D, &rank);
                 if (a.topp) q /= Z;
-                c += q;
-                if (r < c) {
+                cc += q;
+                if (r < cc) {
                     idx = i;
                     break;
                 }
             }
             sh_idx = idx;
         }
-        __syncthreads();
     }
+    __syncthreads();
     if (t == 0) {
         const int idx = sh_idx;
         if (a.out) a.out[b] = idx;
@@ -475,8 +523,14 @@ bool sample_is_greedy(int mode, double temperature) {
 
 size_t sample_workspace_bytes(int rows, int vocab) {
     size_t total = 0;
-    carve(nullptr, rows, vocab, &total);
+    carve(nullptr, rows, vocab, &total, nullptr);
     return total;
+}
+
+int sample_workspace_clear(void* work, int rows, int vocab, hipStream_t st) {
+    size_t zero = 0;
+    carve(work, rows, vocab, nullptr, &zero);
+    return launch_fill_i32((int*)work, 0, zero / 4, st);  // a kernel: safe inside a captured graph
 }
 
 int launch_sample(const SampleLaunch& s, hipStream_t st) {
@@ -492,7 +546,7 @@ int launch_sample(const SampleLaunch& s, hipStream_t st) {
     a.mode = s.mode;
     a.T = s.temperature;
     a.topp = s.mode == AR_SAMPLE_TOKEN && s.top_p < 1.0;
-    a.w = carve(s.work, s.rows, s.vocab, nullptr);
+    a.w = carve(s.work, s.rows, s.vocab, nullptr, nullptr);
     a.rng = s.rng;
     a.state = s.state;
     a.keys = s.keys;
@@ -512,9 +566,7 @@ int launch_sample(const SampleLaunch& s, hipStream_t st) {
         const double tp = s.top_p > 0.0 ? ceil(s.top_p * kFix) : 0.0;
         const unsigned long long target = (unsigned long long)tp;
         for (int level = 0; level < 8; level++) {
-            hipLaunchKernelGGL(smp_hist_kernel, grid, block, 0, st, a, level);
-            AR_LAUNCH_CHECK();
-            hipLaunchKernelGGL(smp_select_kernel, dim3(s.rows), block, 0, st, a, level, target);
+            hipLaunchKernelGGL(smp_hist_kernel, grid, block, 0, st, a, level, target);
             AR_LAUNCH_CHECK();
         }
     }
