@@ -90,6 +90,22 @@ _SIGS = {
                                      ctypes.c_double, ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_qwen3_set_sampling": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_double, ctypes.c_double,
                                                  ctypes.c_void_p]),
+    # include/ar_tokenizer.h
+    "ar_hip_tokenizer_load": (ctypes.c_int, [ctypes.c_char_p, _c_void_pp]),
+    "ar_hip_tokenizer_from_vocab": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                                   _c_void_pp]),
+    "ar_hip_tokenizer_load_merges": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p]),
+    "ar_hip_tokenizer_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_tokenizer_vocab_size": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
+    "ar_hip_tokenizer_merge_count": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
+    "ar_hip_tokenizer_token": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), _c_int_p,
+                                              ctypes.POINTER(ctypes.c_float)]),
+    "ar_hip_tokenizer_encode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, ctypes.c_int,
+                                               ctypes.c_int, ctypes.c_void_p, ctypes.c_int, _c_int_p]),
+    "ar_hip_tokenizer_decode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                               ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+    "ar_hip_tokenizer_pretokenize": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                                    _c_int_p]),
     # include/ar_state_dict.h
     "ar_hip_state_dict_open": (ctypes.c_int, [ctypes.c_char_p, _c_void_pp]),
     "ar_hip_state_dict_create": (ctypes.c_int, [_c_void_pp]),

@@ -117,8 +117,9 @@ class AutoregressiveModel:
 class Qwen3:
     """Device-resident Qwen3 built from an HF-keyed state dict (or an iterator of (key, tensor))."""
 
-    def __init__(self, config: Qwen3Config, state_dict, ctx: hw.HipContext | None = None):
+    def __init__(self, config: Qwen3Config, state_dict, ctx: hw.HipContext | None = None, tokenizer=None):
         self.config = config
+        self.tokenizer = tokenizer  # a common_amd.tokenizer.Qwen3Tokenizer, for run(); optional
         self.ctx = ctx or hw.HipContext(0)
         self._own_ctx = ctx is None
         h = ctypes.c_void_p()
@@ -137,17 +138,54 @@ class Qwen3:
         self.model = AutoregressiveModel(self)
 
     @classmethod
-    def from_weights_directory(cls, path, config: Qwen3Config | None = None, ctx: hw.HipContext | None = None,
-                               **config_fields) -> "Qwen3":
+    def from_weights_directory(cls, path, tokenizer_path=None, config: Qwen3Config | None = None,
+                               ctx: hw.HipContext | None = None, **config_fields) -> "Qwen3":
         """Qwen3(String weightsDirectory, tokenizerPath, config) (Qwen3.java:154-190): reads the
         protobuf weights with StateDictionary and, without a config, infers one from the weight
         shapes (Qwen3.inferConfigFromWeights); ``config_fields`` override fields of the inferred
-        config (e.g. seq_len, max_batch, weight_dtype)."""
+        config (e.g. seq_len, max_batch, weight_dtype).  The tokenizer is optional, as there."""
         from .state_dict import StateDictionary
+        from .tokenizer import Qwen3Tokenizer
+        tok = Qwen3Tokenizer(tokenizer_path) if tokenizer_path is not None else None
         with StateDictionary(path) as sd:
             if config is None:
                 config = dataclasses.replace(sd.infer_config(), **config_fields)
-            return cls(config, sd, ctx)
+            return cls(config, sd, ctx, tokenizer=tok)
+
+    def run(self, steps: int, prompt: str | None, output, prefill: bool = True) -> float:
+        """Qwen3.run (Qwen3.java:426-478): encodes the prompt with BOS, feeds it and generates until
+        `steps` positions or EOS, handing each token's text to ``output`` between "<|im_start|>\n"
+        and "<|im_end|>"; returns the milliseconds after the first token.  The token loop is the
+        device model's (greedy, or the sampling set with AutoregressiveModel.set_sampling).  With
+        ``prefill`` the prompt runs as one batched prefill (the reference feeds it one token per
+        step; the model ends in the same state) and its tokens are emitted as they would be."""
+        import time
+
+        from .tokenizer import BOS_TOKEN, EOS_TOKEN
+        if steps <= 0 or steps > self.config.seq_len:
+            steps = self.config.seq_len
+        if self.tokenizer is None:
+            raise RuntimeError("No tokenizer loaded. Cannot process text input.")
+        ids = self.tokenizer.encode(prompt, True, False) if prompt is not None else []
+        am = self.model
+        am.reset()
+        # setCurrentToken(BOS) + an empty prompt: the first step feeds BOS
+        am.set_prompt(ids if ids else [BOS_TOKEN])
+        output("<|im_start|>\n")
+        start = 0.0
+        if prefill and len(ids) > 1 and len(ids) < steps:
+            am.prefill()
+            for t in ids:
+                output(self.tokenizer.decode([t]))
+        while am.get_current_step() < steps:
+            nxt = int(am.next()[0])
+            output(self.tokenizer.decode([nxt]))
+            if nxt == EOS_TOKEN:
+                break
+            if start == 0.0:
+                start = time.perf_counter()
+        output("<|im_end|>")
+        return 1000.0 * (time.perf_counter() - start) if start else 0.0
 
     def set_weight(self, key: str, t: np.ndarray):
         t = np.ascontiguousarray(t, dtype=np.float32)

@@ -134,6 +134,44 @@ def test_c1_from_protobuf_weights_directory(ctx, c1, tmp_path, wdtype):
     np.testing.assert_array_equal(lg_p, lg_d)
 
 
+def test_run_with_tokenizer(ctx, tmp_path):
+    """Qwen3.run(steps, prompt, output): the prompt encoded with BOS, fed, then generated tokens,
+    each handed to output as its decoded text between the chat markers."""
+    from common_amd.tokenizer import BOS_TOKEN, Qwen3Tokenizer, write_tokenizer
+    b2c = {}
+    n = 0
+    for b in range(256):  # byte-level alphabet: one vocabulary entry per byte
+        keep = 33 <= b <= 126 or 161 <= b <= 172 or 174 <= b <= 255
+        b2c[b] = chr(b) if keep else chr(256 + n)
+        n += not keep
+    vocab = [b2c[b] for b in range(256)] + ["he", "hel", "hell", "hello", "Ġw", "Ġwo"]
+    merges = [("h", "e"), ("he", "l"), ("hel", "l"), ("hell", "o"), ("Ġ", "w"), ("Ġw", "o")]
+    write_tokenizer(str(tmp_path / "tokenizer.bin"), vocab, None, merges)
+    tok = Qwen3Tokenizer(str(tmp_path / "tokenizer.bin"))
+    ids = tok.encode("hello wo", True, False)
+    assert ids == [BOS_TOKEN, 259, 261]
+    cfg = C.Qwen3Config(dim=128, hidden_dim=256, layer_count=1, head_count=2, kv_head_count=1, head_size=64,
+                        vocab_size=151936, seq_len=12)
+    for wdtype in (C.DTYPE_F32, C.DTYPE_BF16):
+        cfg_w = dataclasses.replace(cfg, weight_dtype=wdtype)
+        sd = synthetic.state_dict(cfg_w, seed=9)
+        with Qwen3(cfg_w, sd, ctx, tokenizer=tok) as m:
+            out, out_steps = [], []
+            m.run(12, "hello wo", out.append)  # prompt prefilled
+            m.run(12, "hello wo", out_steps.append, prefill=False)  # prompt one token per step
+            am = m.model
+            am.reset()
+            am.set_prompt(ids)
+            fed = [int(am.next()[0]) for _ in range(12)]
+        assert out_steps[0] == "<|im_start|>\n" and out_steps[-1] == "<|im_end|>"
+        assert out_steps[1:-1][: len(fed)] == [tok.decode([t]) for t in fed][: len(out_steps) - 2]
+        assert out_steps[2:4] == ["hello", " wo"]  # the prompt tokens (BOS prints nothing)
+        if wdtype == C.DTYPE_F32:  # fp32 prefill is the decode step itself: identical runs
+            assert out == out_steps
+        else:  # the MFMA prefill differs in rounding: the prompt part must agree
+            assert out[:4] == out_steps[:4]
+
+
 def test_c1_batch_sequences_are_independent(ctx, c1):
     cfg, sd, prompt = c1
     cfg2 = dataclasses.replace(cfg, max_batch=3)
