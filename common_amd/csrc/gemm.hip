@@ -218,6 +218,216 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
         }
 }
 
+// ---- large-shape kernel: 256 x 256 tiles fed by direct global -> LDS loads -------------------
+//
+// For products with many tiles (the long prompts of batched prefill) a 4-wavefront block owns a
+// 256 x 256 tile (128 x 128 per wavefront: 16 MFMA accumulators, 256 AGPRs), BK = 64, two LDS stages
+// of 64 KB filled by global_load_lds_dwordx4 (each lane's 16 bytes go straight to LDS; no staging
+// registers, no LDS store instructions).  Rows are 128 B; the 16-byte chunk c of row r sits in slot
+// c ^ ((r >> 1) & 7), so the eight lanes that read one 16-byte piece each per LDS cycle hit eight
+// different bank groups.  Per k-tile the block waits once: after the third k-step's MFMAs every
+// wavefront waits for its own copies of the next tile (vmcnt) and its own LDS reads (lgkmcnt),
+// then a barrier makes both block-wide, the freed stage is refilled with tile kt + 2, and the next
+// tile's first fragments are read while the last k-step's MFMAs run.  Waits are written by hand: a
+// workgroup-scope fence (__syncthreads) would also wait for every outstanding LDS copy.
+namespace dma {
+constexpr int BM = 256, BNW = 256, BK = 64, STAGES = 2, NTHR = 256, KS = BK / 16;
+constexpr int ROWB = BK * 2;
+constexpr int TILE_B = 256 * ROWB;
+constexpr int STAGE_B = 2 * TILE_B;
+constexpr int LDS_BYTES = STAGES * STAGE_B;  // 128 KB
+constexpr int DMA = TILE_B / 1024 / 4;       // copy instructions per wavefront per matrix per stage
+// s_waitcnt immediates (vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
+constexpr int vm_imm(int v, int lgkm) { return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (lgkm << 8); }
+constexpr int VM_PROLOGUE = vm_imm(2 * DMA * (STAGES - 1), 15);  // all but tile 0 may be in flight
+constexpr int VM_LOOP = vm_imm(2 * DMA * (STAGES - 2), 0);       // tile kt + 1 landed, LDS reads done
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ inline int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+}  // namespace dma
+
+template <bool F16, int EPI>
+__global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int mt, int nt) {
+    using Mf = Mfma<F16>;
+    using frag = typename Mf::frag;
+    extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+    constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
+    constexpr int BN = dma::BNW / NW;  // output columns per block (SwiGLU: 128 gate rows + 128 up rows)
+    constexpr int WN = BN / 2, FN = WN / 32, FM = 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int mi, ni;
+    tile_of(blockIdx.x, mt, nt, &mi, &ni);
+    const int m0 = mi * dma::BM, n0 = ni * BN;
+    const int nk = p.K / dma::BK;
+
+    // copy plan: instruction i of wavefront w fills rows 8j .. 8j+7 (j = 4i + w) of a tile; lane l
+    // writes slot l % 8 of row 8j + l / 8, i.e. fetches chunk dma::swz(row, l % 8)
+    const uint16_t* srcA[dma::DMA];
+    const uint16_t* srcW[dma::DMA];
+#pragma unroll
+    for (int i = 0; i < dma::DMA; i++) {
+        const int j = 4 * i + wave, r = 8 * j + (lane >> 3), c = dma::swz(r, lane & 7);
+        srcA[i] = p.A + (size_t)min(m0 + r, p.M - 1) * p.lda + c * 8;
+        const uint16_t* wb = (NW == 2 && r >= BN) ? p.W2 + (size_t)(n0 + r - BN) * p.ldw : p.W + (size_t)(n0 + r) * p.ldw;
+        srcW[i] = wb + c * 8;
+    }
+    auto issue = [&](int slot, int kt) {
+        const int k0 = kt * dma::BK;
+        unsigned char* st = lds + slot * dma::STAGE_B;
+#pragma unroll
+        for (int i = 0; i < dma::DMA; i++) {
+            const int j = 4 * i + wave;
+            __builtin_amdgcn_global_load_lds((const void*)(srcA[i] + k0), (dma::lds_void*)(st + j * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(srcW[i] + k0), (dma::lds_void*)(st + dma::TILE_B + j * 1024), 16, 0, 0);
+        }
+    };
+
+    floatx16 acc[NW][FM][FN];
+#pragma unroll
+    for (int w = 0; w < NW; w++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[w][i][j][r] = 0.f;
+
+    frag fa[2][FM], fb[2][NW][FN];  // fragments of two k-steps
+    auto read = [&](int set, int slot, int kk) {
+        const unsigned char* st = lds + slot * dma::STAGE_B;
+        const int c = kk * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int r = wm * 128 + i * 32 + (lane & 31);
+            fa[set][i] = *reinterpret_cast<const frag*>(st + r * dma::ROWB + dma::swz(r, c) * 16);
+        }
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int r = w * BN + wn * WN + j * 32 + (lane & 31);
+                fb[set][w][j] = *reinterpret_cast<const frag*>(st + dma::TILE_B + r * dma::ROWB + dma::swz(r, c) * 16);
+            }
+    };
+    auto mma = [&](int set) {
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) acc[w][i][j] = Mf::mac(fa[set][i], fb[set][w][j], acc[w][i][j]);
+    };
+
+#pragma unroll
+    for (int s = 0; s < dma::STAGES; s++) issue(s, min(s, nk - 1));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(dma::VM_PROLOGUE);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read(0, 0, 0);
+    read(1, 0, 1);
+    for (int kt = 0; kt < nk; kt++) {
+        const int slot = kt % dma::STAGES, nslot = (kt + 1) % dma::STAGES;
+#pragma unroll
+        for (int kk = 0; kk < dma::KS - 2; kk++) {
+            mma(kk & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            read(kk & 1, slot, kk + 2);
+        }
+        mma((dma::KS - 2) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(dma::VM_LOOP);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        // the stage just finished takes tile kt + dma::STAGES (the last tiles reload tile nk - 1, which
+        // keeps every wait count static); the reads of the last iteration fetch a stale stage
+        issue(slot, min(kt + dma::STAGES, nk - 1));
+        read((dma::KS - 2) & 1, nslot, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma((dma::KS - 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        read((dma::KS - 1) & 1, nslot, 1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // no copy in flight when the block ends
+
+    // epilogue, one 32-row band of the wavefront at a time; the residual's old values are loaded 32
+    // at a time (clamped rows, no branches) before the adds and the guarded stores
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        const int rbase = m0 + wm * 128 + i * 32 + (lane >> 5) * 4;
+        if constexpr (EPI == GEMV_EPI_RESIDUAL) {
+#pragma unroll
+            for (int j0 = 0; j0 < FN; j0 += 2) {
+                float old[2][16];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int col = n0 + wn * WN + (j0 + j) * 32 + (lane & 31);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = min(rbase + (r >> 2) * 8 + (r & 3), p.M - 1);
+                        old[j][r] = p.C[(size_t)row * p.ldc + col];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int col = n0 + wn * WN + (j0 + j) * 32 + (lane & 31);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = rbase + (r >> 2) * 8 + (r & 3);
+                        if (row < p.M) p.C[(size_t)row * p.ldc + col] = old[j][r] + acc[0][i][j0 + j][r];
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int col = n0 + wn * WN + j * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = rbase + (r >> 2) * 8 + (r & 3);
+                    if (row >= p.M) continue;
+                    const float v = acc[0][i][j][r];
+                    if (EPI == GEMV_EPI_STORE) {
+                        p.C[(size_t)row * p.ldc + col] = p.bias ? v + p.bias[col] : v;
+                    } else {
+                        const float g = v, u = acc[NW - 1][i][j][r];
+                        const float sg = 1.0f / (expf(-g) + 1.0f);
+                        p.O[(size_t)row * p.ldo + col] = Mf::from_float(u * (g * sg));
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <bool F16, int EPI>
+int launch_dma(const GemmParams& p, hipStream_t st) {
+    constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
+    const int mt = (p.M + dma::BM - 1) / dma::BM, nt = p.N / (dma::BNW / NW);
+    static bool attr_set = false;  // 128 KB of dynamic LDS needs the per-kernel opt-in
+    if (!attr_set) {
+        AR_HIP_TRY(hipFuncSetAttribute((const void*)gemm_dma_kernel<F16, EPI>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, dma::LDS_BYTES));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((gemm_dma_kernel<F16, EPI>), dim3(mt * nt), dim3(dma::NTHR), dma::LDS_BYTES, st, p, mt, nt);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
+// The large-tile kernel pays off with at least kDmaMinTiles tiles (measured on the prefill shapes:
+// +7-13% at 65,536 rows; fewer, larger tiles leave CUs idle on 2,048-row prompts).
+constexpr long long kDmaMinTiles = 1024;
+
+template <int EPI>
+bool use_dma(const GemmParams& p) {
+    constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
+    const int bn = dma::BNW / NW;
+    if (p.ksplit != 1 || p.N % bn || p.K % dma::BK) return false;
+    return (long long)((p.M + dma::BM - 1) / dma::BM) * (p.N / bn) >= kDmaMinTiles;
+}
+
 template <int EPI, int BMT>
 int launch_bm(const GemmParams& p, bool f16, hipStream_t st) {
     const int mt = (p.M + BMT - 1) / BMT, nt = p.N / BN;
@@ -236,6 +446,7 @@ int launch_bm(const GemmParams& p, bool f16, hipStream_t st) {
 // 51 us, gate/up 163 us with 256-row tiles vs 176 us.
 template <int EPI>
 int launch_t(const GemmParams& p, bool f16, hipStream_t st) {
+    if (use_dma<EPI>(p)) return f16 ? launch_dma<true, EPI>(p, st) : launch_dma<false, EPI>(p, st);
     const long long blocks256 = (long long)((p.M + 255) / 256) * (p.N / BN) * p.ksplit;
     if (blocks256 >= (EPI == GEMV_EPI_SWIGLU ? 256 : 512)) return launch_bm<EPI, 256>(p, f16, st);
     return launch_bm<EPI, 128>(p, f16, st);

@@ -64,6 +64,40 @@ def test_gemm_residual_and_swiglu(ctx):
     assert rel_err(o, u * (g / (1 + np.exp(-g)))) <= 8e-3
 
 
+@pytest.mark.parametrize("K", [64, 192, 320])
+def test_gemm_large_tile_path(ctx, K):
+    """Products with >= 1024 256x256 tiles take the direct-to-LDS kernel: ragged M (8200 rows),
+    1, 3 and 5 k-tiles (fewer k-tiles than stages included), all three epilogues."""
+    M, N = 8200, 8192
+    r = np.random.default_rng(K)
+    A = bf16(r.standard_normal((M, K)))
+    W = bf16(r.standard_normal((N, K)) * 0.05)
+    W2 = bf16(r.standard_normal((N // 2, K)) * 0.05)
+    b = r.standard_normal(N).astype(np.float32)
+    C0 = r.standard_normal((M, N)).astype(np.float32)
+    rows = np.concatenate([np.arange(64), r.choice(M, 64, replace=False), np.arange(M - 40, M)])
+    Ad, Wd, W2d = ctx.to_device(bits(A)), ctx.to_device(bits(W)), ctx.to_device(bits(W2))
+    Cd = ctx.allocate(M * N * 4)
+    ctx.gemm_bf16(Ad, Wd, M, N, K, hw.GEMM_STORE, bias=ctx.to_device(b), C=Cd)
+    ctx.synchronize()
+    got = Cd.download(np.float32, M * N).reshape(M, N)[rows]
+    ref = A[rows].astype(np.float64) @ W.astype(np.float64).T + b
+    assert rel_err(got, ref) <= 1e-5
+    Cd.upload(C0)
+    ctx.gemm_bf16(Ad, Wd, M, N, K, hw.GEMM_RESIDUAL, C=Cd)
+    ctx.synchronize()
+    got = Cd.download(np.float32, M * N).reshape(M, N)[rows]
+    assert rel_err(got, C0[rows] + A[rows].astype(np.float64) @ W.astype(np.float64).T) <= 1e-5
+    Nh = N // 2
+    Od = ctx.allocate(M * Nh * 2)
+    ctx.gemm_bf16(Ad, Wd, M, Nh, K, hw.GEMM_SWIGLU, W2=W2d, O=Od)
+    ctx.synchronize()
+    g = A[rows].astype(np.float64) @ W[:Nh].astype(np.float64).T
+    u = A[rows].astype(np.float64) @ W2.astype(np.float64).T
+    o = (Od.download(np.uint16, M * Nh).astype(np.uint32) << 16).view(np.float32).reshape(M, Nh)[rows]
+    assert rel_err(o, u * (g / (1 + np.exp(-g)))) <= 8e-3
+
+
 def test_gemm_rejects_bad_shapes(ctx):
     z = ctx.allocate(1 << 16)
     with pytest.raises(hw.HardwareException):
