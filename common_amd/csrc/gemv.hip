@@ -32,6 +32,8 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(!a.y_hi || a.epilogue != GEMV_EPI_ARGMAX, "GEMV: no output planes for the argmax epilogue");
     if (mfma) return gemv_launch_mfma(p, a.epilogue, stream);
     if (a.batch >= 3) return gemv_launch_batched(p, a.wdtype, a.epilogue, stream);
+    if (a.epilogue == GEMV_EPI_ARGMAX && gemv_argmax_fits(a.cols, a.batch, a.wdtype) && a.x_stride % 4 == 0)
+        return gemv_launch_argmax(p, a.wdtype, stream);
     if (gemv_rx_fits(a.rows, a.cols, a.batch, a.wdtype, a.epilogue, a.norm_w != nullptr) && (a.cols * 4) % 16 == 0)
         return gemv_launch_rx(p, a.wdtype, a.epilogue, stream);
     const gemv::Shape s = gemv::shape_for(a.rows, a.cols, a.batch, a.wdtype, a.epilogue);

@@ -464,5 +464,9 @@ int gemv_launch_batched(const gemv::Params& p, int wdtype, int epi, hipStream_t 
 // Batch 1, no argmax, cols a multiple of the 64-lane chunk (gemv_rx.hip): input held in registers.
 bool gemv_rx_fits(int rows, int cols, int batch, int wdtype, int epi, bool norm);
 int gemv_launch_rx(const gemv::Params& p, int wdtype, int epi, hipStream_t st);
+// Argmax epilogue (final RMSNorm + logits + greedy keys), batch 1-2, cols = 1, 2 or 4 full 64-lane
+// chunks (gemv_argmax.hip): persistent grid, input in registers.
+bool gemv_argmax_fits(int cols, int batch, int wdtype);
+int gemv_launch_argmax(const gemv::Params& p, int wdtype, hipStream_t st);
 // bf16 weights, batches of 3..16, cols % 32 == 0 (gemv_mfma.hip): 16-row tiles on the MFMA units.
 int gemv_launch_mfma(const gemv::Params& p, int epi, hipStream_t st);
