@@ -9,7 +9,7 @@ trip inside the timed region).  Default: warmup 5 + 251 timed = the config's 256
 
 Extra fields on the JSON line:
   roofline      dominant kernel's achieved HBM GB/s, from HIP events bracketing every launch
-                of that kernel class on the model's stream over a probe pass of --probe-steps
+                of that kernel class on the model's stream, --probe-steps decode steps per class
   cpu_baseline  the CPU oracle (reference semantics, fp32) on this host, over a bounded sample
   c4            BASELINE config 4 (Qwen3-1.7B shape, bf16 weights): a 2048-token prompt through the
                 MFMA prefill path (tok/s and fraction of the 2.5 PFLOP/s dense bf16/fp16 MFMA peak),
@@ -344,7 +344,8 @@ def main():
 
     cfg = C.C3_0_6B
     n_prompt = C.C3_PROMPT
-    total = n_prompt + args.warmup + args.steps + args.probe_steps
+    n_classes = 6  # kernel classes timed by the probe pass below
+    total = n_prompt + args.warmup + args.steps + args.probe_steps * n_classes
     if total > cfg.seq_len:
         import dataclasses
         cfg = dataclasses.replace(cfg, seq_len=total)
@@ -386,7 +387,8 @@ def main():
     names = {q.KT_LOGITS: "logits_gemv_argmax", q.KT_GATE_UP: "gate_up_gemv_swiglu", q.KT_QKV: "qkv_gemv_rmsnorm",
              q.KT_DOWN: "down_gemv_residual", q.KT_O: "o_gemv_residual", q.KT_ATTENTION: "attention_decode"}
     probe_left = cfg.seq_len - (pos0 + args.steps)
-    per_class = max(1, min(args.probe_steps, probe_left // len(names))) if probe_left >= len(names) else 0
+    assert len(names) == n_classes
+    per_class = min(args.probe_steps, probe_left // n_classes)
     for which, name in names.items():
         if per_class == 0:
             break
