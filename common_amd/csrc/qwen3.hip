@@ -563,6 +563,19 @@ extern "C" int ar_hip_qwen3_destroy(ar_qwen3* m) {
 
 extern "C" int ar_hip_qwen3_set_weight(ar_qwen3* m, const char* key, const void* src, int src_dtype, int64_t n) {
     AR_CHECK_ARG(m && key && src, "null argument");
+    if (!strcmp(key, AR_ROPE_TABLE_KEY)) {
+        // a given (cos, sin) table replaces the one computed from rope_theta, as a model built with
+        // a freqCis producer uses it (Llama2.java model(), Llama2Weights.freqCis): rows for
+        // positions 0.., (head_size / 2) pairs each; the first seq_len rows are used
+        const int64_t per_pos = m->cfg.head_size;  // head_size / 2 pairs of two values
+        AR_CHECK_ARG(src_dtype == AR_DTYPE_F32, "%s: fp32 values expected", key);
+        AR_CHECK_ARG(n % per_pos == 0 && n / per_pos >= m->S, "%s: %lld values do not hold %d positions x %lld",
+                     key, (long long)n, m->S, (long long)per_pos);
+        AR_HIP_TRY(hipMemcpyAsync(m->rope_tab, src, (size_t)m->S * per_pos * sizeof(float), hipMemcpyHostToDevice,
+                                  m->ctx->stream));
+        AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+        return AR_HIP_OK;
+    }
     auto it = m->slots.find(key);
     if (it == m->slots.end()) {
         ar_set_error("unknown weight key '%s'", key);

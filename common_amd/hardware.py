@@ -125,6 +125,24 @@ _SIGS = {
     "ar_hip_state_dict_save": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int]),
     "ar_hip_qwen3_infer_config": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_qwen3_load_state_dict": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    # include/ar_llama2.h
+    "ar_hip_llama2_parse_config": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "ar_hip_llama2_open": (ctypes.c_int, [ctypes.c_char_p, _c_void_pp]),
+    "ar_hip_llama2_close": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_llama2_config": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "ar_hip_llama2_tensor": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                            ctypes.POINTER(ctypes.c_int64)]),
+    "ar_hip_llama2_create_model": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                                  ctypes.c_int, _c_void_pp]),
+    "ar_hip_bpe_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, _c_void_pp]),
+    "ar_hip_bpe_create": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _c_void_pp]),
+    "ar_hip_bpe_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "ar_hip_bpe_vocab_size": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
+    "ar_hip_bpe_token": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), _c_int_p,
+                                        ctypes.POINTER(ctypes.c_float)]),
+    "ar_hip_bpe_lookup": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int, _c_int_p]),
+    "ar_hip_bpe_encode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int, ctypes.c_void_p,
+                                         ctypes.c_int, _c_int_p]),
 }
 
 

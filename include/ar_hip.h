@@ -176,7 +176,11 @@ int ar_hip_qwen3_destroy(ar_qwen3 *m);
 
 /* Uploads one tensor by its HF state-dict key, as StateDictionary.get supplies them to
  * Qwen3.model (engine/ml/.../StateDictionary.java; Qwen3.java:338-384).  src is host memory
- * holding n_elems values of src_dtype in the HF (out, in) row-major layout. */
+ * holding n_elems values of src_dtype in the HF (out, in) row-major layout.
+ * Key AR_ROPE_TABLE_KEY takes a RoPE table of fp32 (cos, sin) pairs, (positions >= seq_len,
+ * head_size / 2, 2), that replaces the one computed from rope_theta: the freqCis a model built
+ * from a checkpoint supplies (Llama2Weights.java freqCis, Llama2.java model()). */
+#define AR_ROPE_TABLE_KEY "freq_cis"
 int ar_hip_qwen3_set_weight(ar_qwen3 *m, const char *key, const void *src, int src_dtype, int64_t n_elems);
 /* Checks every required tensor is present and builds the decode plan. */
 int ar_hip_qwen3_finalize(ar_qwen3 *m);

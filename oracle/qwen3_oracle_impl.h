@@ -147,9 +147,18 @@ void FN(oracle_rope_rotate_split)(REAL *x, int heads, int hd, const REAL *freqs_
 
 /* Split-half -> rotate -> unsplit on a flat (heads*hd) vector, as the Qwen3 graph chains
  * them (AttentionFeatures.java:847-851 for keys, 893-897 for queries). */
+/* The same with a given freqCis row (hd/2 (cos, sin) pairs), as a model built from a
+ * checkpoint's table uses it (engine/ml/.../llama2/Llama2.java:181-192, Llama2Weights.freqCis). */
+void FN(oracle_rope_flat_row)(REAL *x, int heads, int hd, const REAL *freq_row) {
+    REAL *tmp = (REAL *)malloc(sizeof(REAL) * (size_t)heads * hd);
+    FN(oracle_split_half)(tmp, x, heads, hd);
+    FN(oracle_rope_rotate_split)(tmp, heads, hd, freq_row);
+    FN(oracle_unsplit_half)(x, tmp, heads, hd);
+    free(tmp);
+}
+
 void FN(oracle_rope_flat)(REAL *x, int heads, int hd, int pos, double theta) {
     int fd = hd / 2;
-    REAL *tmp = (REAL *)malloc(sizeof(REAL) * (size_t)heads * hd);
     REAL *fr = (REAL *)malloc(sizeof(REAL) * (size_t)fd * 2);
     REAL c = (REAL)(-2.0 * log(theta) / hd);
     for (int f = 0; f < fd; f++) {
@@ -158,10 +167,7 @@ void FN(oracle_rope_flat)(REAL *x, int heads, int hd, int pos, double theta) {
         fr[2 * f] = FN(r_cos)(ang);
         fr[2 * f + 1] = FN(r_sin)(ang);
     }
-    FN(oracle_split_half)(tmp, x, heads, hd);
-    FN(oracle_rope_rotate_split)(tmp, heads, hd, fr);
-    FN(oracle_unsplit_half)(x, tmp, heads, hd);
-    free(tmp);
+    FN(oracle_rope_flat_row)(x, heads, hd, fr);
     free(fr);
 }
 
@@ -239,10 +245,11 @@ void FN(oracle_attention)(REAL *out, const REAL *q, const REAL *kc, const REAL *
  * qk_group = heads*hd / kv_heads*hd (whole vector, reference) or hd (per head, HF);
  * pass group <= 0 to select the whole-vector form.
  */
-void FN(oracle_attention_block)(REAL *out, const REAL *q_raw, const REAL *k_raw, const REAL *v_raw,
-                                const REAL *q_norm, const REAL *k_norm, REAL *kc, REAL *vc,
-                                int heads, int kv_heads, int hd, int pos, int seq_len,
-                                double theta, double qk_eps, int per_head_norm, int full_seq) {
+static void FN(attention_block_impl)(REAL *out, const REAL *q_raw, const REAL *k_raw, const REAL *v_raw,
+                                     const REAL *q_norm, const REAL *k_norm, REAL *kc, REAL *vc,
+                                     int heads, int kv_heads, int hd, int pos, int seq_len,
+                                     double theta, const REAL *freq_row, double qk_eps, int per_head_norm,
+                                     int full_seq) {
     int qd = heads * hd, kd = kv_heads * hd;
     REAL *q = (REAL *)malloc(sizeof(REAL) * (size_t)qd);
     REAL *k = (REAL *)malloc(sizeof(REAL) * (size_t)kd);
@@ -254,13 +261,26 @@ void FN(oracle_attention_block)(REAL *out, const REAL *q_raw, const REAL *k_raw,
         if (per_head_norm) FN(oracle_rmsnorm_grouped)(k, k_raw, k_norm, kd, hd, qk_eps);
         else FN(oracle_rmsnorm)(k, k_raw, k_norm, kd, qk_eps);
     } else memcpy(k, k_raw, sizeof(REAL) * kd);
-    FN(oracle_rope_flat)(k, kv_heads, hd, pos, theta);
-    FN(oracle_rope_flat)(q, heads, hd, pos, theta);
+    if (freq_row) {
+        FN(oracle_rope_flat_row)(k, kv_heads, hd, freq_row);
+        FN(oracle_rope_flat_row)(q, heads, hd, freq_row);
+    } else {
+        FN(oracle_rope_flat)(k, kv_heads, hd, pos, theta);
+        FN(oracle_rope_flat)(q, heads, hd, pos, theta);
+    }
     memcpy(kc + (size_t)pos * kd, k, sizeof(REAL) * kd);
     memcpy(vc + (size_t)pos * kd, v_raw, sizeof(REAL) * kd);
     FN(oracle_attention)(out, q, kc, vc, heads, kv_heads, hd, pos, seq_len, full_seq);
     free(q);
     free(k);
+}
+
+void FN(oracle_attention_block)(REAL *out, const REAL *q_raw, const REAL *k_raw, const REAL *v_raw,
+                                const REAL *q_norm, const REAL *k_norm, REAL *kc, REAL *vc,
+                                int heads, int kv_heads, int hd, int pos, int seq_len,
+                                double theta, double qk_eps, int per_head_norm, int full_seq) {
+    FN(attention_block_impl)(out, q_raw, k_raw, v_raw, q_norm, k_norm, kc, vc, heads, kv_heads, hd, pos, seq_len,
+                             theta, NULL, qk_eps, per_head_norm, full_seq);
 }
 
 /* indexOfMax -- compute/algebra/.../AggregationFeatures.java:111-121: start at index 0,
@@ -285,6 +305,7 @@ typedef struct FN(oracle_model) {
     oracle_cfg cfg;
     int q_dim, kv_dim;
     REAL *embed, *final_norm, *lm_head;
+    REAL *rope_tab; /* (seq_len, hd/2, 2) freqCis given as a weight, or NULL: computed from theta */
     FN(oracle_layer) *layers;
     int pos;
     REAL *x, *h, *q, *k, *v, *att, *tmp, *g, *u;
@@ -327,7 +348,7 @@ void FN(oracle_model_destroy)(void *mp) {
     for (int l = 0; l < m->cfg.n_layers; l++) FN(free_layer)(&m->layers[l]);
     free(m->layers);
     if (m->lm_head != m->embed) free(m->lm_head);
-    free(m->embed); free(m->final_norm);
+    free(m->embed); free(m->final_norm); free(m->rope_tab);
     free(m->x); free(m->h); free(m->q); free(m->k); free(m->v); free(m->att); free(m->tmp);
     free(m->g); free(m->u);
     free(m);
@@ -359,6 +380,12 @@ int FN(oracle_model_set_weight)(void *mp, const char *key, const float *src, lon
         if (c->tied) return 0; /* tied embeddings: the embedding matrix is the head */
         free(m->lm_head);
         m->lm_head = FN(copy_in)(src, (size_t)n);
+        return 0;
+    }
+    if (!strcmp(key, "freq_cis")) { /* (positions >= seq_len, hd/2, 2); the first seq_len rows are kept */
+        if (n % c->head_dim != 0 || n / c->head_dim < c->seq_len) return -2;
+        free(m->rope_tab);
+        m->rope_tab = FN(copy_in)(src, (size_t)c->seq_len * c->head_dim);
         return 0;
     }
     if (!strcmp(key, "model.norm.weight")) {
@@ -423,9 +450,10 @@ int FN(oracle_model_step)(void *mp, int token, REAL *logits_out) {
         FN(oracle_dense)(m->k, L->wk, m->h, L->bk, kd, d);
         FN(oracle_dense)(m->v, L->wv, m->h, L->bv, kd, d);
         FN(oracle_dense)(m->q, L->wq, m->h, L->bq, qd, d);
-        FN(oracle_attention_block)(m->att, m->q, m->k, m->v, L->q_norm, L->k_norm, L->kc, L->vc,
-                                   c->n_heads, c->n_kv_heads, hd, pos, c->seq_len, c->rope_theta,
-                                   c->qk_eps, c->qk_norm_mode == 1, c->full_seq_mask);
+        FN(attention_block_impl)(m->att, m->q, m->k, m->v, L->q_norm, L->k_norm, L->kc, L->vc,
+                                 c->n_heads, c->n_kv_heads, hd, pos, c->seq_len, c->rope_theta,
+                                 m->rope_tab ? m->rope_tab + (size_t)pos * hd : NULL,
+                                 c->qk_eps, c->qk_norm_mode == 1, c->full_seq_mask);
         FN(oracle_dense)(m->tmp, L->wo, m->att, NULL, d, qd);
         for (int i = 0; i < d; i++) m->x[i] = m->x[i] + m->tmp[i];
         /* feed-forward branch: x += W2 (W3 h (.) silu(W1 h)) with silu(g) = g * 1/(exp(-g)+1)

@@ -1,5 +1,5 @@
 """TEST INFRASTRUCTURE ONLY: a plain-Python restatement of the reference tokenizer, the checker
-for the native one (common_amd/csrc/tokenizer.cpp).  Only tests/ import it.
+for the native ones (common_amd/csrc/tokenizer.cpp, common_amd/csrc/bpe.cpp).  Only tests/ import it.
 
   * pre-tokenisation: the reference's pattern (RegexPreTokenizer.java:89-98) run by the `regex`
     package's backtracking engine, with Java's ASCII meaning of \\s / \\S written out (Python's
@@ -8,7 +8,8 @@ for the native one (common_amd/csrc/tokenizer.cpp).  Only tests/ import it.
   * BPE (ByteLevelBPETokenizer.applyBPEMerges): merge the lowest-priority adjacent pair, the
     leftmost on ties, one at a time;
   * Qwen3Tokenizer.encode(text, addBos, addEos) / decode (Qwen3Tokenizer.java:271-296,
-    ByteLevelBPETokenizer.decode), merges.txt parsing (loadMergesFromFile, :150-199).
+    ByteLevelBPETokenizer.decode), merges.txt parsing (loadMergesFromFile, :150-199);
+  * llama2.c's score-driven BPE (BPE.java:33-101): llama2_bpe_encode.
 """
 from __future__ import annotations
 
@@ -99,3 +100,38 @@ class Tokenizer:
     def decode(self, ids) -> str:
         s = "".join(self.vocab[i] for i in ids if i not in (BOS, EOS, PAD, UNK) and 0 <= i < len(self.vocab))
         return bytes(_C2B[c] for c in s).decode("utf-8", errors="replace")
+
+
+# ---- llama2.c score-driven BPE (engine/ml/.../BPE.java) ---------------------------------------
+
+def llama2_bpe_encode(text: str, vocab: list[str], scores) -> list[int]:
+    """BPE.encode (BPE.java:57-101) with BPE.lookup's linear scan for the first equal entry
+    (:33-41).  Java strings are UTF-16: the text is split into UTF-16 units, so a supplementary
+    character becomes two lone surrogates that no entry equals (the reference throws; so does this).
+    Scores compare as float32 against a floor of -1e10f."""
+    import numpy as np
+    raw = text.encode("utf-16-le", "surrogatepass")
+    units = [raw[i:i + 2].decode("utf-16-le", "surrogatepass") for i in range(0, len(raw), 2)]
+
+    def lookup(s):
+        for i, v in enumerate(vocab):
+            if v == s:
+                return i
+        return -1
+
+    tokens = []
+    for u in units:
+        i = lookup(u)
+        if i == -1:
+            raise ValueError(f"no token for {u!r}")
+        tokens.append(i)
+    while True:
+        best_score, best_id, best_index = np.float32(-1e10), -1, -1
+        for i in range(len(tokens) - 1):
+            j = lookup(vocab[tokens[i]] + vocab[tokens[i + 1]])
+            if j != -1 and np.float32(scores[j]) > best_score:
+                best_score, best_id, best_index = np.float32(scores[j]), j, i
+        if best_index == -1:
+            return tokens
+        tokens[best_index] = best_id
+        del tokens[best_index + 1]
