@@ -17,6 +17,8 @@ Extra fields on the JSON line:
   c5            BASELINE config 5 (Qwen3-4B shape, bf16 weights): 8 sequences x 8192-token prompts
                 prefilled together, then 64 greedy steps of all 8 (aggregate tok/s, HBM fraction)
   c2            BASELINE config 2: the decode-step attention op at a 4096-row cache (us per call)
+  llama2        the Llama2 family: a stories110M-shaped llama2.c checkpoint (synthetic weights)
+                loaded through the checkpoint path, greedy decode tok/s and HBM fraction
   sampled_c3    the C3 decode with on-device sampling instead of greedy selection: sampleToken
                 at temperature 0.8 / top-p 0.9, and the sample function of AutoregressiveModel.of
                 at temperature 0.7 (tok/s)
@@ -293,6 +295,66 @@ def load_traffic():
         return None
 
 
+def llama2_section(args):
+    """The Llama2 family (Llama2.java): a stories110M-shaped llama2.c checkpoint (d768, 12 layers,
+    12 heads, F2048, V32000, seq 1024, tied classifier) with synthetic weights, written to a
+    temporary file and loaded through the checkpoint path; BOS then greedy decode, timed over
+    the decode steps as Llama2.main reports tokens per second (Llama2.java:80-96)."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from common_amd.llama2 import BOS, Llama2, Llama2Config, write_checkpoint
+
+    cfg = Llama2Config(768, 2048, 12, 12, 12, 32000, 1024, True, 64)
+    d, F, L, V, S, hd = cfg.dim, cfg.hidden_dim, cfg.layer_count, cfg.vocab_size, cfg.seq_len, cfg.head_size
+    rng = np.random.default_rng(args.seed + 7)
+
+    def normal(shape, mean=0.0):
+        return (mean + 0.02 * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+
+    invf = 1.0 / (10000.0 ** (np.arange(0, hd, 2) / hd))
+    ang = np.outer(np.arange(S), invf)
+    w = {"tokenEmbeddings": normal((V, d)), "rmsAttWeights": normal((L, d), 1.0), "wq": normal((L, d, d)),
+         "wk": normal((L, d, d)), "wv": normal((L, d, d)), "wo": normal((L, d, d)),
+         "rmsFfn": normal((L, d), 1.0), "w1": normal((L, F, d)), "w2": normal((L, d, F)), "w3": normal((L, F, d)),
+         "rmsFinalWeight": normal(d, 1.0), "freqCisReal": np.cos(ang), "freqCisImag": np.sin(ang)}
+    tmp = tempfile.mkdtemp(prefix="llama2_bench_")
+    try:
+        path = os.path.join(tmp, "stories110M_synthetic.bin")
+        write_checkpoint(path, cfg, w)
+        del w
+        t0 = time.time()
+        with Llama2(path, None) as m:
+            load_s = time.time() - t0
+            am = m.model
+            am.use_graph(not args.no_graph)
+            am.reset()
+            am.set_prompt([BOS])
+            warm = 8
+            am.run(1 + warm)
+            steps = S - 1 - warm - 1
+            m.ctx.synchronize()
+            t1 = time.perf_counter()
+            am.run(steps)
+            el = time.perf_counter() - t1
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    weights = (V * d + L * (4 * d * d + 3 * d * F + 2 * d) + d) * 4
+    pos0 = 1 + warm
+    kv = float(np.mean([2 * (p + 1) * d * 4 * L for p in range(pos0, pos0 + steps)]))
+    per_tok = weights + kv
+    tok_s = steps / el
+    log(f"[bench] Llama2 (stories110M shape, fp32): {1000 * el / steps:.3f} ms/token, {tok_s:.0f} tok/s; "
+        f"checkpoint load {load_s:.2f} s")
+    return {"workload": "Llama2: stories110M shape fp32 (d768, 12L, 12 heads, hd64, F2048, V32000, tied), "
+                        "llama2.c checkpoint with synthetic N(0,0.02) weights, BOS + greedy decode",
+            "steps": steps, "decode_positions": f"{pos0}..{pos0 + steps - 1}", "tok_s": round(tok_s, 1),
+            "ms_per_token": round(1000 * el / steps, 4), "algorithmic_bytes_per_token": round(per_tok),
+            "hbm_frac": round(per_tok * tok_s / 1e9 / HBM_PEAK_GBS, 4), "checkpoint_load_s": round(load_s, 2)}
+
+
 def step_bytes_batch(cfg, pos, batch, kv_bytes=4):
     """Bytes one batched decode step must move at position `pos`: weights once, KV per sequence."""
     kv = cfg.layer_count * 2 * cfg.kv_dim * kv_bytes * (pos + 1)
@@ -313,7 +375,8 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 batch-8 long-context section")
     ap.add_argument("--no-c2", action="store_true", help="skip the config-2 attention-op section")
     ap.add_argument("--no-fp16-kv", action="store_true", help="skip the config-5 decode run with an fp16 KV cache")
-    ap.add_argument("--sections", default="c3,c4,c5,c2",
+    ap.add_argument("--no-llama2", action="store_true", help="skip the Llama2 (stories110M shape) section")
+    ap.add_argument("--sections", default="c3,c4,c5,c2,llama2",
                     help="comma list of workloads to run (c3 is the headline; the others are extra fields)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload of the rocprofv3 FETCH_SIZE / WRITE_SIZE passes and exit")
@@ -331,7 +394,8 @@ def main():
     if "c3" not in sections:  # profiling aid: only the named extra sections, one JSON line of them
         out = {"c4": c4_section(args) if "c4" in sections and not args.no_c4 else None,
                "c5": c5_section(args) if "c5" in sections and not args.no_c5 else None,
-               "c2": c2_section(args) if "c2" in sections and not args.no_c2 else None}
+               "c2": c2_section(args) if "c2" in sections and not args.no_c2 else None,
+               "llama2": llama2_section(args) if "llama2" in sections and not args.no_llama2 else None}
         print(json.dumps(out), flush=True)
         return
 
@@ -488,6 +552,7 @@ def main():
         "c4": c4_section(args) if "c4" in sections and not args.no_c4 else None,
         "c5": c5_section(args) if "c5" in sections and not args.no_c5 else None,
         "c2": c2_section(args) if "c2" in sections and not args.no_c2 else None,
+        "llama2": llama2_section(args) if "llama2" in sections and not args.no_llama2 else None,
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,
