@@ -21,23 +21,6 @@ using namespace gemv;
 
 constexpr int kAmThreads = 256, kAmWaves = kAmThreads / 64;
 
-// Sum over the 64 lanes on the DPP network (no LDS round trips): quad swaps, row shifts by 4 and 8,
-// then the row totals broadcast across rows; the total lands in lane 63 (the other lanes hold
-// partial sums).
-template <int CTRL, int ROW_MASK>
-__device__ inline float dpp_add(float v) {
-    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, true));
-}
-__device__ inline float dpp_sum_lane63(float v) {
-    v = dpp_add<0xB1, 0xF>(v);   // quad_perm 1,0,3,2
-    v = dpp_add<0x4E, 0xF>(v);   // quad_perm 2,3,0,1
-    v = dpp_add<0x114, 0xF>(v);  // row_shr:4
-    v = dpp_add<0x118, 0xF>(v);  // row_shr:8
-    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
-    return v;
-}
-
 template <typename WT, int NB, int RPW, int NCH>
 __global__ __launch_bounds__(kAmThreads) void gemv_argmax_kernel(Params p) {
     using V = WVec<WT>;

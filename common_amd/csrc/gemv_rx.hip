@@ -14,7 +14,8 @@
 //    so the input is ready first and the RMSNorm sum of squares overlaps the weight stream);
 //  * the RMSNorm factor is computed per wavefront from the same registers (the whole row is
 //    covered, so no block-wide reduction) and applied to the finished dot product;
-//  * no LDS and no barrier; one wavefront butterfly per row.
+//  * no LDS and no barrier; each row (and the sum of squares) is summed over the lanes on the DPP
+//    network into lane 63, which applies the epilogue and stores.
 // Shapes: cols a multiple of the 64-lane chunk (256 fp32 / 512 bf16 columns), at most 16 fp32 or
 // 12 bf16 chunks (8 with the RMSNorm prologue).
 #include "gemv_impl.h"
@@ -40,8 +41,10 @@ __global__ __launch_bounds__(kRxWaves * 64) void gemv_rx_kernel(Params p, int nc
     const int row0 = (blockIdx.x * kRxWaves + wave) * RW;
     const bool norm = p.norm_w != nullptr;
 
-    float res = 0.f;  // residual epilogue: lane r owns output row row0 + r
-    if (EPI == GEMV_EPI_RESIDUAL && lane < RW && row0 + lane < p.rows) res = p.y[row0 + lane];
+    float res[RW];  // residual epilogue: lane 63 (which finishes the row sums) holds the old rows
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+        res[r] = (EPI == GEMV_EPI_RESIDUAL && lane == 63 && row0 + r < p.rows) ? p.y[row0 + r] : 0.f;
 
     // input (and gain) slices of this lane: VEC values at column c * CH + lane * VEC
     float xv[NCH][VEC];
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(kRxWaves * 64) void gemv_rx_kernel(Params p, int nc
                     xv[c][j] *= gv[c][j];
                 }
             }
-        ss = gemv::wave_sum(ss);
+        ss = gemv::dpp_sum_lane63(ss);  // lane 63 alone finishes and stores the rows
         rn = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
     }
 
@@ -110,18 +113,18 @@ __global__ __launch_bounds__(kRxWaves * 64) void gemv_rx_kernel(Params p, int nc
 #pragma unroll
                 for (int j = 0; j < VEC; j++) a = fmaf(wf[j], xv[c][j], a);
             }
-        acc[r] = gemv::wave_sum(a) * rn;
+        acc[r] = gemv::dpp_sum_lane63(a) * rn;  // meaningful in lane 63 only
     }
 
 #pragma unroll
     for (int r = 0; r < RW; r++) {
         const int row = row0 + r;
-        if (lane == r && row < p.rows) {
+        if (lane == 63 && row < p.rows) {
             float* yp = p.y + row;
             if (EPI == GEMV_EPI_STORE) {
                 *yp = p.bias ? acc[r] + p.bias[row] : acc[r];
             } else if (EPI == GEMV_EPI_RESIDUAL) {
-                *yp = res + acc[r];
+                *yp = res[r] + acc[r];
             } else {  // SwiGLU: acc[r] = gate, acc[RW + r] = up
                 const float g = acc[r];
                 const float sg = 1.0f / (expf(-g) + 1.0f);
