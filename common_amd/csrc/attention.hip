@@ -67,16 +67,55 @@ struct AttnParams {
     uint16_t* out_lo;
 };
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane steps without the LDS crossbar (ds_bpermute): DPP within 16-lane rows, gfx950's
+// permlane swaps across rows.
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, true));
+}
+// sum over each 16-lane row, in every lane of the row: quad swaps, half-row mirror, row mirror
+__device__ inline float row16_sum(float v) {
+    v += dpp_mov<0xB1, 0xF>(v);   // quad_perm 1,0,3,2
+    v += dpp_mov<0x4E, 0xF>(v);   // quad_perm 2,3,0,1
+    v += dpp_mov<0x141, 0xF>(v);  // row_half_mirror: the other quad of the half row
+    v += dpp_mov<0x140, 0xF>(v);  // row_mirror: the other half row
     return v;
 }
-
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+// total over the 64 lanes, in lane 63 only (row shifts, then row broadcasts)
+__device__ inline float wave_sum_lane63(float v) {
+    v += dpp_mov<0xB1, 0xF>(v);
+    v += dpp_mov<0x4E, 0xF>(v);
+    v += dpp_mov<0x114, 0xF>(v);  // row_shr:4
+    v += dpp_mov<0x118, 0xF>(v);  // row_shr:8
+    v += dpp_mov<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_mov<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
     return v;
+}
+// maximum over the 64 lanes, in lane 63 only (lanes without a source read -inf)
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_max_step(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), CTRL,
+                                                               ROW_MASK, 0xF, false)));
+}
+__device__ inline float wave_max_lane63(float v) {
+    v = dpp_max_step<0xB1, 0xF>(v);
+    v = dpp_max_step<0x4E, 0xF>(v);
+    v = dpp_max_step<0x114, 0xF>(v);
+    v = dpp_max_step<0x118, 0xF>(v);
+    v = dpp_max_step<0x142, 0xA>(v);
+    v = dpp_max_step<0x143, 0xC>(v);
+    return v;
+}
+// the value held by lane ^ 16 (permlane16_swap of v with itself: the first result holds the
+// even rows in both halves of each row pair, the second the odd rows)
+__device__ inline float xor16(float v, int lane) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((lane & 16) ? r[0] : r[1]);
+}
+// the value held by lane ^ 32 (permlane32_swap: lower half in the first result, upper in the second)
+__device__ inline float xor32(float v, int lane) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((lane & 32) ? r[0] : r[1]);
 }
 
 // (cos, sin) of pos * exp(f * -2 ln(theta) / hd): from the table the model precomputes in
@@ -240,9 +279,9 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
                 const float4 v = *reinterpret_cast<const float4*>(k_raw + i);
                 sk += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
-            sq = wave_sum(sq);
-            sk = wave_sum(sk);
-            if (lane == 0) sq_s[wave] = make_float2(sq, sk);
+            sq = wave_sum_lane63(sq);
+            sk = wave_sum_lane63(sk);
+            if (lane == 63) sq_s[wave] = make_float2(sq, sk);
             __syncthreads();
             float tq = 0.f, tk = 0.f;
 #pragma unroll
@@ -258,8 +297,8 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
                 const float* src = (j < G) ? q_raw + (size_t)(kvh * G + j) * HD : k_raw + (size_t)kvh * HD;
                 float s = 0.f;
                 for (int i = lane; i < HD; i += 64) s += src[i] * src[i];
-                s = wave_sum(s);
-                if (lane == 0) {
+                s = wave_sum_lane63(s);
+                if (lane == 63) {
                     const float r = 1.0f / sqrtf(s / (float)HD + p.qk_eps);
                     if (j < G) rq_s[j] = r; else rk_s = r;
                 }
@@ -351,8 +390,7 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
                 float d = 0.f;
 #pragma unroll
                 for (int e = 0; e < EPL; e++) d = fmaf(qf[g][e], kr[j][e], d);
-#pragma unroll
-                for (int off = 8; off > 0; off >>= 1) d += __shfl_xor(d, off, 16);
+                d = row16_sum(d);
                 sc[g][j] = valid ? d : -INFINITY;
             }
         }
@@ -380,24 +418,25 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
         if (c + 1 < nch) load_rows(vr, vc, c + 1);  // V of the next chunk
     }
 
-    // ---- merge the groups: the four of a wavefront by shuffles, the wavefronts through LDS ---
-#pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
+    // ---- merge the groups: the four of a wavefront by lane swaps, the wavefronts through LDS ---
+    auto merge_with = [&](auto partner) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float mo = __shfl_xor(m[g], off, 64), lo = __shfl_xor(l[g], off, 64);
+            const float mo = partner(m[g]), lo = partner(l[g]);
             const float mn = fmaxf(m[g], mo);
             const float a = (m[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);
             const float bo = (mo == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mo - mn);
             l[g] = l[g] * a + lo * bo;
 #pragma unroll
             for (int e = 0; e < EPL; e++) {
-                const float ao = __shfl_xor(acc[g][e], off, 64);
+                const float ao = partner(acc[g][e]);
                 acc[g][e] = acc[g][e] * a + ao * bo;
             }
             m[g] = mn;
         }
-    }
+    };
+    merge_with([&](float v) { return xor16(v, lane); });
+    merge_with([&](float v) { return xor32(v, lane); });
     if (lane < 16) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -463,8 +502,8 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
     if (nsplit == 1) return;  // the attention kernel wrote the output itself
     float m_loc = i < nsplit ? ml.x : -INFINITY;
     for (int s = i + HD; s < nsplit; s += HD) m_loc = fmaxf(m_loc, p.part_ml[(slot0 + s) * 2]);
-    m_loc = wave_max(m_loc);
-    if (lane == 0) red[wave] = m_loc;
+    m_loc = wave_max_lane63(m_loc);
+    if (lane == 63) red[wave] = m_loc;
     __syncthreads();
     float M = red[0];
 #pragma unroll
@@ -480,9 +519,9 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
         w_s[s] = w;
         l_loc = fmaf(p.part_ml[(slot0 + s) * 2 + 1], w, l_loc);
     }
-    l_loc = wave_sum(l_loc);
+    l_loc = wave_sum_lane63(l_loc);
     __syncthreads();
-    if (lane == 0) red[wave] = l_loc;
+    if (lane == 63) red[wave] = l_loc;
     __syncthreads();
     float L = 0.f;
 #pragma unroll
