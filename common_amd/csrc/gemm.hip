@@ -417,8 +417,9 @@ int launch_dma(const GemmParams& p, hipStream_t st) {
 }
 
 // The large-tile kernel pays off with at least kDmaMinTiles tiles (measured on the prefill shapes:
-// +7-13% at 65,536 rows; fewer, larger tiles leave CUs idle on 2,048-row prompts).
-constexpr long long kDmaMinTiles = 1024;
+// +7-13% at 65,536 rows; at 2,048 rows the SwiGLU product's 384 tiles still gain (C4 prefill
+// 11.56 -> 11.14 ms), while 128-tile products leave too many CUs idle).
+constexpr long long kDmaMinTiles = 256;
 
 template <int EPI>
 bool use_dma(const GemmParams& p) {
