@@ -188,6 +188,164 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
     }
 }
 
+// Four fp32 values -> four fp16 (8 bytes, one store).
+__device__ inline uint2 pack4h(float a, float b, float c, float d) {
+    return make_uint2((unsigned)f2h(a) | ((unsigned)f2h(b) << 16), (unsigned)f2h(c) | ((unsigned)f2h(d) << 16));
+}
+
+__device__ inline float2 block_sum2(float2 v, float2* scratch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v.x = wave_sum(v.x);
+    v.y = wave_sum(v.y);
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float2 t = make_float2(0.f, 0.f);
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) {
+        t.x += scratch[w].x;
+        t.y += scratch[w].y;
+    }
+    return t;
+}
+
+// The fold + row RMSNorm above with 16-byte accesses and the row held in registers (one read of x
+// and of each part, one write of x and of the fp16 row): n % 4 == 0, n <= NV * 1024.  Each value
+// is folded in the same order (x, then parts in slice order).
+template <int NV>
+__global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_v4_kernel(float* x, const float* parts, int nparts,
+                                                                        size_t part_stride, const float* w,
+                                                                        uint16_t* out, int n, float eps) {
+    __shared__ float scratch[4];
+    const int n4 = n >> 2;
+    const size_t row = (size_t)blockIdx.x * n;
+    float4* xr = reinterpret_cast<float4*>(x + row);
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n4) {
+            float4 a = xr[i];
+            for (int s = 0; s < nparts; s++) {
+                const float4 q = reinterpret_cast<const float4*>(parts + s * part_stride + row)[i];
+                a.x += q.x; a.y += q.y; a.z += q.z; a.w += q.w;
+            }
+            if (nparts) xr[i] = a;
+            v[j] = a;
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        }
+    }
+    ss = block_sum(ss, scratch);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    uint2* orow = reinterpret_cast<uint2*>(out + row);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n4) {
+            const float4 g = reinterpret_cast<const float4*>(w)[i];
+            orow[i] = pack4h((g.x * v[j].x) * r, (g.y * v[j].y) * r, (g.z * v[j].z) * r, (g.w * v[j].w) * r);
+        }
+    }
+}
+
+// qk_prep_kernel for the whole-vector QK-norm (the reference's) or no QK-norm, with 16-byte accesses
+// and the row's q / k held in registers: thread i takes rotation pairs (f .. f+3, f+hd/2 .. +3) of
+// query pair-group i (and of key pair-group i), so the norm sums, the rotation and the fp16 / cache
+// stores use the values loaded once.  hd % 8 == 0, heads*hd/8 <= QP*256, kv_heads*hd/8 <= 256.
+template <int QP>
+__global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
+    __shared__ float2 scratch[4];
+    const int tid = threadIdx.x;
+    const int r = blockIdx.x, b = r / p.T, t = r - b * p.T, pos = p.p0 + t;
+    const int hd = p.hd, fd = hd / 2, fd4 = fd / 4, q_dim = p.heads * hd, kv_dim = p.kv_heads * hd;
+    const float* q = p.qkv + (size_t)r * p.qkv_stride;
+    const float* k = q + q_dim;
+    const float* v = k + kv_dim;
+    const int nq = p.heads * fd4, nk = p.kv_heads * fd4;
+    float4 q1[QP], q2[QP], k1 = make_float4(0.f, 0.f, 0.f, 0.f), k2 = k1;
+    float2 ss = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < QP; j++) {
+        const int idx = tid + 256 * j;
+        if (idx < nq) {
+            const int h = idx / fd4, f = (idx - h * fd4) * 4;
+            q1[j] = *reinterpret_cast<const float4*>(q + (size_t)h * hd + f);
+            q2[j] = *reinterpret_cast<const float4*>(q + (size_t)h * hd + fd + f);
+            ss.x += q1[j].x * q1[j].x + q1[j].y * q1[j].y + q1[j].z * q1[j].z + q1[j].w * q1[j].w +
+                    q2[j].x * q2[j].x + q2[j].y * q2[j].y + q2[j].z * q2[j].z + q2[j].w * q2[j].w;
+        }
+    }
+    if (tid < nk) {
+        const int g = tid / fd4, f = (tid - g * fd4) * 4;
+        k1 = *reinterpret_cast<const float4*>(k + (size_t)g * hd + f);
+        k2 = *reinterpret_cast<const float4*>(k + (size_t)g * hd + fd + f);
+        ss.y = k1.x * k1.x + k1.y * k1.y + k1.z * k1.z + k1.w * k1.w + k2.x * k2.x + k2.y * k2.y + k2.z * k2.z +
+               k2.w * k2.w;
+    }
+    float rq = 1.f, rk = 1.f;
+    if (p.q_norm || p.k_norm) {
+        ss = block_sum2(ss, scratch);
+        rq = 1.0f / sqrtf(ss.x / (float)q_dim + p.eps);
+        rk = 1.0f / sqrtf(ss.y / (float)kv_dim + p.eps);
+    }
+    const float4* rope = reinterpret_cast<const float4*>(p.rope_tab + (size_t)pos * fd);  // (c, s) pairs
+    // normalise (g * x) * r and rotate four pairs: out1 = x1 c - x2 s, out2 = x2 c + x1 s
+    auto rotate = [&](float4 a, float4 c, const float* gain, size_t goff, float rn, int f, float* o1, float* o2) {
+        if (gain) {
+            const float4 g1 = *reinterpret_cast<const float4*>(gain + goff + f);
+            const float4 g2 = *reinterpret_cast<const float4*>(gain + goff + fd + f);
+            a.x = (g1.x * a.x) * rn; a.y = (g1.y * a.y) * rn; a.z = (g1.z * a.z) * rn; a.w = (g1.w * a.w) * rn;
+            c.x = (g2.x * c.x) * rn; c.y = (g2.y * c.y) * rn; c.z = (g2.z * c.z) * rn; c.w = (g2.w * c.w) * rn;
+        }
+        const float4 t0 = rope[f / 2], t1 = rope[f / 2 + 1];  // (c_f, s_f, c_f+1, s_f+1), (c_f+2, ...)
+        const float x1[4] = {a.x, a.y, a.z, a.w}, x2[4] = {c.x, c.y, c.z, c.w};
+        const float cs[4] = {t0.x, t0.z, t1.x, t1.z}, sn[4] = {t0.y, t0.w, t1.y, t1.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            o1[e] = x1[e] * cs[e] - x2[e] * sn[e];
+            o2[e] = x2[e] * cs[e] + x1[e] * sn[e];
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < QP; j++) {
+        const int idx = tid + 256 * j;
+        if (idx < nq) {
+            const int h = idx / fd4, f = (idx - h * fd4) * 4;
+            float o1[4], o2[4];
+            rotate(q1[j], q2[j], p.q_norm, (size_t)h * hd, rq, f, o1, o2);
+            uint16_t* qo = p.qb + (size_t)r * q_dim + (size_t)h * hd;
+            *reinterpret_cast<uint2*>(qo + f) = pack4h(o1[0], o1[1], o1[2], o1[3]);
+            *reinterpret_cast<uint2*>(qo + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3]);
+        }
+    }
+    if (tid < nk) {
+        const int g = tid / fd4, f = (tid - g * fd4) * 4;
+        float o1[4], o2[4];
+        rotate(k1, k2, p.k_norm, (size_t)g * hd, rk, f, o1, o2);
+        const size_t kofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd;
+        if (p.kv16) {
+            uint16_t* kc = reinterpret_cast<uint16_t*>(p.kcache) + kofs;
+            *reinterpret_cast<uint2*>(kc + f) = pack4h(o1[0], o1[1], o1[2], o1[3]);
+            *reinterpret_cast<uint2*>(kc + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3]);
+        } else {
+            float* kc = reinterpret_cast<float*>(p.kcache) + kofs;
+            *reinterpret_cast<float4*>(kc + f) = make_float4(o1[0], o1[1], o1[2], o1[3]);
+            *reinterpret_cast<float4*>(kc + fd + f) = make_float4(o2[0], o2[1], o2[2], o2[3]);
+        }
+        uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
+        *reinterpret_cast<uint2*>(k16 + f) = pack4h(o1[0], o1[1], o1[2], o1[3]);
+        *reinterpret_cast<uint2*>(k16 + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3]);
+    }
+    for (int i4 = tid; i4 < kv_dim / 4; i4 += 256) {
+        const int g = (4 * i4) / hd, i = 4 * i4 - g * hd;
+        const float4 vv = reinterpret_cast<const float4*>(v)[i4];
+        const size_t vofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i;
+        if (p.kv16)
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.vcache) + vofs) = pack4h(vv.x, vv.y, vv.z, vv.w);
+        else
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.vcache) + vofs) = vv;
+    }
+}
+
 // fp16 Vᵀ tiles of the prompt rows from the fp32 V cache: block (tile of 64 rows, KV head, sequence)
 // reads 64 contiguous cache rows and writes 64 contiguous keys per hd row through LDS (rows past
 // the prompt are written as 0).
@@ -448,8 +606,21 @@ int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const
                                  int n, float eps, hipStream_t stream) {
     AR_CHECK_ARG(x && w && out && rows > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0),
                  "fold rmsnorm rows: bad arguments");
-    hipLaunchKernelGGL(fold_rmsnorm_rows_f16_kernel, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
-                       (size_t)rows * n, w, out, n, eps);
+    const bool v4 = n % 4 == 0 && n <= 4096 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0 &&
+                    (nparts == 0 || (reinterpret_cast<uintptr_t>(parts) & 15) == 0);
+    if (v4 && n <= 1024)
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f16_v4_kernel<1>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
+    else if (v4 && n <= 2048)
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f16_v4_kernel<2>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
+    else if (v4)
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f16_v4_kernel<4>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
+    else
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f16_kernel, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
@@ -475,7 +646,22 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     p.kv16 = a.kv16;
     p.T = a.T; p.p0 = a.p0; p.heads = a.heads; p.kv_heads = a.kv_heads; p.hd = a.hd; p.qb = a.qb;
     p.k16 = a.k16; p.Tp = a.Tp;
-    hipLaunchKernelGGL(qk_prep_kernel, dim3(a.B * a.T), dim3(256), 0, stream, p);
+    const int nq = a.heads * a.hd / 8, nk = a.kv_heads * a.hd / 8;
+    const bool v4 = !a.per_head && a.hd % 8 == 0 && a.qkv_stride % 4 == 0 && nk <= 256 && nq <= 4 * 256 &&
+                    (reinterpret_cast<uintptr_t>(a.qkv) & 15) == 0 &&
+                    (!a.q_norm || (reinterpret_cast<uintptr_t>(a.q_norm) & 15) == 0) &&
+                    (!a.k_norm || (reinterpret_cast<uintptr_t>(a.k_norm) & 15) == 0) &&
+                    (reinterpret_cast<uintptr_t>(a.rope_tab) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.qb) & 7) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.k16) & 7) == 0 && (reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.vcache) & 15) == 0;
+    if (v4 && nq <= 256)
+        hipLaunchKernelGGL(qk_prep_v4_kernel<1>, dim3(a.B * a.T), dim3(256), 0, stream, p);
+    else if (v4 && nq <= 512)
+        hipLaunchKernelGGL(qk_prep_v4_kernel<2>, dim3(a.B * a.T), dim3(256), 0, stream, p);
+    else if (v4)
+        hipLaunchKernelGGL(qk_prep_v4_kernel<4>, dim3(a.B * a.T), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(qk_prep_kernel, dim3(a.B * a.T), dim3(256), 0, stream, p);
     AR_LAUNCH_CHECK();
     AR_CHECK_ARG(a.Tp % 64 == 0 && a.Tp >= a.T, "qk prep: Vᵀ rows %d not a multiple of 64 covering %d", a.Tp, a.T);
     const dim3 vgrid((a.T + 63) / 64, a.kv_heads, a.B);
