@@ -130,6 +130,35 @@ def test_llama2_bf16_weights(ctx, tmp_path):
     assert rel_err(logits, np.asarray(ref_logits)) <= 2e-2
 
 
+def test_llama2_bf16_prefill_matches_token_by_token(ctx, tmp_path):
+    """A bf16 Llama2 model's batched prefill (MFMA GEMMs + causal flash attention with the checkpoint's
+    RoPE table, head size 64) leaves the model where feeding the prompt one token per step does:
+    the next step's logits agree within the bf16 bar and the greedy continuations match."""
+    cfg = CFG_SHARED
+    w = make_weights(cfg, seed=6)
+    write_checkpoint(tmp_path / "model.bin", cfg, w)
+    prompt = [BOS] + [int(x) for x in np.random.default_rng(9).integers(3, cfg.vocab_size, 30)]
+    with Llama2(tmp_path / "model.bin", None, ctx, weight_dtype=C.DTYPE_BF16) as m:
+        am = m.model
+        am.reset()
+        am.set_prompt(prompt)
+        last = am.prefill(return_logits=True)[0]
+        assert am.get_current_step() == len(prompt)
+        cont_pf = [int(am.next()[0]) for _ in range(6)]
+        am.reset()
+        am.set_prompt(prompt)
+        for _ in range(len(prompt)):
+            _, lg = am.next(return_logits=True)
+        ref_last = lg[0]
+        cont_tt = [int(am.next()[0]) for _ in range(6)]
+    assert rel_err(last, ref_last) <= 2e-2
+    # the token chosen from those logits, fed at the first step after the prompt (unless the two paths'
+    # fp16 / fp32 activations could swap a near-tie)
+    top2 = np.sort(ref_last)[-2:]
+    if (top2[1] - top2[0]) > 2e-2 * np.abs(ref_last).max():
+        assert cont_pf[0] == cont_tt[0]
+
+
 def _vocab(V, rng):
     """A llama2.c-style vocabulary: specials, single characters, then merged strings with scores."""
     chars = list("abcdefghij klmno.")

@@ -130,6 +130,9 @@ def test_bpe_hand_worked():
     assert t.encode("日本") == [11]
     assert t.encode("") == []
     assert t.encode("ba") == [1, 0]
+    # the plain-Python restatement on the same hand-worked cases
+    for text, want in (("abc", [6]), ("cab", [2, 4]), (" ab", [7, 1]), ("日本", [11]), ("", []), ("ba", [1, 0])):
+        assert O.llama2_bpe_encode(text, VOCAB, np.float32(SCORES)) == want, text
     with pytest.raises(hw.HardwareException, match="no token"):
         t.encode("x")
     with pytest.raises(hw.HardwareException, match="no token"):
