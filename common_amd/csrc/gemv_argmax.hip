@@ -165,6 +165,7 @@ int launch_nb(const Params& p, int nch, hipStream_t st) {
     switch (nch) {
         case 1: return launch_nch<WT, NB, 1>(p, st);
         case 2: return launch_nch<WT, NB, 2>(p, st);
+        case 3: return launch_nch<WT, NB, 3>(p, st);
         case 4: return launch_nch<WT, NB, 4>(p, st);
     }
     ar_set_error("argmax GEMV: %d column chunks not supported", nch);
@@ -176,7 +177,7 @@ int launch_nb(const Params& p, int nch, hipStream_t st) {
 bool gemv_argmax_fits(int cols, int batch, int wdtype) {
     const int ch = 64 * (wdtype == AR_DTYPE_BF16 ? 8 : 4);
     const int nch = cols / ch;
-    return batch >= 1 && batch <= 2 && cols % ch == 0 && (nch == 1 || nch == 2 || nch == 4);
+    return batch >= 1 && batch <= 2 && cols % ch == 0 && nch >= 1 && nch <= 4;
 }
 
 int gemv_launch_argmax(const gemv::Params& p, int wdtype, hipStream_t st) {
