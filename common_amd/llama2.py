@@ -66,8 +66,8 @@ class Llama2Config:
 
 
 class Llama2Checkpoint:
-    """A mapped llama2.c checkpoint; ``tensor(name)`` returns a Llama2Weights field as a numpy view
-    (copied for ``freqCis``, which is staged interleaved)."""
+    """A mapped llama2.c checkpoint; ``tensor(name)`` returns a copy of a Llama2Weights field
+    (``freqCis`` with its two planes interleaved, as Llama2Weights stages it)."""
 
     def __init__(self, path):
         h = ctypes.c_void_p()
@@ -165,15 +165,19 @@ class Llama2:
 
     def __init__(self, checkpoint, tokenizer="tokenizer.bin", ctx: hw.HipContext | None = None, max_batch: int = 1,
                  weight_dtype: int = DTYPE_F32, kv_dtype: int = DTYPE_F32):
-        self.ctx = ctx or hw.HipContext(0)
-        self._own_ctx = ctx is None
         self.handle = None
         with Llama2Checkpoint(checkpoint) as ck:
             self.config = dataclasses.replace(ck.config, max_batch=max_batch)
             self.tokenizer = BPE(tokenizer, self.config.vocab_size) if tokenizer is not None else None
+            self.ctx = ctx or hw.HipContext(0)
+            self._own_ctx = ctx is None
             h = ctypes.c_void_p()
-            hw.check(hw.lib().ar_hip_llama2_create_model(self.ctx.handle, ck.handle, max_batch, weight_dtype,
-                                                         kv_dtype, ctypes.byref(h)))
+            try:
+                hw.check(hw.lib().ar_hip_llama2_create_model(self.ctx.handle, ck.handle, max_batch, weight_dtype,
+                                                             kv_dtype, ctypes.byref(h)))
+            except Exception:
+                self.close()
+                raise
             self.handle = h.value
         self.model = AutoregressiveModel(self)
 
