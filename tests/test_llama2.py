@@ -189,6 +189,17 @@ def test_bpe_file(tmp_path):
     assert BPE(tmp_path / "tokenizer.bin", 5).vocab_size() == 5
     with pytest.raises(hw.HardwareException, match="ends at entry"):
         BPE(tmp_path / "tokenizer.bin", len(vocab) + 1)
+    # a negative entry length is rejected; a zero-entry vocabulary has no token for any character
+    with open(tmp_path / "neg.bin", "wb") as f:
+        f.write(struct.pack("<i", 4) + struct.pack("<fi", 0.0, -1))
+    with pytest.raises(hw.HardwareException, match="length"):
+        BPE(tmp_path / "neg.bin", 1)
+    empty = BPE(tmp_path / "tokenizer.bin", 0)
+    assert empty.vocab_size() == 0 and empty.encode("") == [] and empty.lookup("a") == -1
+    with pytest.raises(hw.HardwareException, match="no token"):
+        empty.encode("a")
+    with pytest.raises(hw.HardwareException):
+        BPE(tmp_path / "missing.bin", 3)
     # entry bytes that are not UTF-8 decode to U+FFFD, as new String(bytes) does
     with open(tmp_path / "bad.bin", "wb") as f:
         f.write(struct.pack("<i", 4) + struct.pack("<fi", 0.0, 3) + b"a\xffb")
