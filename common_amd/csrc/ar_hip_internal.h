@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
@@ -67,6 +68,15 @@ struct ar_hip_ctx {
 // Device allocation owned by the context's memory provider.
 int ar_ctx_alloc(ar_hip_ctx* ctx, size_t bytes, void** out);
 int ar_ctx_free(ar_hip_ctx* ctx, void* p);
+
+// Per-device caches of launch facts (CU count, resident-grid size, function attributes set):
+// indexed by the device of the stream a launch goes to.
+constexpr int kMaxDevices = 64;
+// Device of `stream` (the device its launches run on) as a cache index, or -1 (unknown device, or an
+// index past the cache).
+int ar_device_slot(hipStream_t stream);
+// Compute units of the device of `stream` (cached per device; 256 if it cannot be read).
+int ar_device_cus(hipStream_t stream);
 
 // ---- kernel launchers (device pointers, enqueue on `stream`) ----------------------
 struct GemvLaunch {

@@ -20,6 +20,8 @@
 // output tiles in an XCD-grouped order (tile_of).
 // Epilogues: fp32 store (+bias), fp32 residual add, and SwiGLU of two weight matrices written as
 // bf16 (the next GEMM's A operand).
+#include <atomic>
+
 #include "ar_hip_internal.h"
 
 namespace {
@@ -405,11 +407,13 @@ template <bool F16, int EPI>
 int launch_dma(const GemmParams& p, hipStream_t st) {
     constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
     const int mt = (p.M + dma::BM - 1) / dma::BM, nt = p.N / (dma::BNW / NW);
-    static bool attr_set = false;  // 128 KB of dynamic LDS needs the per-kernel opt-in
-    if (!attr_set) {
+    // 128 KB of dynamic LDS needs the per-kernel opt-in, once per device
+    static std::atomic<bool> attr_set[kMaxDevices];
+    const int slot = ar_device_slot(st);
+    if (slot < 0 || !attr_set[slot].load(std::memory_order_relaxed)) {
         AR_HIP_TRY(hipFuncSetAttribute((const void*)gemm_dma_kernel<F16, EPI>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, dma::LDS_BYTES));
-        attr_set = true;
+        if (slot >= 0) attr_set[slot].store(true, std::memory_order_relaxed);
     }
     hipLaunchKernelGGL((gemm_dma_kernel<F16, EPI>), dim3(mt * nt), dim3(dma::NTHR), dma::LDS_BYTES, st, p, mt, nt);
     AR_LAUNCH_CHECK();

@@ -144,15 +144,17 @@ template <typename WT, int NB, int NCH>
 int launch_nch(const Params& p, hipStream_t st) {
     constexpr int RPW = 1;  // one row per wavefront per step measured fastest (C3 logits: 100.9 us vs 101.7-104.3 for 2, 108-110 for 4-8)
     // as many blocks as are resident at once, so every block is running from the start
-    static int grid = 0;
+    // (cached per device: the resident count depends on the device the stream launches to)
+    static std::atomic<int> grid_cache[kMaxDevices];
+    const int slot = ar_device_slot(st);
+    int grid = slot >= 0 ? grid_cache[slot].load(std::memory_order_relaxed) : 0;
     if (!grid) {
-        int dev = 0, cus = 0, per_cu = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            cus = 256;
+        int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_argmax_kernel<WT, NB, RPW, NCH>, kAmThreads, 0) !=
                 hipSuccess || per_cu < 1)
             per_cu = 2;
-        grid = per_cu * cus;
+        grid = per_cu * ar_device_cus(st);
+        if (slot >= 0) grid_cache[slot].store(grid, std::memory_order_relaxed);
     }
     const int g = std::min(grid, (p.rows + kAmWaves * RPW - 1) / (kAmWaves * RPW));
     hipLaunchKernelGGL((gemv_argmax_kernel<WT, NB, RPW, NCH>), dim3(g), dim3(kAmThreads), 0, st, p);

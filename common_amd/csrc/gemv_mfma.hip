@@ -379,31 +379,20 @@ __global__ __launch_bounds__(NWS * 64, NWS == 8 ? 4 : 1) void gemv_mfma_stream_k
     F::emit(p, v, row0, tid, tot);
 }
 
-int persist_blocks() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-            cus = n;
-        else
-            cus = 256;
-    }
-    return cus;
-}
 
 template <int EPI>
 int launch_epi(const gemv::Params& p, hipStream_t st) {
     constexpr int NMAT = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
     const int nsteps = p.cols / 32, tiles = (p.rows + 15) / 16;
     const int kpw_p = (nsteps + kPersistWaves - 1) / kPersistWaves;
+    const int persist = ar_device_cus(st);  // one persistent block per CU of the stream's device
     // register budget of the persistent form: planes 8*KS + weights 4*NMAT*KS
     const int ks_max = NMAT == 2 ? 12 : 16;
     // fewer tiles than CUs (the 2560-row projections at C5): one tile per 16-wavefront block spreads
     // the loads over more wavefronts (measured: O 4096 -> 2560 15.5 us streaming vs 23.7 persistent;
     // QKV 2560 -> 6144 20.3 us persistent vs 25.6 streaming)
-    if (kpw_p <= ks_max && tiles >= persist_blocks()) {
-        const dim3 grid(std::min(tiles, persist_blocks())), block(64 * kPersistWaves);
+    if (kpw_p <= ks_max && tiles >= persist) {
+        const dim3 grid(std::min(tiles, persist)), block(64 * kPersistWaves);
         if (kpw_p <= 4)
             hipLaunchKernelGGL((gemv_mfma_persist_kernel<EPI, 4>), grid, block, 0, st, p, kpw_p, tiles);
         else if (kpw_p <= 8)
@@ -418,8 +407,8 @@ int launch_epi(const gemv::Params& p, hipStream_t st) {
         // ks = 2*CUs / tiles blocks of 8 wavefronts (two per CU), partials folded in order
         int ks = 1;
         if (p.kpart && p.kcount && tiles <= p.kcount_n && !p.norm_w && EPI != GEMV_EPI_ARGMAX &&
-            tiles < persist_blocks()) {
-            ks = std::min(kMaxKSplit, std::max(1, 2 * persist_blocks() / tiles));
+            tiles < persist) {
+            ks = std::min(kMaxKSplit, std::max(1, 2 * persist / tiles));
             while (ks > 1 && ((long long)tiles * ks * NMAT * 256 > p.kpart_floats || nsteps < ks * 8)) ks--;
         }
         if (ks > 1) {

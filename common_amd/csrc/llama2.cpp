@@ -18,6 +18,7 @@
 #include <cerrno>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -124,27 +125,43 @@ extern "C" int ar_hip_llama2_open(const char* path, ar_llama2_ckpt** out) {
     }
     const int64_t d = c.dim, F = c.hidden_dim, L = c.layer_count, V = c.vocab_size, S = c.seq_len,
                   half = c.head_size / 2;
+    // Offsets are sums of products of header fields: every product and sum is checked, so a header
+    // whose sizes overflow 64 bits (or describe more floats than the file could hold) is rejected
+    // instead of wrapping into a small total that passes the length check below.
     int64_t o = 0;
+    bool overflow = false;
+    auto prod = [&](std::initializer_list<int64_t> fs) {
+        int64_t r = 1;
+        for (int64_t f : fs)
+            if (__builtin_mul_overflow(r, f, &r)) overflow = true;
+        return r;
+    };
     auto take = [&](int64_t n) {
         const int64_t at = o;
-        o += n;
+        if (__builtin_add_overflow(o, n, &o)) overflow = true;
         return at;
     };
-    ck->off_embed = take(V * d);
-    ck->off_rms_att = take(L * d);
-    ck->off_wq = take(L * d * d);
-    ck->off_wk = take(L * d * d);
-    ck->off_wv = take(L * d * d);
-    ck->off_wo = take(L * d * d);
-    ck->off_rms_ffn = take(L * d);
-    ck->off_w1 = take(L * F * d);
-    ck->off_w2 = take(L * d * F);
-    ck->off_w3 = take(L * F * d);
+    ck->off_embed = take(prod({V, d}));
+    ck->off_rms_att = take(prod({L, d}));
+    ck->off_wq = take(prod({L, d, d}));
+    ck->off_wk = take(prod({L, d, d}));
+    ck->off_wv = take(prod({L, d, d}));
+    ck->off_wo = take(prod({L, d, d}));
+    ck->off_rms_ffn = take(prod({L, d}));
+    ck->off_w1 = take(prod({L, F, d}));
+    ck->off_w2 = take(prod({L, d, F}));
+    ck->off_w3 = take(prod({L, F, d}));
     ck->off_rms_final = take(d);
-    ck->off_freq_re = take(S * half);
-    ck->off_freq_im = take(S * half);
-    ck->off_wcls = c.shared_weights ? ck->off_embed : take(V * d);
+    ck->off_freq_re = take(prod({S, half}));
+    ck->off_freq_im = take(prod({S, half}));
+    ck->off_wcls = c.shared_weights ? ck->off_embed : take(prod({V, d}));
     ck->end = o;
+    if (overflow || o > (int64_t)((bytes - AR_LLAMA2_HEADER_BYTES) / sizeof(float))) {
+        ar_set_error("checkpoint '%s' is %zu bytes; its header describes %s", path, bytes,
+                     overflow ? "more than 2^63 floats" : "more floats than the file holds");
+        ar_hip_llama2_close(ck);
+        return AR_HIP_ERR_INVALID;
+    }
     const size_t need = AR_LLAMA2_HEADER_BYTES + (size_t)o * sizeof(float);
     if (bytes < need) {
         ar_set_error("checkpoint '%s' is %zu bytes; its header describes %zu", path, bytes, need);

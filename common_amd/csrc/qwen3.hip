@@ -630,10 +630,13 @@ extern "C" int ar_hip_qwen3_set_prompt(ar_qwen3* m, int seq, const int32_t* ids,
     AR_CHECK_ARG(n >= 0 && n <= m->S, "prompt of %d tokens exceeds the %d-position cache", n, m->S);
     for (int i = 0; i < n; i++)
         AR_CHECK_ARG(ids[i] >= 0 && ids[i] < m->cfg.vocab_size, "prompt token %d at %d outside vocab", ids[i], i);
-    for (int b = 0; b < m->B; b++)
-        if (b != seq && m->prompt_set[b])
-            AR_CHECK_ARG(n == m->prompt_len, "all sequences of a batch share one prompt length (%d != %d)", n,
-                         m->prompt_len);
+    // All sequences of a batch share one prompt length.  A prompt of another length replaces the
+    // batch's length: the other sequences' prompts are dropped and must be set again (at the new
+    // length) before the next step, which check_ready enforces.  setPrompt itself accepts any
+    // length at any time (AutoregressiveModel.java:272-275).
+    if (n != m->prompt_len)
+        for (int b = 0; b < m->B; b++)
+            if (b != seq) m->prompt_set[b] = 0;
     if (n > 0)
         AR_HIP_TRY(hipMemcpyAsync(m->tokens + (size_t)seq * (m->S + 1), ids, (size_t)n * 4, hipMemcpyHostToDevice,
                                   m->ctx->stream));

@@ -5,6 +5,7 @@
 //  ComputeContext.java:89,133, MemoryProvider.java:60-188) for one GPU.
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 
 #include "ar_hip_internal.h"
@@ -95,6 +96,24 @@ extern "C" int ar_hip_device_info(ar_hip_ctx* ctx, int* num_cus, size_t* hbm_byt
         snprintf(name, (size_t)name_len, "%s", prop.gcnArchName);
     }
     return AR_HIP_OK;
+}
+
+int ar_device_slot(hipStream_t stream) {
+    int dev = -1;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return -1;
+    return dev >= 0 && dev < kMaxDevices ? dev : -1;
+}
+
+int ar_device_cus(hipStream_t stream) {
+    static std::atomic<int> cache[kMaxDevices];
+    int dev = -1;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return 256;
+    const int slot = dev >= 0 && dev < kMaxDevices ? dev : -1;
+    int n = slot >= 0 ? cache[slot].load(std::memory_order_relaxed) : 0;
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (slot >= 0) cache[slot].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 int ar_ctx_alloc(ar_hip_ctx* ctx, size_t bytes, void** out) {

@@ -69,9 +69,11 @@ struct Tensor {
     Values<float> f32;
     bool has_f64() const { return f64.count() > 0; }
     int64_t count() const { return has_f64() ? f64.count() : f32.count(); }
+    // Element count of the shape, or -1 when the product overflows 64 bits (never equal to a count).
     int64_t shape_size() const {
         int64_t n = 1;
-        for (int32_t d : dims) n *= d;
+        for (int32_t d : dims)
+            if (__builtin_mul_overflow(n, (int64_t)d, &n)) return -1;
         return n;
     }
 };

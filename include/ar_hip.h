@@ -187,8 +187,11 @@ int ar_hip_qwen3_finalize(ar_qwen3 *m);
 
 /* AutoregressiveModel.reset (AutoregressiveModel.java:203-207): position 0. */
 int ar_hip_qwen3_reset(ar_qwen3 *m);
-/* AutoregressiveModel.setPrompt: prompt ids for sequence `seq` (all sequences of a batch
- * share one prompt length). */
+/* AutoregressiveModel.setPrompt (AutoregressiveModel.java:272-275): prompt ids for sequence `seq`.
+ * All sequences of a batch share one prompt length: a prompt whose length differs from the
+ * batch's current one becomes the new length and drops the other sequences' prompts, which must
+ * then be set again (at that length) before the next step.  reset() keeps the prompts, as the
+ * reference's reset keeps its prompt. */
 int ar_hip_qwen3_set_prompt(ar_qwen3 *m, int seq, const int32_t *ids, int n);
 /* AutoregressiveModel.next (AutoregressiveModel.java:295-308) for every sequence: feeds the
  * prompt token or the greedy choice from the previous step's logits, runs one forward pass

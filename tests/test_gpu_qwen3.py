@@ -185,6 +185,34 @@ def test_c1_batch_sequences_are_independent(ctx, c1):
         assert rel_err(logits[b], rl) <= LOGIT_TOL_F32
 
 
+def test_batch_reprompt_with_another_length(ctx, c1):
+    """A batch-8 model re-prompted after reset() with a different prompt length: the first new
+    prompt drops the others (stepping before all eight are set again is a state error), and the
+    new streams equal the oracle's for the new prompts."""
+    cfg, sd, prompt = c1
+    cfg8 = dataclasses.replace(cfg, max_batch=8)
+    first = synthetic.prompt_ids(6, cfg.vocab_size, seed=21, batch=8)
+    second = synthetic.prompt_ids(9, cfg.vocab_size, seed=22, batch=8)
+    with Qwen3(cfg8, sd, ctx) as m:
+        am = m.model
+        am.reset()
+        for b in range(8):
+            am.set_prompt(first[b], seq=b)
+        am.run(8)
+        am.reset()
+        am.set_prompt(second[0], seq=0)
+        with pytest.raises(hw.HardwareException) as e:
+            am.next()
+        assert e.value.code == hw.AR_HIP_ERR_STATE
+        for b in range(1, 8):
+            am.set_prompt(second[b], seq=b)
+        fed = am.run(second.shape[1] + 4)
+    for b in (0, 5):
+        ref = oracle.OracleQwen3(cfg, sd, precision="fp64")
+        rf, rl = ref.generate(second[b], 4)
+        assert compare_tokens(fed[b], rf, rl, second.shape[1]) == len(rf)
+
+
 def test_c1_per_head_qk_norm_and_bias(ctx):
     cfg = dataclasses.replace(C.C1_TINY, qk_norm_mode=C.QK_NORM_PER_HEAD, qkv_bias=True)
     sd = synthetic.state_dict(cfg, seed=3)

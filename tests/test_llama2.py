@@ -109,6 +109,26 @@ def test_checkpoint_size_rules(tmp_path):
         Llama2Checkpoint(tmp_path / "bad.bin")
 
 
+def test_checkpoint_header_overflow_is_rejected(tmp_path):
+    """Header fields whose tensor sizes overflow 64 bits, or describe far more floats than the file
+    holds, are rejected before any tensor offset is used (no wrapped total can pass the length
+    check)."""
+    big = 2 ** 31 - 1
+    cases = {
+        # L * F * d = (2^31-1)^3 overflows int64
+        "mul.bin": header(big - 1, big, big, 1, 1, 5, 2),
+        # every product fits, the sum of the tensors is ~2^62.5 floats: far past the file
+        "sum.bin": header(2 ** 30, 2 ** 30, 2 ** 2, 2 ** 10, 2 ** 10, 2 ** 30, 2),
+        # a negative vocabulary (separate wcls) with a sum past the file
+        "wcls.bin": header(1 << 20, 4, 1, 1 << 10, 1 << 10, -(2 ** 31 - 1), 2),
+    }
+    for name, h in cases.items():
+        (tmp_path / name).write_bytes(h + b"\0" * 4096)
+        with pytest.raises(hw.HardwareException, match="describes") as e:
+            Llama2Checkpoint(tmp_path / name)
+        assert e.value.code == hw.AR_HIP_ERR_INVALID, name
+
+
 # ---- BPE ---------------------------------------------------------------------------------------
 
 VOCAB = ["a", "b", "c", " ", "ab", "bc", "abc", " a", "é", "ab", "日", "日本", "本"]

@@ -233,6 +233,23 @@ def test_errors():
         assert L.ar_hip_state_dict_put(sd.handle, b"k", dims, 2, 0, buf.ctypes.data, F32, 5) == hw.AR_HIP_ERR_INVALID
         assert b"shape" in L.ar_hip_last_error()
         assert L.ar_hip_state_dict_save(sd.handle, b"/tmp/x", 7) == hw.AR_HIP_ERR_INVALID
+        # a shape whose element count overflows 64 bits matches no value count
+        big = (ctypes.c_int32 * 3)(2 ** 31 - 1, 2 ** 31 - 1, 2 ** 31 - 1)
+        assert L.ar_hip_state_dict_put(sd.handle, b"k", big, 3, 0, buf.ctypes.data, F32, 5) == hw.AR_HIP_ERR_INVALID
+
+
+def test_overflowing_shape_in_a_file_is_a_parse_error(tmp_path, capfd):
+    """An entry whose dims multiply past 64 bits is a parse error (the file's later entries are
+    skipped with a warning, as for any undecodable entry), not a wrapped size that matches."""
+    S = _schema()
+    lib = _library(S, {"ok": np.ones(2, np.float32)})
+    e = lib.collections.add()
+    e.key = "huge"
+    e.collection.traversal_policy.dims.extend([2 ** 31 - 1] * 3)
+    e.collection.data_32.extend([1.0] * 5)
+    (tmp_path / "f").write_bytes(lib.SerializeToString())
+    with StateDictionary(tmp_path / "f") as sd:
+        assert sd.keySet() == ["ok"]
 
 
 def test_qwen3_layout_round_trip_and_config_inference(tmp_path):
