@@ -63,7 +63,14 @@ struct ar_hip_ctx {
     std::unordered_map<void*, size_t> device_allocs;  // memory-provider bookkeeping
     std::unordered_map<void*, size_t> host_allocs;
     size_t device_bytes = 0;
+    // device address of this device's copy of the allocation-free attention entry point's scratch
+    // array (ops.hip), looked up once by ar_hip_init
+    float* noalloc_scratch = nullptr;
 };
+
+// Looks up the device addresses the operator entry points need on ctx's device (called by
+// ar_hip_init with that device current).
+int ar_ops_init(ar_hip_ctx* ctx);
 
 // Device allocation owned by the context's memory provider.
 int ar_ctx_alloc(ar_hip_ctx* ctx, size_t bytes, void** out);

@@ -60,26 +60,90 @@ int grow(ar_hip_ctx* ctx, void** p, size_t* have, size_t need, size_t elem) {
 }
 }  // namespace
 
-extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const float* k, const float* v,
-                                       const float* q_norm, const float* k_norm, float qk_eps, int qk_norm_mode,
-                                       float* k_cache, float* v_cache, int max_seq, int pos, int heads, int kv_heads,
-                                       int head_dim, double rope_theta, float* out) {
+namespace {
+int attention_args(ar_hip_ctx* ctx, const float* q, const float* k, const float* v, const float* q_norm,
+                   const float* k_norm, float qk_eps, int qk_norm_mode, float* k_cache, float* v_cache, int max_seq,
+                   int pos, int heads, int kv_heads, int head_dim, double rope_theta, float* out, AttnLaunch* a) {
     AR_CHECK_ARG(ctx && q && k && v && k_cache && v_cache && out, "attention: null pointer");
     AR_CHECK_ARG(pos >= 0 && pos < max_seq, "attention: position %d outside cache of %d rows", pos, max_seq);
     AR_CHECK_ARG(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "attention: bad head counts");
     AR_CHECK_ARG(qk_norm_mode == AR_QK_NORM_WHOLE || qk_norm_mode == AR_QK_NORM_PER_HEAD, "attention: bad qk-norm mode");
+    a->q = q; a->k = k; a->v = v; a->qkv_stride = 0; a->q_norm = q_norm; a->k_norm = k_norm; a->qk_eps = qk_eps;
+    a->per_head_norm = qk_norm_mode == AR_QK_NORM_PER_HEAD; a->kcache = k_cache; a->vcache = v_cache;
+    a->max_seq = max_seq; a->pos = nullptr; a->pos_value = pos; a->heads = heads; a->kv_heads = kv_heads;
+    a->head_dim = head_dim; a->rope_theta = rope_theta; a->max_splits = attention_max_splits(max_seq, kv_heads, 1, false);
+    a->out = out; a->out_stride = heads * head_dim; a->batch = 1;
+    return AR_HIP_OK;
+}
+}  // namespace
+
+extern "C" int ar_hip_attention_decode(ar_hip_ctx* ctx, const float* q, const float* k, const float* v,
+                                       const float* q_norm, const float* k_norm, float qk_eps, int qk_norm_mode,
+                                       float* k_cache, float* v_cache, int max_seq, int pos, int heads, int kv_heads,
+                                       int head_dim, double rope_theta, float* out) {
+    AttnLaunch a;
+    AR_TRY(attention_args(ctx, q, k, v, q_norm, k_norm, qk_eps, qk_norm_mode, k_cache, v_cache, max_seq, pos, heads,
+                          kv_heads, head_dim, rope_theta, out, &a));
     std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnScratch& s = g_attn[ctx];
-    const int max_splits = attention_max_splits(max_seq, kv_heads, 1, false);
-    AR_TRY(grow(ctx, (void**)&s.part_o, &s.part_floats, attention_partial_floats(1, heads, max_splits, head_dim),
+    AR_TRY(grow(ctx, (void**)&s.part_o, &s.part_floats, attention_partial_floats(1, heads, a.max_splits, head_dim),
                 sizeof(float)));
-    AR_TRY(grow(ctx, (void**)&s.part_ml, &s.ml_floats, (size_t)heads * max_splits * 2, sizeof(float)));
+    AR_TRY(grow(ctx, (void**)&s.part_ml, &s.ml_floats, (size_t)heads * a.max_splits * 2, sizeof(float)));
+    a.part_o = s.part_o;
+    a.part_ml = s.part_ml;
+    return launch_attention_decode(a, ctx->stream);
+}
+
+// ---- allocation-free attention -----------------------------------------------------------
+// The split partials of ar_hip_attention_decode_noalloc live in this fixed array: each GPU the
+// library runs on holds one copy (1 MiB) until the process ends.  Host code never passes the
+// array's name to a kernel: ar_ops_init looks up this device's address of it once per context,
+// with the context's device current, and launches use that address.
+constexpr size_t kNoAllocScratchFloats = (size_t)1 << 18;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+std::atomic<float*> g_scratch_addr[kMaxDevices];  // per device: its copy's address, once looked up
+}
+
+int ar_ops_init(ar_hip_ctx* ctx) {
+    const bool cached = ctx->device >= 0 && ctx->device < kMaxDevices;
+    float* addr = cached ? g_scratch_addr[ctx->device].load() : nullptr;
+    if (!addr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            ar_set_error("hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
+                         e != hipSuccess ? hipGetErrorString(e) : "null address");
+            return AR_HIP_ERR_HIP;
+        }
+        addr = static_cast<float*>(ptr);
+        if (cached) g_scratch_addr[ctx->device].store(addr);
+    }
+    ctx->noalloc_scratch = addr;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_attention_decode_noalloc(ar_hip_ctx* ctx, const float* q, const float* k, const float* v,
+                                               const float* q_norm, const float* k_norm, float qk_eps,
+                                               int qk_norm_mode, float* k_cache, float* v_cache, int max_seq, int pos,
+                                               int heads, int kv_heads, int head_dim, double rope_theta, float* out) {
     AttnLaunch a;
-    a.q = q; a.k = k; a.v = v; a.qkv_stride = 0; a.q_norm = q_norm; a.k_norm = k_norm; a.qk_eps = qk_eps;
-    a.per_head_norm = qk_norm_mode == AR_QK_NORM_PER_HEAD; a.kcache = k_cache; a.vcache = v_cache;
-    a.max_seq = max_seq; a.pos = nullptr; a.pos_value = pos; a.heads = heads; a.kv_heads = kv_heads;
-    a.head_dim = head_dim; a.rope_theta = rope_theta; a.max_splits = max_splits; a.part_o = s.part_o;
-    a.part_ml = s.part_ml; a.out = out; a.out_stride = heads * head_dim; a.batch = 1;
+    AR_TRY(attention_args(ctx, q, k, v, q_norm, k_norm, qk_eps, qk_norm_mode, k_cache, v_cache, max_seq, pos, heads,
+                          kv_heads, head_dim, rope_theta, out, &a));
+    AR_CHECK_ARG(ctx->noalloc_scratch, "attention (no-alloc): scratch address of device %d unknown", ctx->device);
+    // partial outputs [heads][splits][hd] at the start, (max, sum) pairs [heads][splits][2] after
+    // them at a 256-byte boundary.  Nothing needs clearing: the combine uses only the splits this
+    // call's attention launch writes (it may load the stale slots past them, never uses them).
+    const size_t o_floats = attention_partial_floats(1, heads, a.max_splits, head_dim);
+    const size_t ml_off = (o_floats + 63) / 64 * 64;
+    const size_t need = ml_off + (size_t)heads * a.max_splits * 2;
+    AR_CHECK_ARG(need <= kNoAllocScratchFloats,
+                 "attention (no-alloc): %d heads x %d splits x (%d + 2) floats of partials exceed the %zu-float "
+                 "scratch (cache of %d rows); use ar_hip_attention_decode",
+                 heads, a.max_splits, head_dim, kNoAllocScratchFloats, max_seq);
+    a.part_o = ctx->noalloc_scratch;
+    a.part_ml = ctx->noalloc_scratch + ml_off;
     return launch_attention_decode(a, ctx->stream);
 }
 

@@ -64,6 +64,12 @@ extern "C" int ar_hip_init(int device, ar_hip_ctx** out) {
         delete ctx;
         return AR_HIP_ERR_HIP;
     }
+    const int rc = ar_ops_init(ctx);
+    if (rc != AR_HIP_OK) {
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return rc;
+    }
     *out = ctx;
     return AR_HIP_OK;
 }

@@ -69,6 +69,11 @@ _SIGS = {
                                                _c_float_p, ctypes.c_float, ctypes.c_int, _c_float_p, _c_float_p,
                                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                ctypes.c_int, ctypes.c_double, _c_float_p]),
+    "ar_hip_attention_decode_noalloc": (ctypes.c_int, [ctypes.c_void_p, _c_float_p, _c_float_p, _c_float_p,
+                                                       _c_float_p, _c_float_p, ctypes.c_float, ctypes.c_int,
+                                                       _c_float_p, _c_float_p, ctypes.c_int, ctypes.c_int,
+                                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double,
+                                                       _c_float_p]),
     "ar_hip_qwen3_create": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _c_void_pp]),
     "ar_hip_qwen3_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "ar_hip_qwen3_set_weight": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int,
@@ -309,10 +314,13 @@ class HipContext:
                                      C.ptr if C else None, O.ptr if O else None, M, N, K, epilogue))
 
     def attention_decode(self, q, k, v, q_norm, k_norm, qk_eps, qk_norm_mode, k_cache, v_cache, max_seq, pos,
-                         heads, kv_heads, head_dim, theta, out):
-        check(lib().ar_hip_attention_decode(
-            self.handle, q.ptr, k.ptr, v.ptr, q_norm.ptr if q_norm else None, k_norm.ptr if k_norm else None,
-            qk_eps, qk_norm_mode, k_cache.ptr, v_cache.ptr, max_seq, pos, heads, kv_heads, head_dim, theta, out.ptr))
+                         heads, kv_heads, head_dim, theta, out, noalloc: bool = False):
+        """ar_hip_attention_decode, or with ``noalloc`` ar_hip_attention_decode_noalloc (partials in the
+        library's fixed per-device scratch array instead of memory it allocates)."""
+        fn = lib().ar_hip_attention_decode_noalloc if noalloc else lib().ar_hip_attention_decode
+        check(fn(self.handle, q.ptr, k.ptr, v.ptr, q_norm.ptr if q_norm else None, k_norm.ptr if k_norm else None,
+                 qk_eps, qk_norm_mode, k_cache.ptr, v_cache.ptr, max_seq, pos, heads, kv_heads, head_dim, theta,
+                 out.ptr))
 
 
 def java_random_state(seed: int) -> int:

@@ -115,6 +115,19 @@ int ar_hip_attention_decode(ar_hip_ctx *ctx, const float *q, const float *k, con
                             float *k_cache, float *v_cache, int max_seq, int pos, int heads,
                             int kv_heads, int head_dim, double rope_theta, float *out);
 
+/* ar_hip_attention_decode without any allocation: no counterpart in the reference.  For callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, kernels and results; the split partials go to a fixed
+ * per-device scratch array of 2^18 floats (1 MiB, held by each GPU the library runs on until the
+ * process ends) instead of memory the library allocates.  Rejects (AR_HIP_ERR_INVALID) shapes whose
+ * partials, heads x splits x (head_dim + 2) floats, exceed it (16 heads x hd 128 caches up to
+ * ~32k rows fit).  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (several streams, or several host threads) race. */
+int ar_hip_attention_decode_noalloc(ar_hip_ctx *ctx, const float *q, const float *k, const float *v,
+                                    const float *q_norm, const float *k_norm, float qk_eps, int qk_norm_mode,
+                                    float *k_cache, float *v_cache, int max_seq, int pos, int heads,
+                                    int kv_heads, int head_dim, double rope_theta, float *out);
+
 /* Token sampling, one draw per row of `rows` logit vectors of n (device, fp32), in double:
  *   AR_SAMPLE_TOKEN: AutoregressiveModel.sampleToken(logits, n, temperature, top_p, random)
  *     (engine/ml/.../AutoregressiveModel.java:323-386): softmax of logits / temperature, nucleus
