@@ -140,6 +140,14 @@ __host__ __device__ inline void bf16_planes(float v, uint16_t* hi, uint16_t* lo)
 
 constexpr int kArgmaxSlots = 1024;
 
+// fp32 values from 65520 up (and infinities) round to an infinite fp16.  The prefill path stores
+// its MFMA operands as fp16; every conversion checks this and marks *range_flag (when given), so the
+// caller can recompute without fp16 operands instead of carrying an infinity.
+constexpr float kF16Overflow = 65520.f;
+__device__ inline void f16_range_check(float v, int* range_flag) {
+    if (__builtin_expect(fabsf(v) >= kF16Overflow, 0) && range_flag) *range_flag = 1;
+}
+
 enum {
     GEMV_EPI_STORE = 0,     // y = W x (+ b)
     GEMV_EPI_RESIDUAL = 1,  // y += W x
@@ -167,6 +175,7 @@ struct GemmLaunch {
     bool f16 = false;
     int ksplit = 1;  // > 1 (store epilogue): k-slice s of the product goes to C + s*M*ldc, for the
                      // consumer to add up in a fixed order (more blocks for small M x N, no atomics)
+    int* range_flag = nullptr;  // set when an fp16 SwiGLU output value overflows (f16_range_check)
 };
 int launch_gemm(const GemmLaunch& a, hipStream_t stream);
 
@@ -175,15 +184,16 @@ int launch_gemm(const GemmLaunch& a, hipStream_t stream);
 int launch_embed_rows(const void* table, int wdtype, int dim, const int* tokens, int token_stride, int T, int rows,
                       float* x, hipStream_t stream);
 int launch_rmsnorm_rows_f16(const float* x, const float* w, uint16_t* out, int rows, int n, float eps,
-                            hipStream_t stream);
+                            int* range_flag, hipStream_t stream);
 // x[r] += sum_s parts[s][r] (s in order; nparts may be 0), then out[r] = fp16 RMSNorm(x[r]) as above.
 int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const float* w, uint16_t* out, int rows,
-                                 int n, float eps, hipStream_t stream);
+                                 int n, float eps, int* range_flag, hipStream_t stream);
 // dst[b] = src[rows[b]] + sum_s parts[s][rows[b]] for b < count (rows of n floats).
 int launch_fold_rows(const float* src, const float* parts, int nparts, size_t part_rows, int first, int step,
                      int count, int n, float* dst, hipStream_t stream);
-// fp16 copy of bf16 data (exact for |v| >= 2^-17 inside the fp16 range), for the prefill GEMMs.
-int launch_bf16_to_f16(const uint16_t* src, uint16_t* dst, size_t n, hipStream_t stream);
+// fp16 copy of bf16 data (exact for |v| >= 2^-17 inside the fp16 range; values below 2^-17 round to
+// the fp16 grid of 2^-24), for the prefill GEMMs; range_flag as f16_range_check.
+int launch_bf16_to_f16(const uint16_t* src, uint16_t* dst, size_t n, int* range_flag, hipStream_t stream);
 struct PrefillPrep {
     const float* qkv = nullptr;
     int qkv_stride = 0;
@@ -200,6 +210,7 @@ struct PrefillPrep {
     uint16_t* k16 = nullptr;   // [B][KV][Tp][hd] fp16 keys of the prompt rows
     uint16_t* vt16 = nullptr;  // [B][KV][hd][Tp] fp16 values, transposed
     int Tp = 0;                // rows reserved per (sequence, KV head), multiple of 64
+    int* range_flag = nullptr; // set when a value stored as fp16 overflows (f16_range_check)
 };
 int launch_qk_prep(const PrefillPrep& a, hipStream_t stream);
 // Causal attention over prompt rows 0..T-1 (prefill from position 0), fp16 MFMAs, fp16 output.

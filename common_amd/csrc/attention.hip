@@ -371,9 +371,12 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     const int nch = (t1 - t0 + NGR * RU - 1) / (NGR * RU);
     for (int c = 0; c < nch; c++) {
         if (has_pos) {
+            // row pos (and every clamped duplicate of it: pos is the split's last row) was loaded
+            // stale from the cache; it takes this step's k and v, so a masked duplicate adds 0 * v
+            // of a finite row even when the stale row holds an infinity or NaN
 #pragma unroll
             for (int j = 0; j < RU; j++)
-                if (t0 + grp + NGR * (c * RU + j) == pos)
+                if (min(t0 + grp + NGR * (c * RU + j), t1 - 1) == pos)
 #pragma unroll
                     for (int e = 0; e < EPL; e++) {
                         kr[j][e] = k_new[dim_of(e)];

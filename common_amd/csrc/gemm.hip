@@ -74,6 +74,7 @@ struct GemmParams {
     uint16_t* O;        // bf16 [M][ldo] (SWIGLU)
     int ldo;
     int ksplit;         // > 1: block (tile, s) multiplies k-slice s and stores into C + s*M*ldc
+    int* rf;            // fp16 SwiGLU output overflow flag (f16_range_check), or null
 };
 
 template <int NW, int BMT>  // 1 weight matrix, or 2 for SwiGLU; BMT rows of A per block
@@ -214,7 +215,9 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
                 } else {
                     const float g = v, u = acc[NW - 1][i][j][r];
                     const float sg = 1.0f / (expf(-g) + 1.0f);
-                    p.O[(size_t)row * p.ldo + col] = M::from_float(u * (g * sg));
+                    const float o = u * (g * sg);
+                    if (F16) f16_range_check(o, p.rf);
+                    p.O[(size_t)row * p.ldo + col] = M::from_float(o);
                 }
             }
         }
@@ -395,7 +398,9 @@ __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int m
                     } else {
                         const float g = v, u = acc[NW - 1][i][j][r];
                         const float sg = 1.0f / (expf(-g) + 1.0f);
-                        p.O[(size_t)row * p.ldo + col] = Mf::from_float(u * (g * sg));
+                        const float o = u * (g * sg);
+                        if (F16) f16_range_check(o, p.rf);
+                        p.O[(size_t)row * p.ldo + col] = Mf::from_float(o);
                     }
                 }
             }
@@ -471,7 +476,7 @@ int launch_gemm(const GemmLaunch& a, hipStream_t stream) {
                  "GEMM: operands must be 16-byte aligned");
     GemmParams p;
     p.A = a.A; p.W = a.W; p.W2 = a.W2; p.M = a.M; p.N = a.N; p.K = a.K; p.lda = a.lda; p.ldw = a.ldw;
-    p.bias = a.bias; p.C = a.C; p.ldc = a.ldc; p.O = a.O; p.ldo = a.ldo; p.ksplit = a.ksplit;
+    p.bias = a.bias; p.C = a.C; p.ldc = a.ldc; p.O = a.O; p.ldo = a.ldo; p.ksplit = a.ksplit; p.rf = a.range_flag;
     switch (a.epilogue) {
         case GEMV_EPI_STORE:
             AR_CHECK_ARG(a.C && a.ldc >= a.N, "GEMM: bad fp32 output");

@@ -136,9 +136,11 @@ __global__ void f32_to_bf16_kernel(const float* src, uint16_t* dst, size_t n) {
     }
 }
 
-__global__ void bf16_to_f16_kernel(const uint16_t* src, uint16_t* dst, size_t n) {
+__global__ void bf16_to_f16_kernel(const uint16_t* src, uint16_t* dst, size_t n, int* rf) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        const _Float16 h = (_Float16)__uint_as_float((unsigned)src[i] << 16);
+        const float f = __uint_as_float((unsigned)src[i] << 16);
+        f16_range_check(f, rf);
+        const _Float16 h = (_Float16)f;
         dst[i] = *reinterpret_cast<const uint16_t*>(&h);
     }
 }
@@ -234,9 +236,9 @@ int launch_prefetch(const void* p, size_t bytes, unsigned* sink, int blocks, hip
     return AR_HIP_OK;
 }
 
-int launch_bf16_to_f16(const uint16_t* src, uint16_t* dst, size_t n, hipStream_t stream) {
+int launch_bf16_to_f16(const uint16_t* src, uint16_t* dst, size_t n, int* range_flag, hipStream_t stream) {
     if (!n) return AR_HIP_OK;
-    hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, src, dst, n);
+    hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, src, dst, n, range_flag);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -17,8 +17,9 @@ typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 halfx8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// fp32 -> fp16 bits (round to nearest even)
-__device__ inline uint16_t f2h(float f) {
+// fp32 -> fp16 bits (round to nearest even); a value that overflows marks *rf (f16_range_check)
+__device__ inline uint16_t f2h(float f, int* rf = nullptr) {
+    f16_range_check(f, rf);
     const _Float16 h = (_Float16)f;
     return *reinterpret_cast<const uint16_t*>(&h);
 }
@@ -55,21 +56,21 @@ __global__ void embed_rows_kernel(const WT* table, int dim, const int* tokens, i
 
 // out[r] = fp16((w * x[r]) * 1/sqrt(mean(x[r]^2) + eps)), one block per row.
 __global__ __launch_bounds__(256) void rmsnorm_rows_f16_kernel(const float* x, const float* w, uint16_t* out,
-                                                                int n, float eps) {
+                                                                int n, float eps, int* rf) {
     __shared__ float scratch[4];
     const float* xr = x + (size_t)blockIdx.x * n;
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) ss += xr[i] * xr[i];
     ss = block_sum(ss, scratch);
     const float r = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = f2h((w[i] * xr[i]) * r);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = f2h((w[i] * xr[i]) * r, rf);
 }
 
 // Residual fold of a split-k projection followed by the row RMSNorm: x[r] += sum_s parts[s][r] (in
 // slice order), written back, then out[r] = fp16((w * x[r]) * 1/sqrt(mean(x[r]^2) + eps)).
 __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_kernel(float* x, const float* parts, int nparts,
                                                                      size_t part_stride, const float* w,
-                                                                     uint16_t* out, int n, float eps) {
+                                                                     uint16_t* out, int n, float eps, int* rf) {
     __shared__ float scratch[4];
     float* xr = x + (size_t)blockIdx.x * n;
     float ss = 0.f;
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_kernel(float* x, co
     }
     ss = block_sum(ss, scratch);
     const float r = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = f2h((w[i] * xr[i]) * r);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = f2h((w[i] * xr[i]) * r, rf);
 }
 
 // dst[b] = src[first + b*step] + sum_s parts[s][first + b*step], rows of n floats.
@@ -110,6 +111,7 @@ struct PrepParams {
     uint16_t* qb;           // [R][heads*hd] fp16 normalised, rotated queries
     uint16_t* k16;          // [B][KV][Tp][hd] fp16 keys of the prompt rows (for the attention MFMAs)
     int Tp;
+    int* rf;                // overflow flag of the fp16 stores (f16_range_check)
 };
 
 // One block per prompt row: QK-norm (whole vector or per head), RoPE at position p0 + t, k and v
@@ -153,8 +155,8 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
         }
         const float2 cs = rope[f];
         uint16_t* qo = p.qb + (size_t)r * q_dim + (size_t)h * hd;
-        qo[f] = f2h(x1 * cs.x - x2 * cs.y);
-        qo[f + fd] = f2h(x2 * cs.x + x1 * cs.y);
+        qo[f] = f2h(x1 * cs.x - x2 * cs.y, p.rf);
+        qo[f + fd] = f2h(x2 * cs.x + x1 * cs.y, p.rf);
     }
     for (int idx = threadIdx.x; idx < p.kv_heads * fd; idx += blockDim.x) {
         const int g = idx / fd, f = idx - g * fd;
@@ -168,29 +170,30 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
         const size_t kofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd;
         const float o1 = x1 * cs.x - x2 * cs.y, o2 = x2 * cs.x + x1 * cs.y;
         if (p.kv16) {
-            reinterpret_cast<uint16_t*>(p.kcache)[kofs + f] = f2h(o1);
-            reinterpret_cast<uint16_t*>(p.kcache)[kofs + f + fd] = f2h(o2);
+            reinterpret_cast<uint16_t*>(p.kcache)[kofs + f] = f2h(o1, p.rf);
+            reinterpret_cast<uint16_t*>(p.kcache)[kofs + f + fd] = f2h(o2, p.rf);
         } else {
             reinterpret_cast<float*>(p.kcache)[kofs + f] = o1;
             reinterpret_cast<float*>(p.kcache)[kofs + f + fd] = o2;
         }
         uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
-        k16[f] = f2h(o1);
-        k16[f + fd] = f2h(o2);
+        k16[f] = f2h(o1, p.rf);
+        k16[f + fd] = f2h(o2, p.rf);
     }
     for (int idx = threadIdx.x; idx < kv_dim; idx += blockDim.x) {
         const int g = idx / hd, i = idx - g * hd;
         const size_t vofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i;
         if (p.kv16)
-            reinterpret_cast<uint16_t*>(p.vcache)[vofs] = f2h(v[idx]);
+            reinterpret_cast<uint16_t*>(p.vcache)[vofs] = f2h(v[idx], p.rf);
         else
             reinterpret_cast<float*>(p.vcache)[vofs] = v[idx];
     }
 }
 
 // Four fp32 values -> four fp16 (8 bytes, one store).
-__device__ inline uint2 pack4h(float a, float b, float c, float d) {
-    return make_uint2((unsigned)f2h(a) | ((unsigned)f2h(b) << 16), (unsigned)f2h(c) | ((unsigned)f2h(d) << 16));
+__device__ inline uint2 pack4h(float a, float b, float c, float d, int* rf) {
+    return make_uint2((unsigned)f2h(a, rf) | ((unsigned)f2h(b, rf) << 16),
+                      (unsigned)f2h(c, rf) | ((unsigned)f2h(d, rf) << 16));
 }
 
 __device__ inline float2 block_sum2(float2 v, float2* scratch) {
@@ -213,7 +216,7 @@ __device__ inline float2 block_sum2(float2 v, float2* scratch) {
 template <int NV>
 __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_v4_kernel(float* x, const float* parts, int nparts,
                                                                         size_t part_stride, const float* w,
-                                                                        uint16_t* out, int n, float eps) {
+                                                                        uint16_t* out, int n, float eps, int* rf) {
     __shared__ float scratch[4];
     const int n4 = n >> 2;
     const size_t row = (size_t)blockIdx.x * n;
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_v4_kernel(float* x,
         const int i = threadIdx.x + 256 * j;
         if (i < n4) {
             const float4 g = reinterpret_cast<const float4*>(w)[i];
-            orow[i] = pack4h((g.x * v[j].x) * r, (g.y * v[j].y) * r, (g.z * v[j].z) * r, (g.w * v[j].w) * r);
+            orow[i] = pack4h((g.x * v[j].x) * r, (g.y * v[j].y) * r, (g.z * v[j].z) * r, (g.w * v[j].w) * r, rf);
         }
     }
 }
@@ -313,8 +316,8 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
             float o1[4], o2[4];
             rotate(q1[j], q2[j], p.q_norm, (size_t)h * hd, rq, f, o1, o2);
             uint16_t* qo = p.qb + (size_t)r * q_dim + (size_t)h * hd;
-            *reinterpret_cast<uint2*>(qo + f) = pack4h(o1[0], o1[1], o1[2], o1[3]);
-            *reinterpret_cast<uint2*>(qo + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3]);
+            *reinterpret_cast<uint2*>(qo + f) = pack4h(o1[0], o1[1], o1[2], o1[3], p.rf);
+            *reinterpret_cast<uint2*>(qo + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3], p.rf);
         }
     }
     if (tid < nk) {
@@ -324,23 +327,23 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
         const size_t kofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd;
         if (p.kv16) {
             uint16_t* kc = reinterpret_cast<uint16_t*>(p.kcache) + kofs;
-            *reinterpret_cast<uint2*>(kc + f) = pack4h(o1[0], o1[1], o1[2], o1[3]);
-            *reinterpret_cast<uint2*>(kc + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3]);
+            *reinterpret_cast<uint2*>(kc + f) = pack4h(o1[0], o1[1], o1[2], o1[3], p.rf);
+            *reinterpret_cast<uint2*>(kc + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3], p.rf);
         } else {
             float* kc = reinterpret_cast<float*>(p.kcache) + kofs;
             *reinterpret_cast<float4*>(kc + f) = make_float4(o1[0], o1[1], o1[2], o1[3]);
             *reinterpret_cast<float4*>(kc + fd + f) = make_float4(o2[0], o2[1], o2[2], o2[3]);
         }
         uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
-        *reinterpret_cast<uint2*>(k16 + f) = pack4h(o1[0], o1[1], o1[2], o1[3]);
-        *reinterpret_cast<uint2*>(k16 + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3]);
+        *reinterpret_cast<uint2*>(k16 + f) = pack4h(o1[0], o1[1], o1[2], o1[3], p.rf);
+        *reinterpret_cast<uint2*>(k16 + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3], p.rf);
     }
     for (int i4 = tid; i4 < kv_dim / 4; i4 += 256) {
         const int g = (4 * i4) / hd, i = 4 * i4 - g * hd;
         const float4 vv = reinterpret_cast<const float4*>(v)[i4];
         const size_t vofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i;
         if (p.kv16)
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.vcache) + vofs) = pack4h(vv.x, vv.y, vv.z, vv.w);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.vcache) + vofs) = pack4h(vv.x, vv.y, vv.z, vv.w, p.rf);
         else
             *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.vcache) + vofs) = vv;
     }
@@ -351,7 +354,7 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
 // the prompt are written as 0).
 template <int HD, typename KVT>
 __global__ __launch_bounds__(256) void vt16_kernel(const KVT* vcache, int S, int p0, int T, int kv_heads,
-                                                   uint16_t* vt16, int Tp) {
+                                                   uint16_t* vt16, int Tp, int* rf) {
     __shared__ float tile[64][HD + 1];
     const int t0 = blockIdx.x * 64, g = blockIdx.y, b = blockIdx.z;
     const size_t head = (size_t)b * kv_heads + g;
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(256) void vt16_kernel(const KVT* vcache, int S, int
     uint16_t* dst = vt16 + head * HD * Tp + t0;
     for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
         const int i = idx / 64, r = idx - i * 64;
-        dst[(size_t)i * Tp + r] = f2h(tile[r][i]);
+        dst[(size_t)i * Tp + r] = f2h(tile[r][i], rf);
     }
 }
 
@@ -595,15 +598,15 @@ int launch_embed_rows(const void* table, int wdtype, int dim, const int* tokens,
 }
 
 int launch_rmsnorm_rows_f16(const float* x, const float* w, uint16_t* out, int rows, int n, float eps,
-                            hipStream_t stream) {
+                            int* range_flag, hipStream_t stream) {
     AR_CHECK_ARG(x && w && out && rows > 0 && n > 0, "rmsnorm rows: bad arguments");
-    hipLaunchKernelGGL(rmsnorm_rows_f16_kernel, dim3(rows), dim3(256), 0, stream, x, w, out, n, eps);
+    hipLaunchKernelGGL(rmsnorm_rows_f16_kernel, dim3(rows), dim3(256), 0, stream, x, w, out, n, eps, range_flag);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
 
 int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const float* w, uint16_t* out, int rows,
-                                 int n, float eps, hipStream_t stream) {
+                                 int n, float eps, int* range_flag, hipStream_t stream) {
     AR_CHECK_ARG(x && w && out && rows > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0),
                  "fold rmsnorm rows: bad arguments");
     const bool v4 = n % 4 == 0 && n <= 4096 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
@@ -611,16 +614,16 @@ int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const
                     (nparts == 0 || (reinterpret_cast<uintptr_t>(parts) & 15) == 0);
     if (v4 && n <= 1024)
         hipLaunchKernelGGL(fold_rmsnorm_rows_f16_v4_kernel<1>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
-                           (size_t)rows * n, w, out, n, eps);
+                           (size_t)rows * n, w, out, n, eps, range_flag);
     else if (v4 && n <= 2048)
         hipLaunchKernelGGL(fold_rmsnorm_rows_f16_v4_kernel<2>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
-                           (size_t)rows * n, w, out, n, eps);
+                           (size_t)rows * n, w, out, n, eps, range_flag);
     else if (v4)
         hipLaunchKernelGGL(fold_rmsnorm_rows_f16_v4_kernel<4>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
-                           (size_t)rows * n, w, out, n, eps);
+                           (size_t)rows * n, w, out, n, eps, range_flag);
     else
         hipLaunchKernelGGL(fold_rmsnorm_rows_f16_kernel, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
-                           (size_t)rows * n, w, out, n, eps);
+                           (size_t)rows * n, w, out, n, eps, range_flag);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
@@ -645,7 +648,7 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     p.per_head = a.per_head; p.rope_tab = a.rope_tab; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.S;
     p.kv16 = a.kv16;
     p.T = a.T; p.p0 = a.p0; p.heads = a.heads; p.kv_heads = a.kv_heads; p.hd = a.hd; p.qb = a.qb;
-    p.k16 = a.k16; p.Tp = a.Tp;
+    p.k16 = a.k16; p.Tp = a.Tp; p.rf = a.range_flag;
     const int nq = a.heads * a.hd / 8, nk = a.kv_heads * a.hd / 8;
     const bool v4 = !a.per_head && a.hd % 8 == 0 && a.qkv_stride % 4 == 0 && nk <= 256 && nq <= 4 * 256 &&
                     (reinterpret_cast<uintptr_t>(a.qkv) & 15) == 0 &&
@@ -667,7 +670,7 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     const dim3 vgrid((a.T + 63) / 64, a.kv_heads, a.B);
 #define AR_VT16(HDV, T_)                                                                                     \
     hipLaunchKernelGGL((vt16_kernel<HDV, T_>), vgrid, dim3(256), 0, stream, reinterpret_cast<const T_*>(a.vcache), \
-                       a.S, a.p0, a.T, a.kv_heads, a.vt16, a.Tp)
+                       a.S, a.p0, a.T, a.kv_heads, a.vt16, a.Tp, a.range_flag)
     if (a.hd != 128 && a.hd != 64) {
         ar_set_error("qk prep: head_dim %d not supported (64, 128)", a.hd);
         return AR_HIP_ERR_INVALID;

@@ -127,6 +127,11 @@ struct ar_qwen3 {
     // fp16 copies of the projection matrices for the prefill GEMMs (made on the first prefill)
     uint16_t* pf_w16 = nullptr;
     bool pf_w16_valid = false;
+    // fp16 range flags (device): [0] an activation stored as fp16 overflowed during the last prefill,
+    // [1] a weight did in the fp16 copies; either sends the prompt through the decode step instead
+    int* pf_flag = nullptr;
+    bool pf_w16_in_range = true;  // host copy of pf_flag[1] after the fp16 copies were made
+    int pf_by_steps = 0;          // prefill calls that went through the decode step
 
     int timed = AR_KT_NONE;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
@@ -154,7 +159,8 @@ void release(ar_qwen3* m) {
     if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
                     m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->smp_rng, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
-                    m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16};
+                    m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16,
+                    m->pf_flag};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     delete m;
@@ -700,6 +706,12 @@ extern "C" int ar_hip_qwen3_run(ar_qwen3* m, int steps, int32_t* tokens_out) {
     return AR_HIP_OK;
 }
 
+extern "C" int ar_hip_qwen3_prefill_by_steps(ar_qwen3* m, int* count) {
+    AR_CHECK_ARG(m && count, "null argument");
+    *count = m->pf_by_steps;
+    return AR_HIP_OK;
+}
+
 extern "C" int ar_hip_qwen3_position(ar_qwen3* m, int* pos) {
     AR_CHECK_ARG(m && pos, "null argument");
     *pos = m->host_pos;
@@ -790,6 +802,7 @@ int prefill_ksplit(const ar_qwen3* m, size_t rows, int N, int K) {
 }
 
 int ensure_prefill_buffers(ar_qwen3* m, size_t rows) {
+    if (!m->pf_flag) AR_TRY(alloc_zero(m, 2 * sizeof(int), (void**)&m->pf_flag));
     if (m->pf_rows >= rows) return AR_HIP_OK;
     void** bufs[] = {(void**)&m->pf_x, (void**)&m->pf_h, (void**)&m->pf_qkv, (void**)&m->pf_q, (void**)&m->pf_act};
     for (void** b : bufs)
@@ -824,21 +837,35 @@ int ensure_f16_weights(ar_qwen3* m) {
     const size_t d = c.dim, F = c.hidden_dim;
     const size_t per_layer = (size_t)m->qkv_dim * d + d * m->q_dim + 3 * F * d;
     if (!m->pf_w16) AR_TRY(ar_ctx_alloc(m->ctx, per_layer * c.layer_count * 2, (void**)&m->pf_w16));
+    AR_HIP_TRY(hipMemsetAsync(m->pf_flag + 1, 0, sizeof(int), m->ctx->stream));
     uint16_t* dst = m->pf_w16;
     for (int l = 0; l < c.layer_count; l++) {
         const Layer& L = m->layers[l];
         const void* srcs[5] = {L.wqkv, L.wo, L.w1, L.w3, L.w2};
         const size_t counts[5] = {(size_t)m->qkv_dim * d, d * m->q_dim, F * d, F * d, d * F};
         for (int i = 0; i < 5; i++) {
-            AR_TRY(launch_bf16_to_f16((const uint16_t*)srcs[i], dst, counts[i], m->ctx->stream));
+            AR_TRY(launch_bf16_to_f16((const uint16_t*)srcs[i], dst, counts[i], m->pf_flag + 1, m->ctx->stream));
             dst += counts[i];
         }
     }
+    int overflow = 0;
+    AR_HIP_TRY(hipMemcpyAsync(&overflow, m->pf_flag + 1, sizeof(int), hipMemcpyDeviceToHost, m->ctx->stream));
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    m->pf_w16_in_range = overflow == 0;  // a weight past the fp16 range: every prefill takes the decode step
     m->pf_w16_valid = true;
     return AR_HIP_OK;
 }
 
 }  // namespace
+
+// The prompt through the decode step, one token per step (the reference's own prefill), from
+// position 0: prompt_len calls of next() leave the model where a batched prefill does.
+static int prefill_by_steps(ar_qwen3* m, int T, float* logits_out) {
+    m->pf_by_steps++;
+    AR_TRY(ar_hip_qwen3_reset(m));
+    if (T > 1) AR_TRY(ar_hip_qwen3_run(m, T - 1, nullptr));
+    return ar_hip_qwen3_next(m, nullptr, logits_out);
+}
 
 extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
     AR_CHECK_ARG(m, "null model");
@@ -846,18 +873,16 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
     AR_TRY(check_ready(m, T));
     AR_CHECK_ARG(m->host_pos == 0, "prefill starts a sequence: reset() first (position is %d)", m->host_pos);
     const ar_qwen3_cfg& c = m->cfg;
-    if (c.weight_dtype != AR_DTYPE_BF16) {
-        // fp32 weights: the MFMA path needs bf16 operands, so the prompt goes through the decode
-        // step token by token (the reference's own prefill)
-        if (T > 1) AR_TRY(ar_hip_qwen3_run(m, T - 1, nullptr));
-        return ar_hip_qwen3_next(m, nullptr, logits_out);
-    }
+    if (c.weight_dtype != AR_DTYPE_BF16) return prefill_by_steps(m, T, logits_out);
     hipStream_t st = m->ctx->stream;
     const int B = m->B, d = c.dim, F = c.hidden_dim, qd = m->q_dim;
     const size_t R = (size_t)B * T;
     AR_CHECK_ARG(R <= (size_t)INT32_MAX / 16, "prefill: %zu rows too many", R);
     AR_TRY(ensure_prefill_buffers(m, R));
     AR_TRY(ensure_f16_weights(m));
+    if (!m->pf_w16_in_range) return prefill_by_steps(m, T, logits_out);
+    AR_HIP_TRY(hipMemsetAsync(m->pf_flag, 0, sizeof(int), st));
+    int* const rf = m->pf_flag;
     const size_t dd = d, FF = F;
     const size_t per_layer16 = (size_t)m->qkv_dim * dd + dd * qd + 3 * FF * dd;
     AR_TRY(launch_embed_rows(m->embed, c.weight_dtype, d, m->tokens, m->S + 1, T, (int)R, m->pf_x, st));
@@ -880,7 +905,7 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         const uint16_t* w3_16 = w1_16 + FF * dd;
         const uint16_t* w2_16 = w3_16 + FF * dd;
         AR_TRY(launch_fold_rmsnorm_rows_f16(m->pf_x, m->pf_part, pending, L.attn_norm, m->pf_h, (int)R, d,
-                                            (float)c.epsilon, st));
+                                            (float)c.epsilon, rf, st));
         pending = 0;
         GemmLaunch g;
         g.A = m->pf_h; g.lda = d; g.W = wqkv16; g.ldw = d; g.M = (int)R; g.N = m->qkv_dim; g.K = d;
@@ -893,7 +918,7 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         pp.vcache = (char*)m->vcache + l * layer_cache * m->kv_elem;
         pp.kv16 = c.kv_dtype == AR_DTYPE_F16; pp.B = B; pp.S = m->S;
         pp.T = T; pp.p0 = 0; pp.heads = c.head_count; pp.kv_heads = c.kv_head_count; pp.hd = c.head_size;
-        pp.qb = m->pf_q; pp.k16 = m->pf_k16; pp.vt16 = m->pf_vt16; pp.Tp = m->pf_tp;
+        pp.qb = m->pf_q; pp.k16 = m->pf_k16; pp.vt16 = m->pf_vt16; pp.Tp = m->pf_tp; pp.range_flag = rf;
         AR_TRY(launch_qk_prep(pp, st));
         AR_TRY(launch_flash_prefill(m->pf_q, m->pf_k16, m->pf_vt16, m->pf_h, B, T, m->pf_tp, c.head_count,
                                     c.kv_head_count, c.head_size, st));
@@ -905,10 +930,11 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         }
         AR_TRY(launch_gemm(o, st));
         AR_TRY(launch_fold_rmsnorm_rows_f16(m->pf_x, m->pf_part, so > 1 ? so : 0, L.ffn_norm, m->pf_h, (int)R, d,
-                                            (float)c.epsilon, st));
+                                            (float)c.epsilon, rf, st));
         GemmLaunch u;
         u.A = m->pf_h; u.lda = d; u.W = w1_16; u.W2 = w3_16; u.ldw = d; u.M = (int)R;
         u.N = F; u.K = d; u.O = m->pf_act; u.ldo = F; u.epilogue = GEMV_EPI_SWIGLU; u.f16 = true;
+        u.range_flag = rf;
         AR_TRY(launch_gemm(u, st));
         GemmLaunch dn;
         dn.A = m->pf_act; dn.lda = F; dn.W = w2_16; dn.ldw = F; dn.M = (int)R; dn.N = d; dn.K = F;
@@ -919,6 +945,14 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         }
         AR_TRY(launch_gemm(dn, st));
     }
+    // A value stored as an fp16 MFMA operand left the fp16 range (outlier activations of a real
+    // checkpoint): the batched pass is discarded and the prompt goes through the decode step, whose
+    // activations stay fp32, leaving the model where the batched pass would.  Checked before the
+    // logits and the sampler run, so no draw of a sequence's generator is spent on the discarded pass.
+    int overflow = 0;
+    AR_HIP_TRY(hipMemcpyAsync(&overflow, m->pf_flag, sizeof(int), hipMemcpyDeviceToHost, st));
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    if (overflow) return prefill_by_steps(m, T, logits_out);
     // last prompt row of every sequence -> residual stream of the decode plan, then the final
     // RMSNorm + logits GEMV leaves the greedy keys for the next step
     AR_TRY(launch_fold_rows(m->pf_x, m->pf_part, pending, R, T - 1, T, B, d, m->x, st));

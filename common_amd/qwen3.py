@@ -72,6 +72,13 @@ class AutoregressiveModel:
         hw.check(hw.lib().ar_hip_qwen3_run(self.handle, steps, out.ctypes.data))
         return out
 
+    def prefill_by_steps(self) -> int:
+        """Prefill calls of this model that went through the decode step (fp32 weights, or a value
+        outside the fp16 range of the bf16 path's MFMA operands)."""
+        v = ctypes.c_int()
+        hw.check(hw.lib().ar_hip_qwen3_prefill_by_steps(self.handle, ctypes.byref(v)))
+        return v.value
+
     def get_current_step(self) -> int:
         v = ctypes.c_int()
         hw.check(hw.lib().ar_hip_qwen3_position(self.handle, ctypes.byref(v)))

@@ -219,8 +219,15 @@ int ar_hip_qwen3_run(ar_qwen3 *m, int steps, int32_t *tokens_out);
  * the model exactly where prompt_len calls of next() would: position = prompt length, KV cache
  * rows 0..prompt_len-1 written, and the next next() feeds the greedy token of the last prompt
  * row.  logits_out (optional, batch x vocab, host) receives the last prompt row's logits.
- * AutoregressiveModel.next over the prompt (AutoregressiveModel.java:295-299), batched. */
+ * AutoregressiveModel.next over the prompt (AutoregressiveModel.java:295-299), batched.
+ * The bf16 path stores its MFMA operands as fp16; when any value stored that way (a weight, a
+ * normalised row, a rotated query or key, a value row, a SwiGLU output) lies outside the fp16 range
+ * (|v| >= 65520), the batched pass is discarded before the logits and the sampler run, and the
+ * prompt goes through the decode step instead (fp32 activations; slower, same result as next()). */
 int ar_hip_qwen3_prefill(ar_qwen3 *m, float *logits_out);
+/* Number of ar_hip_qwen3_prefill calls on this model that went through the decode step (fp32
+ * weights, or a value outside the fp16 range on the bf16 path). */
+int ar_hip_qwen3_prefill_by_steps(ar_qwen3 *m, int *count);
 /* Token selection of next / run / prefill.  Default: AR_SAMPLE_MODEL at temperature 0, i.e. greedy,
  * as a new AutoregressiveModel starts.  AR_SAMPLE_MODEL with another temperature is
  * AutoregressiveModel.setTemperature (AutoregressiveModel.java:258-260) with the sample function of

@@ -270,6 +270,30 @@ class OracleQwen3:
         _fn("oracle_model_hidden", self.precision)(self.h, out.ctypes.data)
         return out
 
+    def prefill(self, tokens, want_logits: bool = True):
+        """The prompt rows at once from the current position (oracle/qwen3_oracle_prefill.h): the
+        same values as one step() per token, computed over all rows together.  Returns (greedy
+        token after the last row, that row's logits)."""
+        ids = np.ascontiguousarray(tokens, dtype=np.int32)
+        logits = np.empty(self.cfg.vocab_size, dtype=self.dt) if want_logits else None
+        fn = _fn("oracle_model_prefill", self.precision)
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        nxt = fn(self.h, ids.ctypes.data, ids.size, logits.ctypes.data if want_logits else None)
+        if nxt < 0:
+            raise RuntimeError("oracle prefill failed (position past capacity, bad token or unsupported shape)")
+        return nxt, logits
+
+    def generate_prefilled(self, prompt, n_decode):
+        """generate() with the prompt through prefill(): returns (tokens fed at each step past the
+        prompt's last row, logits of the last prompt row and of every decode step)."""
+        nxt, lg = self.prefill(prompt)
+        fed, logits = [], [lg]
+        for _ in range(n_decode):
+            fed.append(nxt)
+            nxt, lg = self.step(nxt)
+            logits.append(lg)
+        return np.array(fed, dtype=np.int32), np.stack(logits)
+
     def generate(self, prompt, n_decode, want_logits=True, sampler=None):
         """AutoregressiveModel semantics: returns (tokens fed at each step, logits per step).
         ``sampler(logits) -> token`` replaces the greedy choice past the prompt (it is called only

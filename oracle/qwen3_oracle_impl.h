@@ -211,28 +211,34 @@ void FN(oracle_softmax)(REAL *x, int rows, int n) {
  * full_seq = 0 stops at t = pos.  Both give identical results because exp(-10000 - m)
  * underflows to +0 in both precisions; tests check the two modes agree bit for bit.
  */
+/* One query head of oracle_attention: q_h (hd), KV head g of the compact caches, rows 0..n-1
+ * scored, rows past pos masked; s is scratch of n values. */
+static void FN(attention_head)(REAL *out_h, const REAL *q_h, const REAL *kc, const REAL *vc, int kv_heads, int g,
+                               int hd, int pos, int n, REAL *s) {
+    REAL scale = (REAL)sqrt((double)hd);
+    for (int t = 0; t < n; t++) {
+        const REAL *k = kc + ((size_t)t * kv_heads + g) * hd;
+        REAL acc = 0;
+        for (int i = 0; i < hd; i++) acc += q_h[i] * k[i];
+        acc = acc / scale;
+        s[t] = acc + ((t > pos) ? (REAL)-10000.0 : (REAL)0.0);
+    }
+    FN(oracle_softmax)(s, 1, n);
+    for (int i = 0; i < hd; i++) {
+        REAL acc = 0;
+        for (int t = 0; t < n; t++) acc += s[t] * vc[((size_t)t * kv_heads + g) * hd + i];
+        out_h[i] = acc;
+    }
+}
+
 void FN(oracle_attention)(REAL *out, const REAL *q, const REAL *kc, const REAL *vc,
                           int heads, int kv_heads, int hd, int pos, int seq_len, int full_seq) {
     int per = heads / kv_heads;
     int n = full_seq ? seq_len : pos + 1;
-    REAL scale = (REAL)sqrt((double)hd);
 #pragma omp parallel for schedule(static)
     for (int h = 0; h < heads; h++) {
-        int g = h / per;
         REAL *s = (REAL *)malloc(sizeof(REAL) * (size_t)n);
-        for (int t = 0; t < n; t++) {
-            const REAL *k = kc + ((size_t)t * kv_heads + g) * hd;
-            REAL acc = 0;
-            for (int i = 0; i < hd; i++) acc += q[(size_t)h * hd + i] * k[i];
-            acc = acc / scale;
-            s[t] = acc + ((t > pos) ? (REAL)-10000.0 : (REAL)0.0);
-        }
-        FN(oracle_softmax)(s, 1, n);
-        for (int i = 0; i < hd; i++) {
-            REAL acc = 0;
-            for (int t = 0; t < n; t++) acc += s[t] * vc[((size_t)t * kv_heads + g) * hd + i];
-            out[(size_t)h * hd + i] = acc;
-        }
+        FN(attention_head)(out + (size_t)h * hd, q + (size_t)h * hd, kc, vc, kv_heads, h / per, hd, pos, n, s);
         free(s);
     }
 }
@@ -479,6 +485,8 @@ int FN(oracle_model_step)(void *mp, int token, REAL *logits_out) {
     m->pos = pos + 1;
     return next;
 }
+
+#include "qwen3_oracle_prefill.h"
 
 /* Copies the current residual-stream vector x (dim values) for activation checks. */
 void FN(oracle_model_hidden)(void *mp, REAL *out) {

@@ -191,3 +191,28 @@ def test_attention_rejects_out_of_range_position(ctx):
     with pytest.raises(hw.HardwareException) as e:
         ctx.attention_decode(z, z, z, None, None, 1e-6, 0, z, z, 4, 4, 1, 1, 64, 1e6, z)
     assert e.value.code == hw.AR_HIP_ERR_INVALID
+
+
+@pytest.mark.parametrize("heads,kv,hd,max_seq,pos", [(4, 2, 64, 48, 20), (16, 8, 128, 384, 200), (16, 8, 128, 4097, 3000)])
+def test_attention_ignores_stale_nan_rows(ctx, heads, kv, hd, max_seq, pos):
+    """Rows at and past the position hold NaN (a previous sequence that overflowed): row pos is
+    overwritten by this step and the rest are masked, so the output is finite and matches the oracle
+    (one-block form and split form)."""
+    r = _rng(pos)
+    qd, kd = heads * hd, kv * hd
+    q, k, v = (r.standard_normal(n).astype(np.float32) for n in (qd, kd, kd))
+    kc = np.full((max_seq, kv, hd), np.nan, np.float32)
+    vc = np.full((max_seq, kv, hd), np.nan, np.float32)
+    kc[:pos] = r.standard_normal((pos, kv, hd))
+    vc[:pos] = r.standard_normal((pos, kv, hd))
+    kcd = ctx.to_device(np.ascontiguousarray(kc.transpose(1, 0, 2)))
+    vcd = ctx.to_device(np.ascontiguousarray(vc.transpose(1, 0, 2)))
+    od = ctx.allocate(qd * 4)
+    ctx.attention_decode(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v), None, None, 1e-6, 0, kcd, vcd, max_seq,
+                         pos, heads, kv, hd, 1e6, od)
+    ctx.synchronize()
+    out = od.download(np.float32, qd)
+    kc64, vc64 = kc.astype(np.float64), vc.astype(np.float64)
+    ref = oracle.attention_block(q, k, v, None, None, kc64, vc64, heads, kv, hd, pos, 1e6, 1e-6)
+    assert np.isfinite(out).all()
+    assert rel_err(out, ref) <= TOL

@@ -283,3 +283,54 @@ def test_fp16_kv_cache_c5_layer_shape_close_to_fp32_cache(ctx):
             _, out[kv] = am.next(return_logits=True)
     for b in range(8):
         assert rel_err(out[C.DTYPE_F16][b], out[C.DTYPE_F32][b]) <= BF16_TOL, b
+
+
+def _prefill_vs_oracle(ctx, cfg, sd, prompts, steps):
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        am.reset()
+        for b, p in enumerate(prompts):
+            am.set_prompt(p, seq=b)
+        lp = am.prefill(return_logits=True)
+        toks = am.run(steps)
+        by_steps = am.prefill_by_steps()
+    T = len(prompts[0])
+    for b, p in enumerate(prompts):
+        rf, rl = oracle.OracleQwen3(cfg, sd, precision="fp64").generate(p, steps)
+        assert rel_err(lp[b], rl[T - 1]) <= BF16_TOL, (b, rel_err(lp[b], rl[T - 1]))
+        for s in range(steps):
+            top = np.sort(rl[T - 1 + s])[-2:]
+            if (top[1] - top[0]) / abs(top[1]) < BF16_TOL:
+                break
+            assert toks[b, s] == rf[T + s], (b, s)
+    return by_steps
+
+
+@pytest.mark.parametrize("where", ["ffn_norm_gain", "swiglu_output"])
+def test_prefill_fp16_overflow_takes_the_decode_step(ctx, where):
+    """Activations past the fp16 range (a real checkpoint's outliers): a post-attention RMSNorm gain
+    of 2^17 (normalised rows ~1e5) or gate/up weights scaled by 2^11 (SwiGLU outputs ~1e6).  The
+    batched pass sees the overflow and the prompt goes through the decode step: logits and tokens
+    still match the FP64 oracle."""
+    cfg = _bf16_cfg(C.C1_TINY, seq_len=96, max_batch=2)
+    sd = synthetic.state_dict(cfg, seed=31)
+    if where == "ffn_norm_gain":
+        sd["model.layers.0.post_attention_layernorm.weight"] = sd["model.layers.0.post_attention_layernorm.weight"] * 2.0 ** 17
+    else:
+        for k in ("mlp.gate_proj.weight", "mlp.up_proj.weight"):
+            sd["model.layers.1." + k] = sd["model.layers.1." + k] * 2.0 ** 11
+    prompts = [synthetic.prompt_ids(40, cfg.vocab_size, seed=32 + b) for b in range(2)]
+    assert _prefill_vs_oracle(ctx, cfg, sd, prompts, 4) == 1
+
+
+def test_prefill_tiny_weights_stay_on_the_batched_path(ctx):
+    """Weights below 2^-17 lose bits in their fp16 copies (the fp16 grid there is 2^-24, an absolute
+    error of at most 2^-25 per weight): a down projection scaled by 2^-12 (|w| ~ 5e-6) stays on the
+    batched path and still matches the FP64 oracle within the bf16 tolerance."""
+    cfg = _bf16_cfg(C.C1_TINY, seq_len=96, max_batch=1)
+    sd = synthetic.state_dict(cfg, seed=33)
+    sd["model.layers.1.mlp.down_proj.weight"] = sd["model.layers.1.mlp.down_proj.weight"] * 2.0 ** -12
+    w = sd["model.layers.1.mlp.down_proj.weight"]
+    assert np.mean(np.abs(w) < 2.0 ** -17) > 0.5
+    prompts = [synthetic.prompt_ids(40, cfg.vocab_size, seed=34)]
+    assert _prefill_vs_oracle(ctx, cfg, sd, prompts, 4) == 0

@@ -4,6 +4,7 @@ Each check is a known answer from the reference's own tests, a closed form, an i
 brute-force restatement in a different formulation, chosen so that a plausible mistake (a
 swapped half, a wrong head index, a dropped term, a transposed operand) fails one of them.
 """
+import dataclasses
 import math
 
 import numpy as np
@@ -306,3 +307,74 @@ def test_oracle_rejects_bad_weights_and_positions():
         oracle.OracleQwen3(cfg, {"model.layers.0.mlp.up_proj.weight": np.zeros(3, np.float32)})
     with pytest.raises(RuntimeError):
         m.step(0)  # no embedding loaded
+
+
+# ---- batched prompt pass ---------------------------------------------------------------------------
+PREFILL_CASES = {
+    # C1 (G = 2, hd 64), tied embeddings
+    "c1": dataclasses.replace(C.C1_TINY),
+    # GQA 4 with q_dim != dim, per-head QK-norm, q/k/v biases, untied head, a ragged dense width
+    "gqa4": C.Qwen3Config(dim=200, hidden_dim=328, layer_count=3, head_count=8, kv_head_count=2, vocab_size=301,
+                          seq_len=40, head_size=64, qk_norm_mode=C.QK_NORM_PER_HEAD, qkv_bias=True,
+                          shared_weights=False),
+    # G = 8 heads per KV head (all vector lanes), hd 128
+    "gqa8": C.Qwen3Config(dim=256, hidden_dim=512, layer_count=2, head_count=8, kv_head_count=1, vocab_size=97,
+                          seq_len=24, head_size=128),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PREFILL_CASES))
+@pytest.mark.parametrize("prec", ["fp64", "fp32"])
+@pytest.mark.parametrize("full_seq", [False, True])
+def test_prefill_equals_stepping_bit_for_bit(name, prec, full_seq):
+    """oracle_model_prefill lays the prompt's work out over all rows (packed weight panels, heads in
+    vector lanes, the last layer only for the last row) but must compute exactly what one step per
+    token computes: tokens, last-row logits and hidden state equal bit for bit, then the decode steps
+    after it too.  Prompts of 1, 5 (ragged blocks of 4) and 13 rows; a prefill that starts after 3
+    stepped tokens; the full-sequence -10000 mask form."""
+    cfg = PREFILL_CASES[name]
+    sd = synthetic.state_dict(cfg, seed=5)
+    prompt = synthetic.prompt_ids(16, cfg.vocab_size, seed=5)
+    for n in (1, 5, 13):
+        a = oracle.OracleQwen3(cfg, sd, precision=prec, full_seq_mask=full_seq)
+        b = oracle.OracleQwen3(cfg, sd, precision=prec, full_seq_mask=full_seq)
+        fed, logits = a.generate(prompt[:n], 4)
+        nxt, lg = b.prefill(prompt[:n])
+        assert nxt == fed[n] and np.array_equal(lg, logits[n - 1])
+        assert np.array_equal(b.hidden(), a_hidden_after(cfg, sd, prec, full_seq, prompt[:n]))
+        fed_b, logits_b = [], []
+        for _ in range(4):
+            fed_b.append(nxt)
+            nxt, lgb = b.step(nxt)
+            logits_b.append(lgb)
+        assert fed_b == list(fed[n:]) and np.array_equal(np.stack(logits_b), logits[n:])
+        a.close(); b.close()
+    # starting mid-sequence: 3 stepped tokens, then the rest as one prefill
+    a = oracle.OracleQwen3(cfg, sd, precision=prec, full_seq_mask=full_seq)
+    b = oracle.OracleQwen3(cfg, sd, precision=prec, full_seq_mask=full_seq)
+    fed, logits = a.generate(prompt[:11], 0)
+    for t in prompt[:3]:
+        b.step(int(t))
+    nxt, lg = b.prefill(prompt[3:11])
+    assert np.array_equal(lg, logits[10])
+    assert np.array_equal(b.hidden(), a.hidden())
+
+
+def a_hidden_after(cfg, sd, prec, full_seq, prompt):
+    o = oracle.OracleQwen3(cfg, sd, precision=prec, full_seq_mask=full_seq)
+    for t in prompt:
+        o.step(int(t), want_logits=False)
+    h = o.hidden()
+    o.close()
+    return h
+
+
+def test_prefill_rejects_what_stepping_rejects():
+    cfg = PREFILL_CASES["c1"]
+    sd = synthetic.state_dict(cfg, seed=1)
+    o = oracle.OracleQwen3(cfg, sd)
+    with pytest.raises(RuntimeError):
+        o.prefill(np.arange(cfg.seq_len + 1) % cfg.vocab_size)   # past the cache
+    with pytest.raises(RuntimeError):
+        o.prefill([0, cfg.vocab_size])                            # token outside the vocabulary
+    assert o.prefill([1, 2, 3])[0] >= 0                           # nothing was consumed by the failures
