@@ -71,7 +71,8 @@ def kernel_bytes(cfg, which, batch=1):
     return None
 
 
-MFMA_PEAK_TFLOPS = 2500.0
+MFMA_PEAK_TFLOPS = 2500.0      # dense bf16 / fp16
+MFMA_F32_PEAK_TFLOPS = 157.3   # dense fp32
 
 
 def prefill_flops(cfg, T):
@@ -259,10 +260,14 @@ def c2_section(args):
             "note": "wall time per C-ABI call, including the op's q/k/v staging copies and position upload"}
 
 
+TRAFFIC_STEPS = 8
+
+
 def traffic_probe(args):
     """Workload for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic: one plain
-    256 MiB device copy (the counter scale: known bytes), then a few eager C3 decode steps, so every
-    launch of the logits GEMV is its own dispatch."""
+    256 MiB device copy (the counter scale: known bytes), the C3 prompt (128 tokens) through the
+    prefill, then TRAFFIC_STEPS eager C3 decode steps at positions 128.., so every launch of every
+    decode kernel class is its own dispatch."""
     from common_amd import config as C
     from common_amd import hardware as hw
     from common_amd import synthetic
@@ -270,7 +275,7 @@ def traffic_probe(args):
 
     nbytes = 256 << 20
     cfg = C.C3_0_6B
-    prompt = synthetic.prompt_ids(4, cfg.vocab_size, seed=args.seed)
+    prompt = synthetic.prompt_ids(C.C3_PROMPT, cfg.vocab_size, seed=args.seed)
     with hw.HipContext() as ctx:
         a, b = ctx.allocate(nbytes), ctx.allocate(nbytes)
         ctx.copy(b, a, nbytes)
@@ -280,19 +285,86 @@ def traffic_probe(args):
             am.use_graph(False)
             am.reset()
             am.set_prompt(prompt)
-            am.run(8)
+            am.prefill()
+            am.run(TRAFFIC_STEPS)
             ctx.synchronize()
-    print(json.dumps({"traffic_probe": {"copy_bytes": nbytes, "decode_steps": 8}}), flush=True)
+    print(json.dumps({"traffic_probe": {"copy_bytes": nbytes, "prompt": C.C3_PROMPT, "decode_steps": TRAFFIC_STEPS}}),
+          flush=True)
+
+
+# kernel-name prefixes of the C3 decode classes in a rocprofv3 trace (batch 1, fp32 weights)
+C3_CLASS_KERNELS = {
+    "qkv_gemv_rmsnorm": "gemv_rx_kernel<float, 2, 4, 0>",
+    "o_gemv_residual": "gemv_rx_kernel<float, 1, 8, 1>",
+    "gate_up_gemv_swiglu": "gemv_rx_kernel<float, 2, 4, 2>",
+    "down_gemv_residual": "gemv_rx_kernel<float, 1, 12, 1>",
+    "attention_decode": "attn_decode_kernel",
+    "attention_combine": "attn_combine_kernel",
+    "logits_gemv_argmax": "gemv_argmax_kernel",
+    "step_begin": "step_begin_kernel",
+}
+
+
+def c3_class_bytes(cfg, name, pos):
+    """Algorithmic bytes of one launch of a C3 decode class at position `pos`."""
+    from common_amd import qwen3 as q
+    kt = {"qkv_gemv_rmsnorm": q.KT_QKV, "o_gemv_residual": q.KT_O, "gate_up_gemv_swiglu": q.KT_GATE_UP,
+          "down_gemv_residual": q.KT_DOWN, "logits_gemv_argmax": q.KT_LOGITS}
+    if name in kt:
+        return kernel_bytes(cfg, kt[name])
+    if name == "attention_decode":  # K and V rows 0..pos read, row pos written, q/k/v and gains in, out
+        return 2 * (pos + 1) * cfg.kv_dim * 4 + 2 * cfg.kv_dim * 4 + (cfg.q_dim + 2 * cfg.kv_dim) * 4 * 2 + cfg.q_dim * 4
+    return None
+
+
+def traffic_summary(fetch_dir, write_dir):
+    """Per-class HBM traffic from the two counter passes' CSVs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    of `bench.py --traffic-probe`), each counter scaled by what it reads for the probe's plain copy of
+    known size; prints the JSON that profiles/c3_decode_traffic.json holds."""
+    import csv
+    import glob
+
+    from common_amd import config as C
+
+    def read(d, counter):
+        rows = []
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                rows += [r for r in csv.DictReader(f) if r.get("Counter_Name") == counter]
+        return rows
+
+    out = {"classes": {}}
+    cfg = C.C3_0_6B
+    pos_mean = C.C3_PROMPT + (TRAFFIC_STEPS - 1) / 2
+    for counter, d, key in (("FETCH_SIZE", fetch_dir, "fetch"), ("WRITE_SIZE", write_dir, "write")):
+        rows = read(d, counter)
+        copy = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        if not copy:
+            raise SystemExit(f"no copy dispatch in {d}")
+        scale = (256 << 20) / (max(copy) * 1024.0)  # counter KiB -> bytes, calibrated on the copy
+        out[f"{key}_scale"] = round(scale, 4)
+        for name, prefix in C3_CLASS_KERNELS.items():
+            vals = [float(r["Counter_Value"]) * 1024.0 * scale for r in rows if prefix in r["Kernel_Name"]]
+            if vals:
+                e = out["classes"].setdefault(name, {"kernel": prefix})
+                e[f"{key}_bytes_per_launch"] = round(sum(vals) / len(vals))
+                e["launches"] = len(vals)
+    for name, e in out["classes"].items():
+        alg = c3_class_bytes(cfg, name, pos_mean)
+        e["hbm_bytes_per_launch"] = e.get("fetch_bytes_per_launch", 0) + e.get("write_bytes_per_launch", 0)
+        e["algorithmic_bytes_per_launch"] = round(alg) if alg else None
+        e["traffic_over_algorithmic"] = round(e["hbm_bytes_per_launch"] / alg, 4) if alg else None
+    print(json.dumps(out, indent=1), flush=True)
 
 
 def load_traffic():
-    """roofline.traffic from the committed rocprofv3 counter summary, when present."""
-    path = os.path.join(ROOT, "profiles", "logits_gemv_traffic.json")
+    """Per-class HBM traffic from the committed rocprofv3 counter summary, when present."""
+    path = os.path.join(ROOT, "profiles", "c3_decode_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)
+            return json.load(f).get("classes", {})
     except (OSError, ValueError):
-        return None
+        return {}
 
 
 def llama2_section(args):
@@ -380,6 +452,8 @@ def main():
                     help="comma list of workloads to run (c3 is the headline; the others are extra fields)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload of the rocprofv3 FETCH_SIZE / WRITE_SIZE passes and exit")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise the two counter passes' CSV output directories per decode class and exit")
     ap.add_argument("--prefetch", type=int, default=0,
                     help="blocks of the Infinity-Cache weight prefetch branch (0 disables)")
     args = ap.parse_args()
@@ -389,6 +463,9 @@ def main():
         sys.exit(2)
     if args.traffic_probe:
         traffic_probe(args)
+        return
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
         return
     sections = {x.strip() for x in args.sections.split(",") if x.strip()}
     if "c3" not in sections:  # profiling aid: only the named extra sections, one JSON line of them
@@ -425,11 +502,29 @@ def main():
     am.reset()
     am.set_prompt(prompt)
 
-    # prompt through the decode path (token by token, as AutoregressiveModel feeds it)
+    # prompt token by token through the decode step (as AutoregressiveModel feeds it), timed once
     model.ctx.synchronize()
     tp = time.perf_counter()
-    fed_prompt = am.run(n_prompt)
-    prefill_s = time.perf_counter() - tp
+    am.run(n_prompt)
+    by_steps_s = time.perf_counter() - tp
+    # the same prompt as one batched prefill (fp32 MFMA GEMMs + fp32 causal attention), best of 3;
+    # the last one leaves the model at position n_prompt for the timed decode
+    pre_times = []
+    for _ in range(3):
+        am.reset()
+        am.set_prompt(prompt)
+        model.ctx.synchronize()
+        tp = time.perf_counter()
+        am.prefill()
+        pre_times.append(time.perf_counter() - tp)
+    assert am.prefill_by_steps() == 0, "the C3 prompt must take the batched fp32 path"
+    prefill_s = min(pre_times)
+    pre_flops = prefill_flops(cfg, n_prompt)
+    log(f"[bench] C3 prompt {n_prompt} tokens: batched fp32 prefill {1000 * prefill_s:.2f} ms = "
+        f"{n_prompt / prefill_s:.0f} tok/s ({pre_flops / prefill_s / 1e12:.1f} TFLOP/s, "
+        f"{100 * pre_flops / prefill_s / 1e12 / MFMA_F32_PEAK_TFLOPS:.1f}% of the fp32 MFMA peak); "
+        f"token by token {n_prompt / by_steps_s:.0f} tok/s")
+    fed_prompt = np.asarray(prompt, np.int32)[None, :]
     warm = am.run(args.warmup) if args.warmup else np.zeros((1, 0), np.int32)
 
     # ---- timed region ----------------------------------------------------------------
@@ -446,7 +541,9 @@ def main():
     log(f"[bench] decode {args.steps} tokens: {ms:.3f} ms/token, {tok_s:.1f} tok/s, "
         f"{e2e_gbs:.0f} GB/s algorithmic ({100 * e2e_gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
 
-    # ---- per-kernel probe: HIP events around each launch of one kernel class ----------
+    # ---- per-kernel probe: events inside the dispatches of one kernel class -------------
+    # (hipExtLaunchKernel records the class's start / stop events as part of its kernels' dispatches,
+    # so each interval is kernel execution, as rocprofv3's kernel trace measures it)
     kernels = {}
     names = {q.KT_LOGITS: "logits_gemv_argmax", q.KT_GATE_UP: "gate_up_gemv_swiglu", q.KT_QKV: "qkv_gemv_rmsnorm",
              q.KT_DOWN: "down_gemv_residual", q.KT_O: "o_gemv_residual", q.KT_ATTENTION: "attention_decode"}
@@ -462,24 +559,31 @@ def main():
         am.kernel_timing(q.KT_NONE)
         avg_us = 1000.0 * ms_k / max(n_k, 1)
         per_tok_us = 1000.0 * ms_k / per_class
-        b = kernel_bytes(cfg, which)
+        probe_pos = pos0 + args.steps + len(kernels) * per_class + (per_class - 1) / 2
+        b = c3_class_bytes(cfg, name, probe_pos)
         kernels[name] = {"avg_us": round(avg_us, 3), "launches": n_k, "us_per_token": round(per_tok_us, 2),
-                         "bytes_per_launch": b, "GBs": round(b / avg_us / 1e3, 1) if b else None}
+                         "bytes_per_launch": round(b) if b else None, "GBs": round(b / avg_us / 1e3, 1) if b else None,
+                         "hbm_frac": round(b / avg_us / 1e3 / HBM_PEAK_GBS, 4) if b else None,
+                         "share_of_step": round(per_tok_us / (1000.0 * ms), 4)}
         log(f"[bench] {name}: {avg_us:.2f} us/launch x {n_k // per_class}/token"
             + (f" = {b / avg_us / 1e3:.0f} GB/s" if b else ""))
-    # The roofline kernel is the largest single launch (the logits GEMV, 622 MB): HIP events around
-    # a launch add a few µs of their own, which only a long kernel makes negligible, so this is the
-    # kernel whose event timing agrees with the rocprofv3 duration.  Every class is in "kernels".
-    dom = "logits_gemv_argmax" if "logits_gemv_argmax" in kernels else None
-    roofline = None
-    if dom:
-        kd = kernels[dom]
-        tr = load_traffic()
-        roofline = {"bound": "hbm", "kernel": dom, "achieved": kd["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4),
-                    "traffic": tr.get("hbm_bytes_per_launch") if tr else None,
-                    "traffic_source": "profiles/logits_gemv_traffic.md" if tr else None,
-                    "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": kd["avg_us"]}
+    # The roofline kernel is the weight-streaming class with the largest share of the step (gate/up
+    # SwiGLU GEMV at C3); the logits GEMV (the largest single launch) rides along as roofline_logits.
+    # The attention class is latency-bound (~1 MB of K/V per layer at C3), not an HBM roofline kernel.
+    traffic = load_traffic()
+
+    def roof(name):
+        kd = kernels[name]
+        tr = traffic.get(name, {})
+        return {"bound": "hbm", "kernel": name, "achieved": kd["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr.get("hbm_bytes_per_launch"),
+                "traffic_source": "profiles/c3_decode_traffic.md" if tr else None,
+                "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": kd["avg_us"],
+                "share_of_step": kd["share_of_step"]}
+
+    gemv_classes = [k for k in kernels if k != "attention_decode" and kernels[k]["GBs"]]
+    roofline = roof(max(gemv_classes, key=lambda k: kernels[k]["us_per_token"])) if gemv_classes else None
+    roofline_logits = roof("logits_gemv_argmax") if "logits_gemv_argmax" in kernels else None
 
     # ---- the same decode with on-device sampling instead of greedy selection ----------------
     sampled = {}
@@ -547,13 +651,18 @@ def main():
         "hbm": {"algorithmic_bytes_per_token": round(mean_bytes), "achieved_GBs": round(e2e_gbs, 1),
                 "frac_of_peak": round(e2e_gbs / HBM_PEAK_GBS, 4)},
         "sampled_c3": sampled,
-        "prompt_c3": {"tok_s": round(n_prompt / prefill_s, 1), "tokens": n_prompt,
-                      "path": "fp32 weights: token by token through the decode step (reference semantics)"},
+        "prompt_c3": {"tokens": n_prompt, "tok_s": round(n_prompt / prefill_s, 1), "ms": round(1000 * prefill_s, 3),
+                      "tflop": round(pre_flops / 1e12, 4),
+                      "achieved_tflops": round(pre_flops / prefill_s / 1e12, 2),
+                      "mfma_f32_frac": round(pre_flops / prefill_s / 1e12 / MFMA_F32_PEAK_TFLOPS, 4),
+                      "path": "batched prefill: fp32 MFMA GEMMs (v_mfma_f32_32x32x2_f32) + fp32 causal attention",
+                      "by_steps_tok_s": round(n_prompt / by_steps_s, 1)},
         "c4": c4_section(args) if "c4" in sections and not args.no_c4 else None,
         "c5": c5_section(args) if "c5" in sections and not args.no_c5 else None,
         "c2": c2_section(args) if "c2" in sections and not args.no_c2 else None,
         "llama2": llama2_section(args) if "llama2" in sections and not args.no_llama2 else None,
         "roofline": roofline,
+        "roofline_logits": roofline_logits,
         "kernels": kernels,
         "cpu_baseline": cpu,
         "parity": parity,

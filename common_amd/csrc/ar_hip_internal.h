@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
+#include <hip/hip_ext.h>
 
 #include <atomic>
 #include <cstddef>
@@ -84,6 +85,29 @@ constexpr int kMaxDevices = 64;
 int ar_device_slot(hipStream_t stream);
 // Compute units of the device of `stream` (cached per device; 256 if it cannot be read).
 int ar_device_cus(hipStream_t stream);
+
+// ---- kernel timing hook ------------------------------------------------------------
+// While a LaunchTiming is installed on the calling thread, the decode launchers that go through
+// ar_launch (the GEMVs, the decode attention and its combine) put `start` into the dispatch of the
+// first kernel they launch and `stop` into every dispatch after it (hipExtLaunchKernel records the
+// events as part of the dispatch), so stop - start spans the class's kernels' execution, as a
+// profiler's kernel trace measures it, without the enqueue gaps around them.  Eager launches only.
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool started = false;
+};
+extern thread_local LaunchTiming* g_launch_timing;
+
+template <typename... Args, typename F = void (*)(Args...)>
+inline void ar_launch(F kernel, const dim3& grid, const dim3& block, uint32_t shmem, hipStream_t stream, Args... args) {
+    LaunchTiming* t = g_launch_timing;
+    if (!t) {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...);
+        return;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, t->started ? nullptr : t->start, t->stop, 0u, args...);
+    t->started = true;
+}
 
 // ---- kernel launchers (device pointers, enqueue on `stream`) ----------------------
 struct GemvLaunch {
@@ -179,6 +203,22 @@ struct GemmLaunch {
 };
 int launch_gemm(const GemmLaunch& a, hipStream_t stream);
 
+// fp32 prefill GEMM on MFMA (gemm_f32.hip): C[M x N] = A[M x K] . W[N x K]^T, all fp32.  Epilogues as
+// GemmLaunch (SwiGLU writes fp32 C).  N % 64 == 0, K % (32 * ksplit) == 0.
+struct GemmF32Launch {
+    const float* A = nullptr;
+    const float* W = nullptr;
+    const float* W2 = nullptr;
+    const float* bias = nullptr;
+    float* C = nullptr;
+    int M = 0, N = 0, K = 0, lda = 0, ldw = 0, ldc = 0;
+    int epilogue = GEMV_EPI_STORE;
+    int ksplit = 1;  // > 1 (store epilogue): k-slice s goes to C + s*M*ldc, added up by the consumer
+};
+int launch_gemm_f32(const GemmF32Launch& a, hipStream_t stream);
+// k-slices for an fp32 prefill product whose 32 x 64 tiles would not give every CU two blocks.
+int gemm_f32_ksplit(int M, int N, int K, int cus);
+
 // ---- prefill (prefill.hip) ---------------------------------------------------------
 // x[r] = E[tokens[b][t]] for r = b*T + t.
 int launch_embed_rows(const void* table, int wdtype, int dim, const int* tokens, int token_stride, int T, int rows,
@@ -211,8 +251,19 @@ struct PrefillPrep {
     uint16_t* vt16 = nullptr;  // [B][KV][hd][Tp] fp16 values, transposed
     int Tp = 0;                // rows reserved per (sequence, KV head), multiple of 64
     int* range_flag = nullptr; // set when a value stored as fp16 overflows (f16_range_check)
+    float* q32 = nullptr;      // fp32-weight prefill: queries go here as fp32 [R][heads*hd] (no fp16
+                               // q / K / Vᵀ copies are written; qb, k16, vt16 unused)
 };
 int launch_qk_prep(const PrefillPrep& a, hipStream_t stream);
+// x[r] += sum_s parts[s][r] (s in order; nparts may be 0), then out[r] = fp32 RMSNorm(x[r]) (the
+// fp32-weight prefill's GEMM input).
+int launch_fold_rmsnorm_rows_f32(float* x, const float* parts, int nparts, const float* w, float* out, int rows,
+                                 int n, float eps, hipStream_t stream);
+// Causal attention of the prompt rows of an fp32-weight prefill (attention.hip): row t of sequence b
+// attends cache rows 0..p0+t; q32 [B*T][heads*hd] normalised rotated queries, fp32 caches
+// [B][KV][S][hd] holding the prompt rows, out [B*T][heads*hd] fp32.
+int launch_attention_prefill_f32(const float* q32, const float* kcache, const float* vcache, float* out, int B, int T,
+                                 int p0, int S, int heads, int kv_heads, int hd, hipStream_t stream);
 // Causal attention over prompt rows 0..T-1 (prefill from position 0), fp16 MFMAs, fp16 output.
 int launch_flash_prefill(const uint16_t* qb, const uint16_t* k16, const uint16_t* vt16, uint16_t* out, int B, int T,
                          int Tp, int heads, int kv_heads, int hd, hipStream_t stream);

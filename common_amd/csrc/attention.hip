@@ -556,8 +556,8 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
         // whole context in one block
         constexpr int NT = 512;
         const dim3 grid(1, a.kv_heads, a.batch);
-        if (p.rope_tab) hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, true, 4>), grid, dim3(NT), 0, stream, p);
-        else hipLaunchKernelGGL((attn_decode_kernel<HD, G, NT, KV16, false, 4>), grid, dim3(NT), 0, stream, p);
+        if (p.rope_tab) ar_launch((attn_decode_kernel<HD, G, NT, KV16, true, 4>), grid, dim3(NT), 0, stream, p);
+        else ar_launch((attn_decode_kernel<HD, G, NT, KV16, false, 4>), grid, dim3(NT), 0, stream, p);
         AR_LAUNCH_CHECK();
         return AR_HIP_OK;
     }
@@ -574,16 +574,16 @@ int launch_t(const AttnLaunch& a, hipStream_t stream) {
     }
     constexpr int NGR = kThreads / 16;
     if (p.rope_tab && longest <= NGR)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true, 1>), grid, dim3(kThreads), 0, stream, p);
+        ar_launch((attn_decode_kernel<HD, G, kThreads, KV16, true, 1>), grid, dim3(kThreads), 0, stream, p);
     else if (p.rope_tab && longest <= 2 * NGR)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true, 2>), grid, dim3(kThreads), 0, stream, p);
+        ar_launch((attn_decode_kernel<HD, G, kThreads, KV16, true, 2>), grid, dim3(kThreads), 0, stream, p);
     else if (p.rope_tab)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, true, 4>), grid, dim3(kThreads), 0, stream, p);
+        ar_launch((attn_decode_kernel<HD, G, kThreads, KV16, true, 4>), grid, dim3(kThreads), 0, stream, p);
     else
-        hipLaunchKernelGGL((attn_decode_kernel<HD, G, kThreads, KV16, false, 4>), grid, dim3(kThreads), 0, stream, p);
+        ar_launch((attn_decode_kernel<HD, G, kThreads, KV16, false, 4>), grid, dim3(kThreads), 0, stream, p);
     AR_LAUNCH_CHECK();
     if (a.max_splits > 1) {
-        hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.heads, a.batch), dim3(HD), 0, stream, p);
+        ar_launch((attn_combine_kernel<HD>), dim3(a.heads, a.batch), dim3(HD), 0, stream, p);
         AR_LAUNCH_CHECK();
     }
     return AR_HIP_OK;
@@ -601,7 +601,159 @@ int pick_g(const AttnLaunch& a, hipStream_t s) {
     return AR_HIP_ERR_INVALID;
 }
 
+// Causal attention of prompt rows in fp32, the attention of the fp32-weight prefill: row t of
+// sequence b (block (b*T + t, g)) attends cache rows 0..p0+t of KV head g for the G query heads of
+// the group, with the decode kernel's arithmetic (queries pre-scaled by log2(e)/sqrt(hd), online
+// softmax in base 2, 16-lane groups each streaming every 16th row, group states merged by lane swaps
+// and through LDS).  The cache rows of the prompt are written beforehand (qk_prep), so every row
+// reads finished rows only.  q32: [B*T][heads*hd] normalised, rotated queries; caches fp32
+// [B][KV][S][hd]; out: [B*T][heads*hd].
+template <int HD, int G>
+__global__ __launch_bounds__(256) void attn_prefill_f32_kernel(const float* q32, const float* kcache,
+                                                                const float* vcache, float* out, int T, int p0,
+                                                                int S, int heads, int kv_heads) {
+    constexpr int EPL = HD / 16, NGR = 16, NWV = 4;
+    __shared__ __attribute__((aligned(16))) float red_acc[NWV][G][HD];
+    __shared__ float red_m[NWV][G], red_l[NWV][G];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = tid >> 4, gl = tid & 15;
+    const int r = blockIdx.x, g = blockIdx.y, b = r / T, t = r - b * T, n = p0 + t + 1;
+    const size_t head = ((size_t)b * kv_heads + g) * (size_t)S * HD;
+    const float* kc = kcache + head;
+    const float* vc = vcache + head;
+    auto dim_of = [&](int e) { return 16 * (e & ~3) + gl * 4 + (e & 3); };
+    const float c2 = 1.4426950408889634f / sqrtf((float)HD);
+    float qf[G][EPL];
+#pragma unroll
+    for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(q32 + (size_t)r * heads * HD + (size_t)(g * G + h) * HD +
+                                                              16 * e + gl * 4);
+            qf[h][e] = v.x * c2; qf[h][e + 1] = v.y * c2; qf[h][e + 2] = v.z * c2; qf[h][e + 3] = v.w * c2;
+        }
+    float m[G], l[G], acc[G][EPL];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) acc[h][e] = 0.f;
+    }
+    auto load_row = [&](float (&dst)[EPL], const float* src, int row) {
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(src + (size_t)row * HD + 16 * e + gl * 4);
+            dst[e] = v.x; dst[e + 1] = v.y; dst[e + 2] = v.z; dst[e + 3] = v.w;
+        }
+    };
+    float kr[EPL], vr[EPL];
+    int row = grp;
+    if (row < n) {
+        load_row(kr, kc, row);
+        load_row(vr, vc, row);
+    }
+    for (; row < n; row += NGR) {
+        float kn[EPL], vn[EPL];
+        const bool more = row + NGR < n;
+        if (more) {  // the group's next row, in flight while this one is used
+            load_row(kn, kc, row + NGR);
+            load_row(vn, vc, row + NGR);
+        }
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) d = fmaf(qf[h][e], kr[e], d);
+            d = row16_sum(d);
+            const float mn = fmaxf(m[h], d);
+            const float alpha = (m[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
+            const float pj = __builtin_amdgcn_exp2f(d - mn);
+            l[h] = l[h] * alpha + pj;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[h][e] = fmaf(pj, vr[e], acc[h][e] * alpha);
+            m[h] = mn;
+        }
+        if (more) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                kr[e] = kn[e];
+                vr[e] = vn[e];
+            }
+        }
+    }
+    auto merge_with = [&](auto partner) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float mo = partner(m[h]), lo = partner(l[h]);
+            const float mn = fmaxf(m[h], mo);
+            const float a = (m[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
+            const float bo = (mo == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mo - mn);
+            l[h] = l[h] * a + lo * bo;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[h][e] = acc[h][e] * a + partner(acc[h][e]) * bo;
+            m[h] = mn;
+        }
+    };
+    merge_with([&](float v) { return xor16(v, lane); });
+    merge_with([&](float v) { return xor32(v, lane); });
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) red_acc[wave][h][dim_of(e)] = acc[h][e];
+            if (lane == 0) {
+                red_m[wave][h] = m[h];
+                red_l[wave][h] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += 256) {
+        const int h = idx / HD, i = idx - h * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NWV; w++) M = fmaxf(M, red_m[w][h]);
+        float L = 0.f, o = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWV; w++) {
+            const float wt = (red_m[w][h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(red_m[w][h] - M);
+            L = fmaf(red_l[w][h], wt, L);
+            o = fmaf(red_acc[w][h][i], wt, o);
+        }
+        out[(size_t)r * heads * HD + (size_t)(g * G + h) * HD + i] = o / L;
+    }
+}
+
+template <int HD>
+int launch_prefill_f32_hd(const float* q32, const float* kc, const float* vc, float* out, int B, int T, int p0, int S,
+                          int heads, int kv_heads, hipStream_t st) {
+    const dim3 grid(B * T, kv_heads);
+    switch (heads / kv_heads) {
+        case 1: hipLaunchKernelGGL((attn_prefill_f32_kernel<HD, 1>), grid, dim3(256), 0, st, q32, kc, vc, out, T, p0, S, heads, kv_heads); break;
+        case 2: hipLaunchKernelGGL((attn_prefill_f32_kernel<HD, 2>), grid, dim3(256), 0, st, q32, kc, vc, out, T, p0, S, heads, kv_heads); break;
+        case 4: hipLaunchKernelGGL((attn_prefill_f32_kernel<HD, 4>), grid, dim3(256), 0, st, q32, kc, vc, out, T, p0, S, heads, kv_heads); break;
+        case 8: hipLaunchKernelGGL((attn_prefill_f32_kernel<HD, 8>), grid, dim3(256), 0, st, q32, kc, vc, out, T, p0, S, heads, kv_heads); break;
+        default:
+            ar_set_error("prefill attention: heads/kv_heads = %d not in {1,2,4,8}", heads / kv_heads);
+            return AR_HIP_ERR_INVALID;
+    }
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
 }  // namespace
+
+int launch_attention_prefill_f32(const float* q32, const float* kcache, const float* vcache, float* out, int B, int T,
+                                 int p0, int S, int heads, int kv_heads, int hd, hipStream_t stream) {
+    AR_CHECK_ARG(q32 && kcache && vcache && out && B > 0 && T > 0, "prefill attention: bad arguments");
+    AR_CHECK_ARG(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "prefill attention: bad head counts");
+    AR_CHECK_ARG(p0 >= 0 && p0 + T <= S, "prefill attention: rows %d..%d outside the %d-row cache", p0, p0 + T, S);
+    AR_CHECK_ARG((long long)B * T <= 0x7fffffffLL && kv_heads <= 65535, "prefill attention: grid too large");
+    if (hd == 128) return launch_prefill_f32_hd<128>(q32, kcache, vcache, out, B, T, p0, S, heads, kv_heads, stream);
+    if (hd == 64) return launch_prefill_f32_hd<64>(q32, kcache, vcache, out, B, T, p0, S, heads, kv_heads, stream);
+    ar_set_error("prefill attention: head_dim %d not supported (64, 128)", hd);
+    return AR_HIP_ERR_INVALID;
+}
 
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd) {
     return (size_t)batch * heads * max_splits * (size_t)hd;

@@ -157,7 +157,7 @@ int launch_nch(const Params& p, hipStream_t st) {
         if (slot >= 0) grid_cache[slot].store(grid, std::memory_order_relaxed);
     }
     const int g = std::min(grid, (p.rows + kAmWaves * RPW - 1) / (kAmWaves * RPW));
-    hipLaunchKernelGGL((gemv_argmax_kernel<WT, NB, RPW, NCH>), dim3(g), dim3(kAmThreads), 0, st, p);
+    ar_launch((gemv_argmax_kernel<WT, NB, RPW, NCH>), dim3(g), dim3(kAmThreads), 0, st, p);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -213,10 +213,10 @@ int launch_nb(const Params& p, int epi, hipStream_t st) {
     const int rb = (64 / NB) / (epi == GEMV_EPI_SWIGLU ? 2 : 1);
     const dim3 grid((p.rows + rb - 1) / rb), block(threads);
     switch (epi) {
-        case GEMV_EPI_STORE: hipLaunchKernelGGL((gemv_batched_kernel<WT, NB, GEMV_EPI_STORE>), grid, block, 0, st, p, passes); break;
-        case GEMV_EPI_RESIDUAL: hipLaunchKernelGGL((gemv_batched_kernel<WT, NB, GEMV_EPI_RESIDUAL>), grid, block, 0, st, p, passes); break;
-        case GEMV_EPI_SWIGLU: hipLaunchKernelGGL((gemv_batched_kernel<WT, NB, GEMV_EPI_SWIGLU>), grid, block, 0, st, p, passes); break;
-        case GEMV_EPI_ARGMAX: hipLaunchKernelGGL((gemv_batched_kernel<WT, NB, GEMV_EPI_ARGMAX>), grid, block, 0, st, p, passes); break;
+        case GEMV_EPI_STORE: ar_launch((gemv_batched_kernel<WT, NB, GEMV_EPI_STORE>), grid, block, 0, st, p, passes); break;
+        case GEMV_EPI_RESIDUAL: ar_launch((gemv_batched_kernel<WT, NB, GEMV_EPI_RESIDUAL>), grid, block, 0, st, p, passes); break;
+        case GEMV_EPI_SWIGLU: ar_launch((gemv_batched_kernel<WT, NB, GEMV_EPI_SWIGLU>), grid, block, 0, st, p, passes); break;
+        case GEMV_EPI_ARGMAX: ar_launch((gemv_batched_kernel<WT, NB, GEMV_EPI_ARGMAX>), grid, block, 0, st, p, passes); break;
         default: ar_set_error("GEMV: unknown epilogue %d", epi); return AR_HIP_ERR_INVALID;
     }
     AR_LAUNCH_CHECK();

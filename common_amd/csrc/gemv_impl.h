@@ -426,7 +426,7 @@ inline int grid_for(const Shape& s, int rows) {
 
 template <typename WT, int NB, int RPW, int UNR, int EPI>
 int launch_t(const Params& p, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_kernel<WT, NB, RPW, UNR, EPI>), dim3(grid), dim3(kThreads), 0, stream, p);
+    ar_launch((gemv_kernel<WT, NB, RPW, UNR, EPI>), dim3(grid), dim3(kThreads), 0, stream, p);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

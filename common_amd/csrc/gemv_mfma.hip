@@ -394,13 +394,13 @@ int launch_epi(const gemv::Params& p, hipStream_t st) {
     if (kpw_p <= ks_max && tiles >= persist) {
         const dim3 grid(std::min(tiles, persist)), block(64 * kPersistWaves);
         if (kpw_p <= 4)
-            hipLaunchKernelGGL((gemv_mfma_persist_kernel<EPI, 4>), grid, block, 0, st, p, kpw_p, tiles);
+            ar_launch((gemv_mfma_persist_kernel<EPI, 4>), grid, block, 0, st, p, kpw_p, tiles);
         else if (kpw_p <= 8)
-            hipLaunchKernelGGL((gemv_mfma_persist_kernel<EPI, 8>), grid, block, 0, st, p, kpw_p, tiles);
+            ar_launch((gemv_mfma_persist_kernel<EPI, 8>), grid, block, 0, st, p, kpw_p, tiles);
         else if (kpw_p <= 12)
-            hipLaunchKernelGGL((gemv_mfma_persist_kernel<EPI, 12>), grid, block, 0, st, p, kpw_p, tiles);
+            ar_launch((gemv_mfma_persist_kernel<EPI, 12>), grid, block, 0, st, p, kpw_p, tiles);
         else
-            hipLaunchKernelGGL((gemv_mfma_persist_kernel<EPI, (NMAT == 2 ? 12 : 16)>), grid, block, 0, st, p, kpw_p,
+            ar_launch((gemv_mfma_persist_kernel<EPI, (NMAT == 2 ? 12 : 16)>), grid, block, 0, st, p, kpw_p,
                                tiles);
     } else {
         // fewer tiles than CUs and nothing that needs the whole row in one block: split k over
@@ -413,10 +413,10 @@ int launch_epi(const gemv::Params& p, hipStream_t st) {
         }
         if (ks > 1) {
             const int per = (nsteps + ks - 1) / ks, kpw = (per + 7) / 8;
-            hipLaunchKernelGGL((gemv_mfma_stream_kernel<EPI, 8>), dim3(tiles * ks), dim3(64 * 8), 0, st, p, kpw, ks);
+            ar_launch((gemv_mfma_stream_kernel<EPI, 8>), dim3(tiles * ks), dim3(64 * 8), 0, st, p, kpw, ks);
         } else {
             const int kpw = (nsteps + kStreamWaves - 1) / kStreamWaves;
-            hipLaunchKernelGGL((gemv_mfma_stream_kernel<EPI, kStreamWaves>), dim3(tiles), dim3(64 * kStreamWaves), 0, st,
+            ar_launch((gemv_mfma_stream_kernel<EPI, kStreamWaves>), dim3(tiles), dim3(64 * kStreamWaves), 0, st,
                                p, kpw, 1);
         }
     }

@@ -139,11 +139,11 @@ int launch_nch(const Params& p, int epi, int nch, hipStream_t st) {
     const int rw = (epi == GEMV_EPI_SWIGLU) ? NR / 2 : NR;
     const dim3 grid((p.rows + kRxWaves * rw - 1) / (kRxWaves * rw)), block(kRxWaves * 64);
     switch (epi) {
-        case GEMV_EPI_STORE: hipLaunchKernelGGL((gemv_rx_kernel<WT, NR, NCH, GEMV_EPI_STORE>), grid, block, 0, st, p, nch); break;
-        case GEMV_EPI_RESIDUAL: hipLaunchKernelGGL((gemv_rx_kernel<WT, NR, NCH, GEMV_EPI_RESIDUAL>), grid, block, 0, st, p, nch); break;
+        case GEMV_EPI_STORE: ar_launch((gemv_rx_kernel<WT, NR, NCH, GEMV_EPI_STORE>), grid, block, 0, st, p, nch); break;
+        case GEMV_EPI_RESIDUAL: ar_launch((gemv_rx_kernel<WT, NR, NCH, GEMV_EPI_RESIDUAL>), grid, block, 0, st, p, nch); break;
         case GEMV_EPI_SWIGLU:
             if constexpr (NR % 2 == 0) {
-                hipLaunchKernelGGL((gemv_rx_kernel<WT, NR, NCH, GEMV_EPI_SWIGLU>), grid, block, 0, st, p, nch);
+                ar_launch((gemv_rx_kernel<WT, NR, NCH, GEMV_EPI_SWIGLU>), grid, block, 0, st, p, nch);
                 break;
             }
             ar_set_error("register-input GEMV: SwiGLU needs a row pair per wavefront");

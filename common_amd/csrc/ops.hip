@@ -185,3 +185,17 @@ extern "C" int ar_hip_gemm_bf16(ar_hip_ctx* ctx, const uint16_t* A, const uint16
     }
     return launch_gemm(g, ctx->stream);
 }
+
+extern "C" int ar_hip_gemm_f32(ar_hip_ctx* ctx, const float* A, const float* W, const float* W2, const float* bias,
+                               float* C, int M, int N, int K, int epilogue) {
+    AR_CHECK_ARG(ctx, "ctx is null");
+    GemmF32Launch g;
+    g.A = A; g.W = W; g.W2 = W2; g.bias = bias; g.C = C; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldw = K; g.ldc = N;
+    switch (epilogue) {
+        case AR_GEMM_STORE: g.epilogue = GEMV_EPI_STORE; break;
+        case AR_GEMM_RESIDUAL: g.epilogue = GEMV_EPI_RESIDUAL; break;
+        case AR_GEMM_SWIGLU: g.epilogue = GEMV_EPI_SWIGLU; break;
+        default: AR_CHECK_ARG(false, "GEMM f32: unknown epilogue %d", epilogue);
+    }
+    return launch_gemm_f32(g, ctx->stream);
+}

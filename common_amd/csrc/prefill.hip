@@ -85,6 +85,24 @@ __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_kernel(float* x, co
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = f2h((w[i] * xr[i]) * r, rf);
 }
 
+// The fold + row RMSNorm above with an fp32 output row (the fp32-weight prefill's GEMM input).
+__global__ __launch_bounds__(256) void fold_rmsnorm_rows_f32_kernel(float* x, const float* parts, int nparts,
+                                                                     size_t part_stride, const float* w, float* out,
+                                                                     int n, float eps) {
+    __shared__ float scratch[4];
+    float* xr = x + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = xr[i];
+        for (int s = 0; s < nparts; s++) v += parts[s * part_stride + (size_t)blockIdx.x * n + i];
+        if (nparts) xr[i] = v;
+        ss += v * v;
+    }
+    ss = block_sum(ss, scratch);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[(size_t)blockIdx.x * n + i] = (w[i] * xr[i]) * r;
+}
+
 // dst[b] = src[first + b*step] + sum_s parts[s][first + b*step], rows of n floats.
 __global__ __launch_bounds__(256) void fold_rows_kernel(const float* src, const float* parts, int nparts,
                                                         size_t part_stride, int first, int step, int n, float* dst) {
@@ -112,6 +130,7 @@ struct PrepParams {
     uint16_t* k16;          // [B][KV][Tp][hd] fp16 keys of the prompt rows (for the attention MFMAs)
     int Tp;
     int* rf;                // overflow flag of the fp16 stores (f16_range_check)
+    float* q32;             // fp32-weight prefill: fp32 queries [R][heads*hd], no fp16 q / k16 copies
 };
 
 // One block per prompt row: QK-norm (whole vector or per head), RoPE at position p0 + t, k and v
@@ -154,9 +173,15 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
             x2 = (p.q_norm[(size_t)h * hd + f + fd] * x2) * s;
         }
         const float2 cs = rope[f];
-        uint16_t* qo = p.qb + (size_t)r * q_dim + (size_t)h * hd;
-        qo[f] = f2h(x1 * cs.x - x2 * cs.y, p.rf);
-        qo[f + fd] = f2h(x2 * cs.x + x1 * cs.y, p.rf);
+        if (p.q32) {
+            float* qo = p.q32 + (size_t)r * q_dim + (size_t)h * hd;
+            qo[f] = x1 * cs.x - x2 * cs.y;
+            qo[f + fd] = x2 * cs.x + x1 * cs.y;
+        } else {
+            uint16_t* qo = p.qb + (size_t)r * q_dim + (size_t)h * hd;
+            qo[f] = f2h(x1 * cs.x - x2 * cs.y, p.rf);
+            qo[f + fd] = f2h(x2 * cs.x + x1 * cs.y, p.rf);
+        }
     }
     for (int idx = threadIdx.x; idx < p.kv_heads * fd; idx += blockDim.x) {
         const int g = idx / fd, f = idx - g * fd;
@@ -176,9 +201,11 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(PrepParams p) {
             reinterpret_cast<float*>(p.kcache)[kofs + f] = o1;
             reinterpret_cast<float*>(p.kcache)[kofs + f + fd] = o2;
         }
-        uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
-        k16[f] = f2h(o1, p.rf);
-        k16[f + fd] = f2h(o2, p.rf);
+        if (!p.q32) {
+            uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
+            k16[f] = f2h(o1, p.rf);
+            k16[f + fd] = f2h(o2, p.rf);
+        }
     }
     for (int idx = threadIdx.x; idx < kv_dim; idx += blockDim.x) {
         const int g = idx / hd, i = idx - g * hd;
@@ -315,9 +342,15 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
             const int h = idx / fd4, f = (idx - h * fd4) * 4;
             float o1[4], o2[4];
             rotate(q1[j], q2[j], p.q_norm, (size_t)h * hd, rq, f, o1, o2);
-            uint16_t* qo = p.qb + (size_t)r * q_dim + (size_t)h * hd;
-            *reinterpret_cast<uint2*>(qo + f) = pack4h(o1[0], o1[1], o1[2], o1[3], p.rf);
-            *reinterpret_cast<uint2*>(qo + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3], p.rf);
+            if (p.q32) {
+                float* qo = p.q32 + (size_t)r * q_dim + (size_t)h * hd;
+                *reinterpret_cast<float4*>(qo + f) = make_float4(o1[0], o1[1], o1[2], o1[3]);
+                *reinterpret_cast<float4*>(qo + fd + f) = make_float4(o2[0], o2[1], o2[2], o2[3]);
+            } else {
+                uint16_t* qo = p.qb + (size_t)r * q_dim + (size_t)h * hd;
+                *reinterpret_cast<uint2*>(qo + f) = pack4h(o1[0], o1[1], o1[2], o1[3], p.rf);
+                *reinterpret_cast<uint2*>(qo + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3], p.rf);
+            }
         }
     }
     if (tid < nk) {
@@ -334,9 +367,11 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
             *reinterpret_cast<float4*>(kc + f) = make_float4(o1[0], o1[1], o1[2], o1[3]);
             *reinterpret_cast<float4*>(kc + fd + f) = make_float4(o2[0], o2[1], o2[2], o2[3]);
         }
-        uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
-        *reinterpret_cast<uint2*>(k16 + f) = pack4h(o1[0], o1[1], o1[2], o1[3], p.rf);
-        *reinterpret_cast<uint2*>(k16 + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3], p.rf);
+        if (!p.q32) {
+            uint16_t* k16 = p.k16 + (((size_t)b * p.kv_heads + g) * p.Tp + t) * hd;
+            *reinterpret_cast<uint2*>(k16 + f) = pack4h(o1[0], o1[1], o1[2], o1[3], p.rf);
+            *reinterpret_cast<uint2*>(k16 + fd + f) = pack4h(o2[0], o2[1], o2[2], o2[3], p.rf);
+        }
     }
     for (int i4 = tid; i4 < kv_dim / 4; i4 += 256) {
         const int g = (4 * i4) / hd, i = 4 * i4 - g * hd;
@@ -628,6 +663,16 @@ int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const
     return AR_HIP_OK;
 }
 
+int launch_fold_rmsnorm_rows_f32(float* x, const float* parts, int nparts, const float* w, float* out, int rows,
+                                 int n, float eps, hipStream_t stream) {
+    AR_CHECK_ARG(x && w && out && rows > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0),
+                 "fold rmsnorm rows: bad arguments");
+    hipLaunchKernelGGL(fold_rmsnorm_rows_f32_kernel, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                       (size_t)rows * n, w, out, n, eps);
+    AR_LAUNCH_CHECK();
+    return AR_HIP_OK;
+}
+
 int launch_fold_rows(const float* src, const float* parts, int nparts, size_t part_rows, int first, int step,
                      int count, int n, float* dst, hipStream_t stream) {
     AR_CHECK_ARG(src && dst && count > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0), "fold rows: bad arguments");
@@ -638,8 +683,10 @@ int launch_fold_rows(const float* src, const float* parts, int nparts, size_t pa
 }
 
 int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
-    AR_CHECK_ARG(a.qkv && a.rope_tab && a.kcache && a.vcache && a.qb && a.k16 && a.vt16, "qk prep: null pointer");
-    AR_CHECK_ARG(a.Tp >= a.T, "qk prep: fp16 copies hold %d rows, %d needed", a.Tp, a.T);
+    AR_CHECK_ARG(a.qkv && a.rope_tab && a.kcache && a.vcache && (a.q32 || (a.qb && a.k16 && a.vt16)),
+                 "qk prep: null pointer");
+    AR_CHECK_ARG(a.q32 || a.Tp >= a.T, "qk prep: fp16 copies hold %d rows, %d needed", a.Tp, a.T);
+    AR_CHECK_ARG(!a.q32 || !a.kv16, "qk prep: the fp32 path keeps an fp32 cache");
     AR_CHECK_ARG(a.heads + a.kv_heads <= 64, "qk prep: too many heads");
     AR_CHECK_ARG(a.p0 >= 0 && a.p0 + a.T <= a.S, "qk prep: rows %d..%d outside the %d-row cache", a.p0, a.p0 + a.T,
                  a.S);
@@ -648,14 +695,15 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     p.per_head = a.per_head; p.rope_tab = a.rope_tab; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.S;
     p.kv16 = a.kv16;
     p.T = a.T; p.p0 = a.p0; p.heads = a.heads; p.kv_heads = a.kv_heads; p.hd = a.hd; p.qb = a.qb;
-    p.k16 = a.k16; p.Tp = a.Tp; p.rf = a.range_flag;
+    p.k16 = a.k16; p.Tp = a.Tp; p.rf = a.range_flag; p.q32 = a.q32;
     const int nq = a.heads * a.hd / 8, nk = a.kv_heads * a.hd / 8;
     const bool v4 = !a.per_head && a.hd % 8 == 0 && a.qkv_stride % 4 == 0 && nk <= 256 && nq <= 4 * 256 &&
                     (reinterpret_cast<uintptr_t>(a.qkv) & 15) == 0 &&
                     (!a.q_norm || (reinterpret_cast<uintptr_t>(a.q_norm) & 15) == 0) &&
                     (!a.k_norm || (reinterpret_cast<uintptr_t>(a.k_norm) & 15) == 0) &&
                     (reinterpret_cast<uintptr_t>(a.rope_tab) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.qb) & 7) == 0 &&
-                    (reinterpret_cast<uintptr_t>(a.k16) & 7) == 0 && (reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.k16) & 7) == 0 && (reinterpret_cast<uintptr_t>(a.q32) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(a.vcache) & 15) == 0;
     if (v4 && nq <= 256)
         hipLaunchKernelGGL(qk_prep_v4_kernel<1>, dim3(a.B * a.T), dim3(256), 0, stream, p);
@@ -666,6 +714,7 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
     else
         hipLaunchKernelGGL(qk_prep_kernel, dim3(a.B * a.T), dim3(256), 0, stream, p);
     AR_LAUNCH_CHECK();
+    if (a.q32) return AR_HIP_OK;  // fp32 path: attention reads the fp32 cache rows directly
     AR_CHECK_ARG(a.Tp % 64 == 0 && a.Tp >= a.T, "qk prep: Vᵀ rows %d not a multiple of 64 covering %d", a.Tp, a.T);
     const dim3 vgrid((a.T + 63) / 64, a.kv_heads, a.B);
 #define AR_VT16(HDV, T_)                                                                                     \

@@ -114,7 +114,8 @@ struct ar_qwen3 {
     // prefill buffers, sized for pf_rows = batch x prompt rows on first use
     size_t pf_rows = 0;
     float* pf_x = nullptr;       // [R][dim] residual stream
-    uint16_t* pf_h = nullptr;    // [R][max(dim, q_dim)] fp16 GEMM input (normalised x / attention out)
+    uint16_t* pf_h = nullptr;    // [R][max(dim, q_dim)] fp16 GEMM input (normalised x / attention out);
+                                 // fp32 for fp32 weights (as are pf_q and pf_act)
     float* pf_qkv = nullptr;     // [R][qkv_dim]
     uint16_t* pf_q = nullptr;    // [R][q_dim] fp16 normalised, rotated queries
     uint16_t* pf_act = nullptr;  // [R][F] fp16 SwiGLU output
@@ -201,6 +202,11 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     const ar_qwen3_cfg& c = m->cfg;
     hipStream_t st = m->ctx->stream;
     const int B = m->B, dim = c.dim, F = c.hidden_dim;
+    // the timed class's kernels carry a start / stop event pair in their dispatches (ar_launch)
+    LaunchTiming timing;
+    struct TimingReset {  // an early error return must not leave the hook pointing at `timing`
+        ~TimingReset() { g_launch_timing = nullptr; }
+    } timing_reset;
     auto timed_begin = [&](int which) -> int {
         if (m->timed != which) return AR_HIP_OK;
         if (m->events_used == m->events.size()) {
@@ -209,12 +215,15 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
             AR_HIP_TRY(hipEventCreate(&b));
             m->events.push_back({a, b});
         }
-        AR_HIP_TRY(hipEventRecord(m->events[m->events_used].first, st));
+        timing.start = m->events[m->events_used].first;
+        timing.stop = m->events[m->events_used].second;
+        timing.started = false;
+        g_launch_timing = &timing;
         return AR_HIP_OK;
     };
     auto timed_end = [&](int which) -> int {
         if (m->timed != which) return AR_HIP_OK;
-        AR_HIP_TRY(hipEventRecord(m->events[m->events_used].second, st));
+        g_launch_timing = nullptr;
         m->events_used++;
         return AR_HIP_OK;
     };
@@ -813,6 +822,16 @@ int ensure_prefill_buffers(ar_qwen3* m, size_t rows) {
     m->pf_rows = 0;
     const ar_qwen3_cfg& c = m->cfg;
     const size_t hw = (size_t)std::max(c.dim, m->q_dim);
+    if (c.weight_dtype == AR_DTYPE_F32) {
+        // fp32 path: GEMM input rows (normalised x / attention output), queries and SwiGLU output in fp32
+        AR_TRY(ar_ctx_alloc(m->ctx, rows * c.dim * 4, (void**)&m->pf_x));
+        AR_TRY(ar_ctx_alloc(m->ctx, rows * hw * 4, (void**)&m->pf_h));
+        AR_TRY(ar_ctx_alloc(m->ctx, rows * m->qkv_dim * 4, (void**)&m->pf_qkv));
+        AR_TRY(ar_ctx_alloc(m->ctx, rows * m->q_dim * 4, (void**)&m->pf_q));
+        AR_TRY(ar_ctx_alloc(m->ctx, rows * c.hidden_dim * 4, (void**)&m->pf_act));
+        m->pf_rows = rows;
+        return AR_HIP_OK;
+    }
     AR_TRY(ar_ctx_alloc(m->ctx, rows * c.dim * 4, (void**)&m->pf_x));
     AR_TRY(ar_ctx_alloc(m->ctx, rows * hw * 2, (void**)&m->pf_h));
     AR_TRY(ar_ctx_alloc(m->ctx, rows * m->qkv_dim * 4, (void**)&m->pf_qkv));
@@ -867,13 +886,118 @@ static int prefill_by_steps(ar_qwen3* m, int T, float* logits_out) {
     return ar_hip_qwen3_next(m, nullptr, logits_out);
 }
 
+// The end of a batched prefill: the last prompt row of every sequence (the residual stream plus the
+// `pending` k-slices of the last residual projection) becomes the decode plan's residual stream, the
+// final RMSNorm + logits GEMV leaves the greedy keys for the next step, and the loop state moves to
+// where prompt_len calls of next() leave it.
+static int prefill_finish(ar_qwen3* m, int T, int pending, float* logits_out) {
+    const ar_qwen3_cfg& c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int B = m->B, d = c.dim;
+    const size_t R = (size_t)B * T;
+    AR_TRY(launch_fold_rows(m->pf_x, m->pf_part, pending, R, T - 1, T, B, d, m->x, st));
+    AR_HIP_TRY(hipMemsetAsync(m->am_keys, 0, (size_t)B * kArgmaxSlots * 8, st));
+    GemvLaunch h;
+    h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
+    const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
+    h.cols = d; h.x = m->x; h.x_stride = d; h.norm_w = m->final_norm;
+    h.y = (logits_out || sampling) ? m->logits : nullptr;
+    h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.keys = m->am_keys;
+    AR_TRY(launch_gemv(h, st));
+    const int state[3] = {T - 1, T, T};
+    AR_HIP_TRY(hipMemcpyAsync(m->state, state, sizeof(state), hipMemcpyHostToDevice, st));
+    if (sampling) AR_TRY(enqueue_sample(m));  // the first generated token
+    if (logits_out)
+        AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)B * c.vocab_size * 4, hipMemcpyDeviceToHost, st));
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    m->host_pos = T;
+    return AR_HIP_OK;
+}
+
+// k-split of an fp32 residual projection (at most kMaxKSplit slices, consumed by the fold kernels)
+static int prefill_f32_ksplit(const ar_qwen3* m, size_t rows, int N, int K) {
+    return std::min(kMaxKSplit, gemm_f32_ksplit((int)rows, N, K, m->ctx->num_cus));
+}
+
+// fp32 weights: the prompt rows as fp32 MFMA GEMMs (gemm_f32.hip) with the decode path's RMSNorm,
+// QK-norm, RoPE and cache write, and fp32 causal attention over the cache rows.
+static int prefill_f32(ar_qwen3* m, int T, float* logits_out) {
+    const ar_qwen3_cfg& c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int B = m->B, d = c.dim, F = c.hidden_dim, qd = m->q_dim;
+    const size_t R = (size_t)B * T;
+    AR_CHECK_ARG(R <= (size_t)INT32_MAX / 16, "prefill: %zu rows too many", R);
+    AR_TRY(ensure_prefill_buffers(m, R));
+    float* const h32 = reinterpret_cast<float*>(m->pf_h);
+    float* const q32 = reinterpret_cast<float*>(m->pf_q);
+    float* const act32 = reinterpret_cast<float*>(m->pf_act);
+    AR_TRY(launch_embed_rows(m->embed, c.weight_dtype, d, m->tokens, m->S + 1, T, (int)R, m->pf_x, st));
+    const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
+    const int so = prefill_f32_ksplit(m, R, d, qd), sd = prefill_f32_ksplit(m, R, d, F);
+    if ((so > 1 || sd > 1) && m->pf_part_rows < R) {
+        if (m->pf_part) AR_TRY(ar_ctx_free(m->ctx, m->pf_part));
+        m->pf_part = nullptr;
+        m->pf_part_rows = 0;
+        AR_TRY(ar_ctx_alloc(m->ctx, (size_t)kMaxKSplit * R * d * 4, (void**)&m->pf_part));
+        m->pf_part_rows = R;
+    }
+    int pending = 0;
+    for (int l = 0; l < c.layer_count; l++) {
+        const Layer& L = m->layers[l];
+        AR_TRY(launch_fold_rmsnorm_rows_f32(m->pf_x, m->pf_part, pending, L.attn_norm, h32, (int)R, d,
+                                            (float)c.epsilon, st));
+        pending = 0;
+        GemmF32Launch g;
+        g.A = h32; g.lda = d; g.W = (const float*)L.wqkv; g.ldw = d; g.M = (int)R; g.N = m->qkv_dim; g.K = d;
+        g.bias = L.bqkv; g.C = m->pf_qkv; g.ldc = m->qkv_dim; g.epilogue = GEMV_EPI_STORE;
+        AR_TRY(launch_gemm_f32(g, st));
+        PrefillPrep pp;
+        pp.qkv = m->pf_qkv; pp.qkv_stride = m->qkv_dim; pp.q_norm = L.q_norm; pp.k_norm = L.k_norm;
+        pp.eps = (float)c.epsilon; pp.per_head = c.qk_norm_mode == AR_QK_NORM_PER_HEAD; pp.rope_tab = m->rope_tab;
+        pp.kcache = (char*)m->kcache + l * layer_cache * m->kv_elem;
+        pp.vcache = (char*)m->vcache + l * layer_cache * m->kv_elem;
+        pp.B = B; pp.S = m->S; pp.T = T; pp.p0 = 0; pp.heads = c.head_count; pp.kv_heads = c.kv_head_count;
+        pp.hd = c.head_size; pp.q32 = q32;
+        AR_TRY(launch_qk_prep(pp, st));
+        AR_TRY(launch_attention_prefill_f32(q32, (const float*)pp.kcache, (const float*)pp.vcache, h32, B, T, 0, m->S,
+                                            c.head_count, c.kv_head_count, c.head_size, st));
+        GemmF32Launch o;
+        o.A = h32; o.lda = qd; o.W = (const float*)L.wo; o.ldw = qd; o.M = (int)R; o.N = d; o.K = qd;
+        o.C = m->pf_x; o.ldc = d; o.epilogue = GEMV_EPI_RESIDUAL;
+        if (so > 1) {  // k-slices into pf_part, added into pf_x by the next row RMSNorm
+            o.C = m->pf_part; o.epilogue = GEMV_EPI_STORE; o.ksplit = so;
+        }
+        AR_TRY(launch_gemm_f32(o, st));
+        AR_TRY(launch_fold_rmsnorm_rows_f32(m->pf_x, m->pf_part, so > 1 ? so : 0, L.ffn_norm, h32, (int)R, d,
+                                            (float)c.epsilon, st));
+        GemmF32Launch u;
+        u.A = h32; u.lda = d; u.W = (const float*)L.w1; u.W2 = (const float*)L.w3; u.ldw = d; u.M = (int)R;
+        u.N = F; u.K = d; u.C = act32; u.ldc = F; u.epilogue = GEMV_EPI_SWIGLU;
+        AR_TRY(launch_gemm_f32(u, st));
+        GemmF32Launch dn;
+        dn.A = act32; dn.lda = F; dn.W = (const float*)L.w2; dn.ldw = F; dn.M = (int)R; dn.N = d; dn.K = F;
+        dn.C = m->pf_x; dn.ldc = d; dn.epilogue = GEMV_EPI_RESIDUAL;
+        if (sd > 1) {
+            dn.C = m->pf_part; dn.epilogue = GEMV_EPI_STORE; dn.ksplit = sd;
+            pending = sd;
+        }
+        AR_TRY(launch_gemm_f32(dn, st));
+    }
+    return prefill_finish(m, T, pending, logits_out);
+}
+
 extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
     AR_CHECK_ARG(m, "null model");
     const int T = m->prompt_len;
     AR_TRY(check_ready(m, T));
     AR_CHECK_ARG(m->host_pos == 0, "prefill starts a sequence: reset() first (position is %d)", m->host_pos);
     const ar_qwen3_cfg& c = m->cfg;
-    if (c.weight_dtype != AR_DTYPE_BF16) return prefill_by_steps(m, T, logits_out);
+    if (c.weight_dtype == AR_DTYPE_F32) {
+        // fp32 MFMA GEMMs need 64-wide outputs and 32-deep inputs; other shapes take the decode step
+        const bool fits = c.dim % 64 == 0 && m->qkv_dim % 64 == 0 && c.hidden_dim % 64 == 0 && m->q_dim % 32 == 0 &&
+                          c.kv_dtype == AR_DTYPE_F32;
+        return fits ? prefill_f32(m, T, logits_out) : prefill_by_steps(m, T, logits_out);
+    }
     hipStream_t st = m->ctx->stream;
     const int B = m->B, d = c.dim, F = c.hidden_dim, qd = m->q_dim;
     const size_t R = (size_t)B * T;
@@ -953,23 +1077,5 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
     AR_HIP_TRY(hipMemcpyAsync(&overflow, m->pf_flag, sizeof(int), hipMemcpyDeviceToHost, st));
     AR_HIP_TRY(hipStreamSynchronize(st));
     if (overflow) return prefill_by_steps(m, T, logits_out);
-    // last prompt row of every sequence -> residual stream of the decode plan, then the final
-    // RMSNorm + logits GEMV leaves the greedy keys for the next step
-    AR_TRY(launch_fold_rows(m->pf_x, m->pf_part, pending, R, T - 1, T, B, d, m->x, st));
-    AR_HIP_TRY(hipMemsetAsync(m->am_keys, 0, (size_t)B * kArgmaxSlots * 8, st));
-    GemvLaunch h;
-    h.wdtype = c.weight_dtype; h.batch = B; h.eps = (float)c.epsilon; h.w = m->lm_head; h.rows = c.vocab_size;
-    const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
-    h.cols = d; h.x = m->x; h.x_stride = d; h.norm_w = m->final_norm;
-    h.y = (logits_out || sampling) ? m->logits : nullptr;
-    h.y_stride = c.vocab_size; h.epilogue = GEMV_EPI_ARGMAX; h.keys = m->am_keys;
-    AR_TRY(launch_gemv(h, st));
-    const int state[3] = {T - 1, T, T};
-    AR_HIP_TRY(hipMemcpyAsync(m->state, state, sizeof(state), hipMemcpyHostToDevice, st));
-    if (sampling) AR_TRY(enqueue_sample(m));  // the first generated token
-    if (logits_out)
-        AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)B * c.vocab_size * 4, hipMemcpyDeviceToHost, st));
-    AR_HIP_TRY(hipStreamSynchronize(st));
-    m->host_pos = T;
-    return AR_HIP_OK;
+    return prefill_finish(m, T, pending, logits_out);
 }

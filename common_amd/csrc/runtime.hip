@@ -14,6 +14,8 @@ namespace {
 thread_local char g_last_error[1024] = "";
 }
 
+thread_local LaunchTiming* g_launch_timing = nullptr;
+
 void ar_set_error(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);

@@ -92,6 +92,7 @@ _SIGS = {
     "ar_hip_qwen3_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_qwen3_prefill_by_steps": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
     "ar_hip_gemm_bf16": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4),
+    "ar_hip_gemm_f32": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4),
     "ar_hip_sample": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_double, ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_qwen3_set_sampling": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_double, ctypes.c_double,
@@ -313,6 +314,11 @@ class HipContext:
                   O: DeviceBuffer | None = None):
         check(lib().ar_hip_gemm_bf16(self.handle, A.ptr, W.ptr, W2.ptr if W2 else None, bias.ptr if bias else None,
                                      C.ptr if C else None, O.ptr if O else None, M, N, K, epilogue))
+
+    def gemm_f32(self, A: DeviceBuffer, W: DeviceBuffer, M: int, N: int, K: int, epilogue: int = GEMM_STORE,
+                 W2: DeviceBuffer | None = None, bias: DeviceBuffer | None = None, C: DeviceBuffer | None = None):
+        check(lib().ar_hip_gemm_f32(self.handle, A.ptr, W.ptr, W2.ptr if W2 else None, bias.ptr if bias else None,
+                                    C.ptr if C else None, M, N, K, epilogue))
 
     def attention_decode(self, q, k, v, q_norm, k_norm, qk_eps, qk_norm_mode, k_cache, v_cache, max_seq, pos,
                          heads, kv_heads, head_dim, theta, out, noalloc: bool = False):

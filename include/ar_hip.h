@@ -158,6 +158,11 @@ int ar_hip_sample(ar_hip_ctx *ctx, const float *logits, int rows, int n, int mod
 #define AR_GEMM_SWIGLU 2
 int ar_hip_gemm_bf16(ar_hip_ctx *ctx, const uint16_t *A, const uint16_t *W, const uint16_t *W2, const float *bias,
                      float *C, uint16_t *O, int M, int N, int K, int epilogue);
+/* The same product with fp32 operands and accumulation on the fp32 MFMA units
+ * (v_mfma_f32_32x32x2_f32), the prompt projections of an fp32-weight model: C (fp32, [M][N]);
+ * AR_GEMM_SWIGLU writes (A.W2^T) * silu(A.W^T) to C in fp32.  N % 64 == 0, K % 32 == 0. */
+int ar_hip_gemm_f32(ar_hip_ctx *ctx, const float *A, const float *W, const float *W2, const float *bias, float *C,
+                    int M, int N, int K, int epilogue);
 
 /* ---- Qwen3 model -------------------------------------------------------------------
  * Replaces Qwen3.model + CompiledModel.forward + AutoregressiveModel
@@ -215,7 +220,9 @@ int ar_hip_qwen3_next(ar_qwen3 *m, int32_t *tokens_out, float *logits_out);
  * loop stays on the device); tokens_out is batch x steps (row-major by sequence). */
 int ar_hip_qwen3_run(ar_qwen3 *m, int steps, int32_t *tokens_out);
 /* Whole-prompt prefill from position 0: the prompt rows of every sequence run together (bf16
- * weights: MFMA GEMMs + causal flash attention; fp32 weights: the decode step per token).  Leaves
+ * weights: fp16 MFMA GEMMs + causal flash attention; fp32 weights: fp32 MFMA GEMMs + fp32 causal
+ * attention, or the decode step per token when dim, the q+k+v rows or the FFN width is not a
+ * multiple of 64).  Leaves
  * the model exactly where prompt_len calls of next() would: position = prompt length, KV cache
  * rows 0..prompt_len-1 written, and the next next() feeds the greedy token of the last prompt
  * row.  logits_out (optional, batch x vocab, host) receives the last prompt row's logits.
