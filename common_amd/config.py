@@ -11,6 +11,7 @@ computation reduces to the reference graph.
 from __future__ import annotations
 
 import dataclasses
+import os
 
 QK_NORM_WHOLE = 0     # one RMS over the whole q / k vector (AttentionFeatures.java:840-845, :886-891)
 QK_NORM_PER_HEAD = 1  # one RMS per head (HF Qwen3 semantics)
@@ -18,6 +19,17 @@ QK_NORM_PER_HEAD = 1  # one RMS per head (HF Qwen3 semantics)
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F16 = 2  # KV-cache storage option (kv_dtype)
+
+
+def default_kv_dtype() -> int:
+    """KV-cache storage of a config that does not name one: AR_HIP_KV_DTYPE = "fp32" (default, the
+    reference keeps its cache at the context precision) or "fp16"."""
+    v = os.environ.get("AR_HIP_KV_DTYPE", "fp32").strip().lower()
+    if v in ("fp32", "f32", "float32", ""):
+        return DTYPE_F32
+    if v in ("fp16", "f16", "float16", "half"):
+        return DTYPE_F16
+    raise ValueError(f"AR_HIP_KV_DTYPE={v!r}: expected fp32 or fp16")
 
 
 @dataclasses.dataclass(frozen=True)
@@ -35,7 +47,8 @@ class Qwen3Config:
     epsilon: float = 1e-6     # Qwen3.java:397,402
     qk_norm_mode: int = QK_NORM_WHOLE
     weight_dtype: int = DTYPE_F32
-    kv_dtype: int = DTYPE_F32  # KV cache storage: DTYPE_F32 (reference) or DTYPE_F16
+    kv_dtype: int = dataclasses.field(default_factory=lambda: default_kv_dtype())
+    # KV cache storage: DTYPE_F32 (reference) or DTYPE_F16; default from AR_HIP_KV_DTYPE
     max_batch: int = 1
     qkv_bias: bool = False
 

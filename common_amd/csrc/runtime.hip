@@ -4,6 +4,7 @@
 // (base/code/src/main/java/io/almostrealism/code/DataContext.java:81-88,
 //  ComputeContext.java:89,133, MemoryProvider.java:60-188) for one GPU.
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <atomic>
 #include <cstring>
@@ -16,11 +17,23 @@ thread_local char g_last_error[1024] = "";
 
 thread_local LaunchTiming* g_launch_timing = nullptr;
 
+// AR_HIP_LOG=1 (read once): every error message set for a caller is also written to stderr, the
+// library's counterpart of the reference's verbose hardware logging flags (SystemUtils.getProperty
+// over AR_* variables, base/io/src/main/java/org/almostrealism/io/SystemUtils.java:180-237).
+static bool log_errors() {
+    static const bool on = [] {
+        const char* v = getenv("AR_HIP_LOG");
+        return v && *v && strcmp(v, "0") != 0 && strcmp(v, "false") != 0;
+    }();
+    return on;
+}
+
 void ar_set_error(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
     va_end(ap);
+    if (log_errors()) fprintf(stderr, "[ar_hip] %s\n", g_last_error);
 }
 
 void ar_clear_error() { g_last_error[0] = '\0'; }
@@ -50,6 +63,14 @@ extern "C" int ar_hip_init(int device, ar_hip_ctx** out) {
     if (e != hipSuccess || n == 0) {
         ar_set_error("no HIP device available (%s)", e == hipSuccess ? "0 devices" : hipGetErrorString(e));
         return AR_HIP_ERR_NO_DEVICE;
+    }
+    if (device < 0) {  // the device AR_HIP_DEVICE names (default 0)
+        const char* v = getenv("AR_HIP_DEVICE");
+        char* end = nullptr;
+        const long d = v && *v ? strtol(v, &end, 10) : 0;
+        AR_CHECK_ARG(!v || !*v || (*end == '\0' && d >= 0 && d < n), "AR_HIP_DEVICE='%s' is not a device in [0,%d)",
+                     v ? v : "", n);
+        device = (int)d;
     }
     AR_CHECK_ARG(device >= 0 && device < n, "device %d out of range [0,%d)", device, n);
     AR_HIP_TRY(hipSetDevice(device));

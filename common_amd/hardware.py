@@ -239,9 +239,10 @@ class DeviceBuffer:
 class HipContext:
     """One GPU: data context + compute context (one in-order stream) + memory provider."""
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int | None = None):
+        """device None: the device AR_HIP_DEVICE names (default 0)."""
         h = ctypes.c_void_p()
-        check(lib().ar_hip_init(device, ctypes.byref(h)))
+        check(lib().ar_hip_init(-1 if device is None else device, ctypes.byref(h)))
         self.handle = h.value
         self.device = device
 

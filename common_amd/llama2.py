@@ -169,7 +169,7 @@ class Llama2:
         with Llama2Checkpoint(checkpoint) as ck:
             self.config = dataclasses.replace(ck.config, max_batch=max_batch)
             self.tokenizer = BPE(tokenizer, self.config.vocab_size) if tokenizer is not None else None
-            self.ctx = ctx or hw.HipContext(0)
+            self.ctx = ctx or hw.HipContext()
             self._own_ctx = ctx is None
             h = ctypes.c_void_p()
             try:

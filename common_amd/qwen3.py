@@ -127,7 +127,7 @@ class Qwen3:
     def __init__(self, config: Qwen3Config, state_dict, ctx: hw.HipContext | None = None, tokenizer=None):
         self.config = config
         self.tokenizer = tokenizer  # a common_amd.tokenizer.Qwen3Tokenizer, for run(); optional
-        self.ctx = ctx or hw.HipContext(0)
+        self.ctx = ctx or hw.HipContext()
         self._own_ctx = ctx is None
         h = ctypes.c_void_p()
         cfg = native_cfg(config)

@@ -50,6 +50,9 @@ const char *ar_hip_version(void);
  * ComputeContext (base/code/src/main/java/io/almostrealism/code/ComputeContext.java:89,133)
  * for the HIP driver: one context per GPU, one in-order HIP stream per context. */
 int ar_hip_device_count(int *count);
+/* device < 0 selects the device the environment variable AR_HIP_DEVICE names (default 0), as the
+ * reference selects its hardware from AR_* variables (Hardware.java:526,684 via SystemUtils).
+ * AR_HIP_LOG=1 additionally writes every error message to stderr as it is set. */
 int ar_hip_init(int device, ar_hip_ctx **out);
 int ar_hip_destroy(ar_hip_ctx *ctx);
 int ar_hip_synchronize(ar_hip_ctx *ctx);

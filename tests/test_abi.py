@@ -93,3 +93,29 @@ def test_bf16_rounding_is_nearest_even():
     assert r[2] == 1.0 + 4 * 2 ** -8        # tie -> even (rounds up)
     assert r[3] == 1.0
     assert abs(r[4] + 2.5e-3) < 2e-5
+
+
+def test_log_flag_writes_errors_to_stderr():
+    """AR_HIP_LOG=1: every error message the library sets is also written to stderr."""
+    import sys
+    code = ("import ctypes; from common_amd import hardware as hw; "
+            "assert hw.lib().ar_hip_device_count(None) == hw.AR_HIP_ERR_INVALID")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for flag, expect in (("1", True), ("0", False)):
+        env = dict(os.environ, AR_HIP_LOG=flag, PYTHONPATH=root)
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, cwd=root)
+        assert r.returncode == 0, r.stderr
+        assert ("[ar_hip] count is null" in r.stderr) == expect, r.stderr
+
+
+def test_kv_dtype_default_from_environment(monkeypatch):
+    from common_amd import config as C
+    monkeypatch.delenv("AR_HIP_KV_DTYPE", raising=False)
+    assert C.Qwen3Config(dim=64, hidden_dim=64, layer_count=1, head_count=1, kv_head_count=1, vocab_size=8,
+                         seq_len=4).kv_dtype == C.DTYPE_F32
+    monkeypatch.setenv("AR_HIP_KV_DTYPE", "fp16")
+    assert C.Qwen3Config(dim=64, hidden_dim=64, layer_count=1, head_count=1, kv_head_count=1, vocab_size=8,
+                         seq_len=4).kv_dtype == C.DTYPE_F16
+    monkeypatch.setenv("AR_HIP_KV_DTYPE", "int4")
+    with pytest.raises(ValueError):
+        C.Qwen3Config(dim=64, hidden_dim=64, layer_count=1, head_count=1, kv_head_count=1, vocab_size=8, seq_len=4)

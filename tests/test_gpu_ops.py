@@ -216,3 +216,15 @@ def test_attention_ignores_stale_nan_rows(ctx, heads, kv, hd, max_seq, pos):
     ref = oracle.attention_block(q, k, v, None, None, kc64, vc64, heads, kv, hd, pos, 1e6, 1e-6)
     assert np.isfinite(out).all()
     assert rel_err(out, ref) <= TOL
+
+
+def test_device_selected_by_environment(monkeypatch):
+    """ar_hip_init(-1): the device AR_HIP_DEVICE names (default 0); a device that does not exist is
+    an argument error."""
+    monkeypatch.setenv("AR_HIP_DEVICE", "0")
+    with hw.HipContext() as c:
+        assert c.info()["num_cus"] > 0
+    monkeypatch.setenv("AR_HIP_DEVICE", "99")
+    with pytest.raises(hw.HardwareException) as e:
+        hw.HipContext()
+    assert e.value.code == hw.AR_HIP_ERR_INVALID
