@@ -292,6 +292,39 @@ def traffic_probe(args):
           flush=True)
 
 
+PREFILL_PROBE_RUNS = 2
+
+
+def prefill_probe(args):
+    """Workload for the rocprofv3 counter passes over the prefill kernels (MFMA busy, VALU busy, LDS
+    bank conflicts): the C3 prompt (128 tokens, fp32 weights, fp32 MFMA path) or the C4 prompt
+    (2048 tokens, bf16 weights, fp16 MFMA path) through the batched prefill, a warm call and
+    PREFILL_PROBE_RUNS more.  No decode step is launched."""
+    import dataclasses
+
+    from common_amd import config as C
+    from common_amd import synthetic
+    from common_amd.qwen3 import Qwen3
+
+    if args.prefill_probe == "c3":
+        cfg, T, seed = C.C3_0_6B, C.C3_PROMPT, args.seed
+    else:
+        cfg, T, seed = C.C4_1_7B, C.C4_PROMPT, args.seed + 4
+        cfg = dataclasses.replace(cfg, seq_len=T + 8)
+    prompt = synthetic.prompt_ids(T, cfg.vocab_size, seed=seed)
+    with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=seed)) as model:
+        am = model.model
+        am.use_graph(False)
+        for _ in range(1 + PREFILL_PROBE_RUNS):
+            am.reset()
+            am.set_prompt(prompt)
+            am.prefill()
+        model.ctx.synchronize()
+        by_steps = am.prefill_by_steps()
+    print(json.dumps({"prefill_probe": {"workload": args.prefill_probe, "prompt": T, "runs": 1 + PREFILL_PROBE_RUNS,
+                                        "by_steps": by_steps}}), flush=True)
+
+
 # kernel-name prefixes of the C3 decode classes in a rocprofv3 trace (batch 1, fp32 weights)
 C3_CLASS_KERNELS = {
     "qkv_gemv_rmsnorm": "gemv_rx_kernel<float, 2, 4, 0>",
@@ -454,6 +487,9 @@ def main():
                     help="only run the workload of the rocprofv3 FETCH_SIZE / WRITE_SIZE passes and exit")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise the two counter passes' CSV output directories per decode class and exit")
+    ap.add_argument("--prefill-probe", choices=("c3", "c4"),
+                    help="only run that workload's prompt through the batched prefill (a warm call and "
+                         "PREFILL_PROBE_RUNS more, no decode step) for rocprofv3 counter passes, and exit")
     ap.add_argument("--prefetch", type=int, default=0,
                     help="blocks of the Infinity-Cache weight prefetch branch (0 disables)")
     args = ap.parse_args()
@@ -466,6 +502,9 @@ def main():
         return
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
+        return
+    if args.prefill_probe:
+        prefill_probe(args)
         return
     sections = {x.strip() for x in args.sections.split(",") if x.strip()}
     if "c3" not in sections:  # profiling aid: only the named extra sections, one JSON line of them
