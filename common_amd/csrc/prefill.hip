@@ -386,7 +386,7 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
 
 // fp16 Vᵀ tiles of the prompt rows from the fp32 V cache: block (tile of 64 rows, KV head, sequence)
 // reads 64 contiguous cache rows and writes 64 contiguous keys per hd row through LDS (rows past
-// the prompt are written as 0).
+// the prompt, up to the grid's last tile, are written as 0).
 template <int HD, typename KVT>
 __global__ __launch_bounds__(256) void vt16_kernel(const KVT* vcache, int S, int p0, int T, int kv_heads,
                                                    uint16_t* vt16, int Tp, int* rf) {
@@ -419,13 +419,16 @@ struct FlashParams {
 };
 
 // Causal attention over the prompt, one 8-wavefront block per (sequence, KV head, query block).
-// Waves w and w+4 own the same queries: `gsub` query heads of the KV group x (4/gsub) query tiles
-// of 32 rows.  Keys advance in super-tiles of 64, staged once per block in double-buffered LDS (the
-// next super-tile's global loads are in flight while the current one is used); wave w takes the
-// first 32 keys of each super-tile and wave w+4 the second 32, and the two partial softmax states
-// are merged through LDS at the end.  Blocks of one (sequence, KV head) are placed on one XCD when
-// the pair count allows, so that pair's K/V stays in that XCD's L2; the heaviest query blocks are
-// dispatched first.
+// The 8 wavefronts are NG = 8/KS query groups x KS key slices: a query group is `gsub` query heads
+// of the KV group x (NG/gsub) query tiles of 32 rows, and keys advance in super-tiles of SK = 32*KS,
+// staged once per block in double-buffered LDS (the next super-tile's global loads are in flight
+// while the current one is used); key slice j of a group takes keys 32j .. 32j+31 of each super-tile,
+// and the KS partial softmax states are merged through LDS at the end.  KS = 4 (32-row query blocks,
+// 128-key super-tiles) when the KV group's heads fit in two groups: causal blocks carry work
+// proportional to their last row, so many small blocks dispatched heaviest first balance the CUs
+// (a 2048-row prompt of 8 KV pairs makes 512 blocks instead of 256, one per CU, each waiting on the
+// longest); KS = 2 (64-key super-tiles) for four heads per group.  Blocks of one (sequence, KV head)
+// are placed on one XCD when the pair count allows, so that pair's K/V stays in that XCD's L2.
 // Per wave the product is computed transposed so every lane owns one query:
 //   S^T (32 keys x 32 queries) = K . Q^T   A = K rows (LDS), B = Q (registers)
 //   O^T (hd x 32 queries)     += V^T . P^T A = V^T rows (LDS), B = P^T straight from registers
@@ -435,31 +438,33 @@ struct FlashParams {
 // rounding), so P^T registers are the B operand as they are, and V^T is read in the matching order.
 // Softmax runs in base 2 on scores pre-multiplied by log2(e)/sqrt(hd); the running maximum is only
 // raised (and O, l rescaled) when a tile's maximum exceeds it by more than 8, so P <= 2^8 in fp16.
-constexpr int kFlashWaves = 8;   // per block: 4 query groups x 2 key halves
-constexpr int kFlashKeys = 64;   // keys per super-tile (Tp is a multiple of this)
+constexpr int kFlashWaves = 8;   // per block: NG query groups x KS key slices
 
-template <int HD>
+template <int HD, int SK>
 struct FlashLds {
-    static constexpr int KS = HD + 8;  // K tile row stride (halves): 16-byte rows, conflict-free b128 reads
-    static constexpr int VS = 64 + 4;  // V^T tile row stride (halves): conflict-free b64 reads
-    static constexpr int K_HALVES = kFlashKeys * KS;
+    static constexpr int KROW = HD + 8;  // K tile row stride (halves): 16-byte rows, conflict-free b128 reads
+    static constexpr int VS = SK + 4;    // V^T tile row stride (halves): conflict-free b64 reads
+    static constexpr int K_HALVES = SK * KROW;
     static constexpr int V_HALVES = HD * VS;
     static constexpr int TILE_BYTES = 2 * 2 * (K_HALVES + V_HALVES);  // two buffers of K and V^T
-    static constexpr int MERGE_BYTES = 4 * (HD / 2 + 2) * 64 * 4;      // 4 waves x (O^T + m + l) x 64 lanes
+    static constexpr int WRITERS = 8 - 8 / (SK / 32);                 // waves of key slices 1 .. KS-1
+    static constexpr int MERGE_BYTES = WRITERS * (HD / 2 + 2) * 64 * 4;  // (O^T + m + l) x 64 lanes each
     static constexpr int BYTES = TILE_BYTES > MERGE_BYTES ? TILE_BYTES : MERGE_BYTES;
 };
 
-template <int HD>
+template <int HD, int KS>
 __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
-    using L = FlashLds<HD>;
+    constexpr int SK = 32 * KS;           // keys per super-tile
+    constexpr int NG = 8 / KS;            // query groups
+    using L = FlashLds<HD, SK>;
     constexpr int NT = HD / 32;           // 32-row hd tiles of O^T
-    constexpr int CPT = HD * 8 / 512;     // 16-byte chunks per thread per super-tile (K and V^T alike)
+    constexpr int CPT = HD * SK / 8 / 512;  // 16-byte chunks per thread per super-tile (K and V^T alike)
     __shared__ __attribute__((aligned(16))) unsigned char lds[L::BYTES];
-    uint16_t* const ks = reinterpret_cast<uint16_t*>(lds);              // [2][64][KS]
+    uint16_t* const ks = reinterpret_cast<uint16_t*>(lds);              // [2][SK][KROW]
     uint16_t* const vs = ks + 2 * L::K_HALVES;                          // [2][HD][VS]
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, h2 = lane >> 5, lq = lane & 31;
-    const int half = w >> 2, wq = w & 3;
+    const int slice = w / NG, wq = w % NG;
     // block -> (unit, query block); unit -> (pair = sequence*KV + g, head subset)
     const int units = p.pairs * p.nsub;
     int unit, qrank;
@@ -474,7 +479,7 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
     const int pair = unit % p.pairs, sub = unit / p.pairs;
     const int b = pair / p.kv_heads, g = pair % p.kv_heads;
     const int qblk = p.nq - 1 - qrank;
-    const int rows_blk = 32 * (4 / p.gsub);
+    const int rows_blk = 32 * (NG / p.gsub);
     const int h = g * (p.heads / p.kv_heads) + sub * p.gsub + wq % p.gsub;
     const int row0 = qblk * rows_blk + (wq / p.gsub) * 32;
     const int myq = row0 + lq;  // this lane's query row (may be >= T: computed, not stored)
@@ -482,7 +487,7 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
     const uint16_t* kb = p.k16 + (size_t)pair * p.Tp * HD;
     const uint16_t* vb = p.vt16 + (size_t)pair * HD * p.Tp;
     const int kend = min(qblk * rows_blk + rows_blk, p.T);  // keys the block needs: 0 .. kend-1
-    const int ntiles = (kend + kFlashKeys - 1) / kFlashKeys;
+    const int ntiles = (kend + SK - 1) / SK;
 
     halfx8 qf[HD / 16];  // B operand: query lq, hd (l/32)*8 + 16*kk .. +7
     {
@@ -499,102 +504,126 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
     float m = -INFINITY, l = 0.f;
     const float c2 = 1.4426950408889634f / sqrtf((float)HD);
 
-    // super-tile staging: chunk c of K is key row c/(HD/8), halves (c%(HD/8))*8; of V^T, hd row c/8,
-    // keys (c%8)*8.  Rows k0..k0+63 < Tp always (k0 < T, Tp a multiple of 64).
-    u32x4 kreg[CPT], vreg[CPT];
-#define FLASH_LOAD_TILE(k0_)                                                                                     \
-    _Pragma("unroll") for (int i = 0; i < CPT; i++) {                                                            \
-        const int c = tid + 512 * i;                                                                             \
-        kreg[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)((k0_) + c / (HD / 8)) * HD + (c % (HD / 8)) * 8); \
-        vreg[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)(c / 8) * p.Tp + (k0_) + (c % 8) * 8);             \
-    }
-#define FLASH_STORE_TILE(buf_)                                                                                   \
-    _Pragma("unroll") for (int i = 0; i < CPT; i++) {                                                            \
-        const int c = tid + 512 * i;                                                                             \
-        *reinterpret_cast<u32x4*>(ks + (buf_) * L::K_HALVES + (c / (HD / 8)) * L::KS + (c % (HD / 8)) * 8) =      \
-            kreg[i];                                                                                             \
-        uint2* vd = reinterpret_cast<uint2*>(vs + (buf_) * L::V_HALVES + (c / 8) * L::VS + (c % 8) * 8);         \
-        vd[0] = make_uint2(vreg[i].x, vreg[i].y);                                                                \
-        vd[1] = make_uint2(vreg[i].z, vreg[i].w);                                                                \
-    }
-    FLASH_LOAD_TILE(0)
-    FLASH_STORE_TILE(0)
-    __syncthreads();
-    for (int t = 0; t < ntiles; t++) {
-        const int buf = t & 1, kh = t * kFlashKeys + 32 * half;  // this wave's 32 keys: kh .. kh+31
-        if (t + 1 < ntiles) {
-            FLASH_LOAD_TILE((t + 1) * kFlashKeys)
+    // super-tile staging: chunk c of K is key row c/(HD/8), halves (c%(HD/8))*8; of V^T, hd row
+    // c/(SK/8), keys (c%(SK/8))*8.  Rows k0..k0+SK-1 < Tp always (k0 < T, Tp a multiple of SK).
+    // Two register sets alternate, so a super-tile's global loads are issued two iterations
+    // before the iteration that stores them into LDS.
+    u32x4 kreg[2][CPT], vreg[2][CPT];
+    auto load_tile = [&](int set, int k0) {
+#pragma unroll
+        for (int i = 0; i < CPT; i++) {
+            const int c = tid + 512 * i;
+            kreg[set][i] = *reinterpret_cast<const u32x4*>(kb + (size_t)(k0 + c / (HD / 8)) * HD + (c % (HD / 8)) * 8);
+            vreg[set][i] = *reinterpret_cast<const u32x4*>(vb + (size_t)(c / (SK / 8)) * p.Tp + k0 + (c % (SK / 8)) * 8);
         }
-        if (kh <= row0 + 31 && kh < p.T) {  // else every key of the tile is masked for this wave
-            const uint16_t* kt = ks + buf * L::K_HALVES + (32 * half + lq) * L::KS + h2 * 8;
-            floatx16 s;
+    };
+    auto store_tile = [&](int set, int buf) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[r] = 0.f;
+        for (int i = 0; i < CPT; i++) {
+            const int c = tid + 512 * i;
+            *reinterpret_cast<u32x4*>(ks + buf * L::K_HALVES + (c / (HD / 8)) * L::KROW + (c % (HD / 8)) * 8) =
+                kreg[set][i];
+            uint2* vd = reinterpret_cast<uint2*>(vs + buf * L::V_HALVES + (c / (SK / 8)) * L::VS + (c % (SK / 8)) * 8);
+            vd[0] = make_uint2(vreg[set][i].x, vreg[set][i].y);
+            vd[1] = make_uint2(vreg[set][i].z, vreg[set][i].w);
+        }
+    };
+    // block barrier that waits for this wavefront's LDS accesses only: the global loads into the
+    // staging registers stay in flight across it (__syncthreads would also wait for them)
+    auto lds_barrier = [] {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt not waited on
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // one super-tile for this wavefront's 32 keys kh .. kh+31 (skipped when all are masked)
+    auto tile = [&](int t) {
+        const int buf = t & 1, kh = t * SK + 32 * slice;
+        if (!(kh <= row0 + 31 && kh < p.T)) return;  // every key of the slice is masked for this wave
+        const uint16_t* kt = ks + buf * L::K_HALVES + (32 * slice + lq) * L::KROW + h2 * 8;
+        floatx16 s;
 #pragma unroll
-            for (int kk = 0; kk < HD / 16; kk++)
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const halfx8*>(kt + kk * 16), qf[kk], s,
-                                                           0, 0, 0);
-            float mx = -INFINITY;
-            const bool edge = (kh + 31 > row0) || (kh + 31 >= p.T);
+        for (int r = 0; r < 16; r++) s[r] = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float v = s[r] * c2;
-                if (edge) {
-                    const int key = kh + (r >> 2) * 8 + h2 * 4 + (r & 3);
-                    if (key > myq || key >= p.T) v = -INFINITY;
-                }
-                s[r] = v;
-                mx = fmaxf(mx, v);
+        for (int kk = 0; kk < HD / 16; kk++)
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const halfx8*>(kt + kk * 16), qf[kk], s, 0, 0,
+                                                       0);
+        float mx = -INFINITY;
+        const bool edge = (kh + 31 > row0) || (kh + 31 >= p.T);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            float v = s[r] * c2;
+            if (edge) {
+                const int key = kh + (r >> 2) * 8 + h2 * 4 + (r & 3);
+                if (key > myq || key >= p.T) v = -INFINITY;
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            if (__ballot(mx > m + 8.0f)) {
-                const float m_new = fmaxf(m, mx);
-                const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
-                l *= alpha;
+            s[r] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (__ballot(mx > m + 8.0f)) {
+            const float m_new = fmaxf(m, mx);
+            const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+            l *= alpha;
 #pragma unroll
-                for (int j = 0; j < NT; j++)
+            for (int j = 0; j < NT; j++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) o[j][r] *= alpha;
-                m = m_new;
-            }
-            // a query whose keys so far are all masked keeps m = -inf: its weights are exp2(-inf) = 0
-            const float mu = (m == -INFINITY) ? 0.f : m;
-            float sum = 0.f;
+                for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+            m = m_new;
+        }
+        // a query whose keys so far are all masked keeps m = -inf: its weights are exp2(-inf) = 0
+        const float mu = (m == -INFINITY) ? 0.f : m;
+        float sum = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float e = __builtin_amdgcn_exp2f(s[r] - mu);
-                s[r] = e;
-                sum += e;
-            }
-            l += sum + __shfl_xor(sum, 32, 64);
-            // O^T += V^T P^T over the 32 keys, in register order: k-step kk, slot i <-> register 8kk+i
-            // <-> key kh + 16kk + 8*(i/4) + (l/32)*4 + i%4
-            const uint16_t* vt0 = vs + buf * L::V_HALVES + lq * L::VS + 32 * half + h2 * 4;
+        for (int r = 0; r < 16; r++) {
+            const float e = __builtin_amdgcn_exp2f(s[r] - mu);
+            s[r] = e;
+            sum += e;
+        }
+        l += sum + __shfl_xor(sum, 32, 64);
+        // O^T += V^T P^T over the 32 keys, in register order: k-step kk, slot i <-> register 8kk+i
+        // <-> key kh + 16kk + 8*(i/4) + (l/32)*4 + i%4
+        const uint16_t* vt0 = vs + buf * L::V_HALVES + lq * L::VS + 32 * slice + h2 * 4;
 #pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                halfx8 pf;
+        for (int kk = 0; kk < 2; kk++) {
+            halfx8 pf;
 #pragma unroll
-                for (int i = 0; i < 8; i++) pf[i] = (_Float16)s[8 * kk + i];
+            for (int i = 0; i < 8; i++) pf[i] = (_Float16)s[8 * kk + i];
 #pragma unroll
-                for (int j = 0; j < NT; j++) {
-                    const uint16_t* vt = vt0 + j * 32 * L::VS + 16 * kk;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vt);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vt + 8);
-                    const halfx8 vf = __builtin_bit_cast(halfx8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[j], 0, 0, 0);
-                }
+            for (int j = 0; j < NT; j++) {
+                const uint16_t* vt = vt0 + j * 32 * L::VS + 16 * kk;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vt);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vt + 8);
+                const halfx8 vf = __builtin_bit_cast(halfx8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[j], 0, 0, 0);
             }
         }
-        if (t + 1 < ntiles) {  // buffer buf^1 was last read before the previous barrier
-            FLASH_STORE_TILE(buf ^ 1)
-        }
-        __syncthreads();
+    };
+    // iteration t: LDS buffer t&1 holds tile t; register set (t+1)&1 holds tile t+1 (loaded two
+    // iterations ago), which goes into buffer (t+1)&1 (last read in iteration t-1), and then takes
+    // the loads of tile t+3; set t&1 holds tile t+2, in flight
+    load_tile(0, 0);
+    if (ntiles > 1) load_tile(1, SK);
+    store_tile(0, 0);
+    if (ntiles > 2) load_tile(0, 2 * SK);
+    lds_barrier();
+    for (int t = 0; t < ntiles; t += 2) {
+        // (the register set is a compile-time index in each half of the unrolled pair)
+        if (t + 1 < ntiles) store_tile(1, 1);
+        if (t + 3 < ntiles) load_tile(1, (t + 3) * SK);
+        tile(t);
+        lds_barrier();
+        if (t + 1 >= ntiles) break;
+        if (t + 2 < ntiles) store_tile(0, 0);
+        if (t + 4 < ntiles) load_tile(0, (t + 4) * SK);
+        tile(t + 1);
+        lds_barrier();
     }
-#undef FLASH_LOAD_TILE
-#undef FLASH_STORE_TILE
-    // merge the second key half into the first (the tile buffers are free after the last barrier)
-    float* mg = reinterpret_cast<float*>(lds) + wq * (HD / 2 + 2) * 64 + lane;  // [wq][value][lane]
-    if (half == 1) {
+    // merge key slices 1 .. KS-1 into slice 0 (the tile buffers are free after the last barrier)
+    float* const mg0 = reinterpret_cast<float*>(lds) + lane;  // [writer][value][lane], writer = (slice-1)*NG + wq
+    if (slice > 0) {
+        float* mg = mg0 + ((slice - 1) * NG + wq) * (HD / 2 + 2) * 64;
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
@@ -603,18 +632,32 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
         mg[(HD / 2 + 1) * 64] = l;
     }
     __syncthreads();
-    if (half == 1 || myq >= p.T) return;
-    const float m1 = mg[(HD / 2) * 64], l1 = mg[(HD / 2 + 1) * 64];
-    const float m_all = fmaxf(m, m1);  // m is finite: key 0 is in this half's first tile
-    const float a0 = __builtin_amdgcn_exp2f(m - m_all);
-    const float a1 = (m1 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m1 - m_all);
-    const float inv = 1.0f / (l * a0 + l1 * a1);
+    if (slice > 0 || myq >= p.T) return;
+    // m is finite: key 0 is in slice 0's first super-tile; slices whose keys were all masked keep -inf
+    float m_all = m;
+#pragma unroll
+    for (int j = 1; j < KS; j++) m_all = fmaxf(m_all, mg0[(((j - 1) * NG + wq) * (HD / 2 + 2) + HD / 2) * 64]);
+    float wgt[KS], den;
+    wgt[0] = __builtin_amdgcn_exp2f(m - m_all);
+    den = l * wgt[0];
+#pragma unroll
+    for (int j = 1; j < KS; j++) {
+        const float* mg = mg0 + ((j - 1) * NG + wq) * (HD / 2 + 2) * 64;
+        const float ms = mg[(HD / 2) * 64];
+        wgt[j] = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - m_all);
+        den = fmaf(mg[(HD / 2 + 1) * 64], wgt[j], den);
+    }
+    const float inv = 1.0f / den;
     uint16_t* orow = p.out + ((size_t)b * p.T + myq) * q_dim + (size_t)h * HD;
 #pragma unroll
     for (int j = 0; j < NT; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-            orow[j * 32 + (r >> 2) * 8 + h2 * 4 + (r & 3)] = f2h((o[j][r] * a0 + mg[(j * 16 + r) * 64] * a1) * inv);
+        for (int r = 0; r < 16; r++) {
+            float v = o[j][r] * wgt[0];
+#pragma unroll
+            for (int k = 1; k < KS; k++) v = fmaf(mg0[(((k - 1) * NG + wq) * (HD / 2 + 2) + j * 16 + r) * 64], wgt[k], v);
+            orow[j * 32 + (r >> 2) * 8 + h2 * 4 + (r & 3)] = f2h(v * inv);
+        }
 }
 
 }  // namespace
@@ -715,8 +758,10 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
         hipLaunchKernelGGL(qk_prep_kernel, dim3(a.B * a.T), dim3(256), 0, stream, p);
     AR_LAUNCH_CHECK();
     if (a.q32) return AR_HIP_OK;  // fp32 path: attention reads the fp32 cache rows directly
-    AR_CHECK_ARG(a.Tp % 64 == 0 && a.Tp >= a.T, "qk prep: Vᵀ rows %d not a multiple of 64 covering %d", a.Tp, a.T);
-    const dim3 vgrid((a.T + 63) / 64, a.kv_heads, a.B);
+    AR_CHECK_ARG(a.Tp % 128 == 0 && a.Tp >= a.T, "qk prep: Vᵀ rows %d not a multiple of 128 covering %d", a.Tp, a.T);
+    // whole 128-key super-tiles of the flash pass: rows T .. up to the next multiple of 128 are written
+    // as 0, so a masked key (weight 0) never meets a stale infinity of an earlier, longer prompt
+    const dim3 vgrid((a.T + 127) / 128 * 2, a.kv_heads, a.B);
 #define AR_VT16(HDV, T_)                                                                                     \
     hipLaunchKernelGGL((vt16_kernel<HDV, T_>), vgrid, dim3(256), 0, stream, reinterpret_cast<const T_*>(a.vcache), \
                        a.S, a.p0, a.T, a.kv_heads, a.vt16, a.Tp, a.range_flag)
@@ -740,25 +785,35 @@ int launch_qk_prep(const PrefillPrep& a, hipStream_t stream) {
 int launch_flash_prefill(const uint16_t* qb, const uint16_t* k16, const uint16_t* vt16, uint16_t* out, int B, int T,
                          int Tp, int heads, int kv_heads, int hd, hipStream_t stream) {
     AR_CHECK_ARG(qb && k16 && vt16 && out && T > 0 && B > 0, "flash prefill: bad arguments");
-    AR_CHECK_ARG(heads % kv_heads == 0 && Tp >= T && Tp % kFlashKeys == 0, "flash prefill: bad shape");
+    AR_CHECK_ARG(heads % kv_heads == 0 && Tp >= T, "flash prefill: bad shape");
     FlashParams p;
     p.qb = qb; p.k16 = k16; p.vt16 = vt16; p.out = out; p.T = T; p.Tp = Tp; p.heads = heads; p.kv_heads = kv_heads;
     const int G = heads / kv_heads;
     p.gsub = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
     p.nsub = G / p.gsub;
     p.pairs = B * kv_heads;
-    p.nq = (T + 32 * (4 / p.gsub) - 1) / (32 * (4 / p.gsub));
+    // four key slices (two query groups of 32 rows) unless the group holds four heads
+    const int KS = p.gsub == 4 ? 2 : 4;
+    AR_CHECK_ARG(Tp % (32 * KS) == 0, "flash prefill: Tp=%d not a multiple of the %d-key super-tile", Tp, 32 * KS);
+    const int rows_blk = 32 * ((8 / KS) / p.gsub);
+    p.nq = (T + rows_blk - 1) / rows_blk;
     const long long blocks = (long long)p.nq * p.pairs * p.nsub;
     AR_CHECK_ARG(blocks <= 0x7fffffff, "flash prefill: too many blocks");
     dim3 grid((unsigned)blocks);
-    if (hd == 128)
-        hipLaunchKernelGGL(flash_prefill_kernel<128>, grid, dim3(512), 0, stream, p);
+#define AR_FLASH(HDV, KSV) hipLaunchKernelGGL((flash_prefill_kernel<HDV, KSV>), grid, dim3(512), 0, stream, p)
+    if (hd == 128 && KS == 4)
+        AR_FLASH(128, 4);
+    else if (hd == 128)
+        AR_FLASH(128, 2);
+    else if (hd == 64 && KS == 4)
+        AR_FLASH(64, 4);
     else if (hd == 64)
-        hipLaunchKernelGGL(flash_prefill_kernel<64>, grid, dim3(512), 0, stream, p);
+        AR_FLASH(64, 2);
     else {
         ar_set_error("flash prefill: head_dim %d not supported", hd);
         return AR_HIP_ERR_INVALID;
     }
+#undef AR_FLASH
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -839,7 +839,7 @@ int ensure_prefill_buffers(ar_qwen3* m, size_t rows) {
     AR_TRY(ar_ctx_alloc(m->ctx, rows * c.hidden_dim * 2, (void**)&m->pf_act));
     m->pf_rows = rows;
     if (!m->pf_k16) {
-        m->pf_tp = (m->S + 63) / 64 * 64;
+        m->pf_tp = (m->S + 127) / 128 * 128;  // a multiple of every flash super-tile
         const size_t n = (size_t)m->B * c.kv_head_count * m->pf_tp * c.head_size * 2;
         AR_TRY(ar_ctx_alloc(m->ctx, n, (void**)&m->pf_k16));
         AR_TRY(ar_ctx_alloc(m->ctx, n, (void**)&m->pf_vt16));
