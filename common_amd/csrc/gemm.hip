@@ -226,8 +226,9 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
 // ---- large-shape kernel: 256 x 256 tiles fed by direct global -> LDS loads -------------------
 //
 // For products with many tiles (the long prompts of batched prefill) a 4-wavefront block owns a
-// 256 x 256 tile (128 x 128 per wavefront: 16 MFMA accumulators, 256 AGPRs), BK = 64, two LDS stages
-// of 64 KB filled by global_load_lds_dwordx4 (each lane's 16 bytes go straight to LDS; no staging
+// BM x 256 tile (BM = 256: 128 x 128 per wavefront, 16 MFMA accumulators; BM = 128 for the last
+// partial round of a product whose tile count is not a multiple of the CU count, see launch_t), BK =
+// 64, two LDS stages of 64 KB (BM 256) filled by global_load_lds_dwordx4 (each lane's 16 bytes go straight to LDS; no staging
 // registers, no LDS store instructions).  Rows are 128 B; the 16-byte chunk c of row r sits in slot
 // c ^ ((r >> 1) & 7), so the eight lanes that read one 16-byte piece each per LDS cycle hit eight
 // different bank groups.  Per k-tile the block waits once: after the third k-step's MFMAs every
@@ -236,54 +237,63 @@ __global__ __launch_bounds__(BMT * 2) void gemm_kernel(GemmParams p, int mt, int
 // tile's first fragments are read while the last k-step's MFMAs run.  Waits are written by hand: a
 // workgroup-scope fence (__syncthreads) would also wait for every outstanding LDS copy.
 namespace dma {
-constexpr int BM = 256, BNW = 256, BK = 64, STAGES = 2, NTHR = 256, KS = BK / 16;
+constexpr int BNW = 256, BK = 64, STAGES = 2, NTHR = 256, KS = BK / 16;
 constexpr int ROWB = BK * 2;
-constexpr int TILE_B = 256 * ROWB;
-constexpr int STAGE_B = 2 * TILE_B;
-constexpr int LDS_BYTES = STAGES * STAGE_B;  // 128 KB
-constexpr int DMA = TILE_B / 1024 / 4;       // copy instructions per wavefront per matrix per stage
+constexpr int TILE_W = 256 * ROWB;
+template <int BM>
+struct Shape {
+    static constexpr int TILE_A = BM * ROWB;
+    static constexpr int STAGE_B = TILE_A + TILE_W;
+    static constexpr int LDS_BYTES = STAGES * STAGE_B;  // 128 KB (BM 256) or 96 KB (BM 128)
+    static constexpr int DMA_A = TILE_A / 1024 / 4;      // copy instructions per wavefront per stage: A
+    static constexpr int DMA_W = TILE_W / 1024 / 4;      // and W
+};
 // s_waitcnt immediates (vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
 constexpr int vm_imm(int v, int lgkm) { return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (lgkm << 8); }
-constexpr int VM_PROLOGUE = vm_imm(2 * DMA * (STAGES - 1), 15);  // all but tile 0 may be in flight
-constexpr int VM_LOOP = vm_imm(2 * DMA * (STAGES - 2), 0);       // tile kt + 1 landed, LDS reads done
 typedef __attribute__((address_space(3))) void lds_void;
 __device__ inline int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 }  // namespace dma
 
-template <bool F16, int EPI>
+template <bool F16, int EPI, int BM>
 __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int mt, int nt) {
+    using Sh = dma::Shape<BM>;
     using Mf = Mfma<F16>;
     using frag = typename Mf::frag;
     extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
     constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
     constexpr int BN = dma::BNW / NW;  // output columns per block (SwiGLU: 128 gate rows + 128 up rows)
-    constexpr int WN = BN / 2, FN = WN / 32, FM = 4;
+    constexpr int WN = BN / 2, FN = WN / 32, FM = BM / 64, WM = BM / 2;  // wavefront tile WM x WN
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     int mi, ni;
     tile_of(blockIdx.x, mt, nt, &mi, &ni);
-    const int m0 = mi * dma::BM, n0 = ni * BN;
+    const int m0 = mi * BM, n0 = ni * BN;
     const int nk = p.K / dma::BK;
 
     // copy plan: instruction i of wavefront w fills rows 8j .. 8j+7 (j = 4i + w) of a tile; lane l
     // writes slot l % 8 of row 8j + l / 8, i.e. fetches chunk dma::swz(row, l % 8)
-    const uint16_t* srcA[dma::DMA];
-    const uint16_t* srcW[dma::DMA];
+    const uint16_t* srcA[Sh::DMA_A];
+    const uint16_t* srcW[Sh::DMA_W];
 #pragma unroll
-    for (int i = 0; i < dma::DMA; i++) {
+    for (int i = 0; i < Sh::DMA_A; i++) {
         const int j = 4 * i + wave, r = 8 * j + (lane >> 3), c = dma::swz(r, lane & 7);
         srcA[i] = p.A + (size_t)min(m0 + r, p.M - 1) * p.lda + c * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < Sh::DMA_W; i++) {
+        const int j = 4 * i + wave, r = 8 * j + (lane >> 3), c = dma::swz(r, lane & 7);
         const uint16_t* wb = (NW == 2 && r >= BN) ? p.W2 + (size_t)(n0 + r - BN) * p.ldw : p.W + (size_t)(n0 + r) * p.ldw;
         srcW[i] = wb + c * 8;
     }
     auto issue = [&](int slot, int kt) {
         const int k0 = kt * dma::BK;
-        unsigned char* st = lds + slot * dma::STAGE_B;
+        unsigned char* st = lds + slot * Sh::STAGE_B;
 #pragma unroll
-        for (int i = 0; i < dma::DMA; i++) {
+        for (int i = 0; i < Sh::DMA_W; i++) {
             const int j = 4 * i + wave;
-            __builtin_amdgcn_global_load_lds((const void*)(srcA[i] + k0), (dma::lds_void*)(st + j * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(srcW[i] + k0), (dma::lds_void*)(st + dma::TILE_B + j * 1024), 16, 0, 0);
+            if (i < Sh::DMA_A)
+                __builtin_amdgcn_global_load_lds((const void*)(srcA[i] + k0), (dma::lds_void*)(st + j * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(srcW[i] + k0), (dma::lds_void*)(st + Sh::TILE_A + j * 1024), 16, 0, 0);
         }
     };
 
@@ -299,11 +309,11 @@ __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int m
 
     frag fa[2][FM], fb[2][NW][FN];  // fragments of two k-steps
     auto read = [&](int set, int slot, int kk) {
-        const unsigned char* st = lds + slot * dma::STAGE_B;
+        const unsigned char* st = lds + slot * Sh::STAGE_B;
         const int c = kk * 2 + (lane >> 5);
 #pragma unroll
         for (int i = 0; i < FM; i++) {
-            const int r = wm * 128 + i * 32 + (lane & 31);
+            const int r = wm * WM + i * 32 + (lane & 31);
             fa[set][i] = *reinterpret_cast<const frag*>(st + r * dma::ROWB + dma::swz(r, c) * 16);
         }
 #pragma unroll
@@ -311,7 +321,7 @@ __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int m
 #pragma unroll
             for (int j = 0; j < FN; j++) {
                 const int r = w * BN + wn * WN + j * 32 + (lane & 31);
-                fb[set][w][j] = *reinterpret_cast<const frag*>(st + dma::TILE_B + r * dma::ROWB + dma::swz(r, c) * 16);
+                fb[set][w][j] = *reinterpret_cast<const frag*>(st + Sh::TILE_A + r * dma::ROWB + dma::swz(r, c) * 16);
             }
     };
     auto mma = [&](int set) {
@@ -326,7 +336,8 @@ __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int m
 #pragma unroll
     for (int s = 0; s < dma::STAGES; s++) issue(s, min(s, nk - 1));
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(dma::VM_PROLOGUE);
+    // all but stage 0's copies may be in flight
+    __builtin_amdgcn_s_waitcnt(dma::vm_imm((Sh::DMA_A + Sh::DMA_W) * (dma::STAGES - 1), 15));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     read(0, 0, 0);
@@ -342,7 +353,7 @@ __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int m
         mma((dma::KS - 2) & 1);
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt(dma::VM_LOOP);
+        __builtin_amdgcn_s_waitcnt(dma::vm_imm((Sh::DMA_A + Sh::DMA_W) * (dma::STAGES - 2), 0));  // tile kt+1 landed, LDS reads done
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         // the stage just finished takes tile kt + dma::STAGES (the last tiles reload tile nk - 1, which
@@ -360,7 +371,7 @@ __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int m
     // at a time (clamped rows, no branches) before the adds and the guarded stores
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-        const int rbase = m0 + wm * 128 + i * 32 + (lane >> 5) * 4;
+        const int rbase = m0 + wm * WM + i * 32 + (lane >> 5) * 4;
         if constexpr (EPI == GEMV_EPI_RESIDUAL) {
 #pragma unroll
             for (int j0 = 0; j0 < FN; j0 += 2) {
@@ -408,19 +419,20 @@ __global__ __launch_bounds__(dma::NTHR) void gemm_dma_kernel(GemmParams p, int m
     }
 }
 
-template <bool F16, int EPI>
+template <bool F16, int EPI, int BM>
 int launch_dma(const GemmParams& p, hipStream_t st) {
     constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
-    const int mt = (p.M + dma::BM - 1) / dma::BM, nt = p.N / (dma::BNW / NW);
-    // 128 KB of dynamic LDS needs the per-kernel opt-in, once per device
+    using Sh = dma::Shape<BM>;
+    const int mt = (p.M + BM - 1) / BM, nt = p.N / (dma::BNW / NW);
+    // more than 64 KB of dynamic LDS needs the per-kernel opt-in, once per device
     static std::atomic<bool> attr_set[kMaxDevices];
     const int slot = ar_device_slot(st);
     if (slot < 0 || !attr_set[slot].load(std::memory_order_relaxed)) {
-        AR_HIP_TRY(hipFuncSetAttribute((const void*)gemm_dma_kernel<F16, EPI>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, dma::LDS_BYTES));
+        AR_HIP_TRY(hipFuncSetAttribute((const void*)gemm_dma_kernel<F16, EPI, BM>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS_BYTES));
         if (slot >= 0) attr_set[slot].store(true, std::memory_order_relaxed);
     }
-    hipLaunchKernelGGL((gemm_dma_kernel<F16, EPI>), dim3(mt * nt), dim3(dma::NTHR), dma::LDS_BYTES, st, p, mt, nt);
+    hipLaunchKernelGGL((gemm_dma_kernel<F16, EPI, BM>), dim3(mt * nt), dim3(dma::NTHR), Sh::LDS_BYTES, st, p, mt, nt);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
@@ -435,7 +447,41 @@ bool use_dma(const GemmParams& p) {
     constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
     const int bn = dma::BNW / NW;
     if (p.ksplit != 1 || p.N % bn || p.K % dma::BK) return false;
-    return (long long)((p.M + dma::BM - 1) / dma::BM) * (p.N / bn) >= kDmaMinTiles;
+    return (long long)((p.M + 255) / 256) * (p.N / bn) >= kDmaMinTiles;
+}
+
+// The columns [n0, n0 + n) of a product: the same A, the weight rows n0.. and the output columns n0..
+GemmParams column_range(const GemmParams& p, int n0, int n) {
+    GemmParams q = p;
+    q.W = p.W + (size_t)n0 * p.ldw;
+    if (p.W2) q.W2 = p.W2 + (size_t)n0 * p.ldw;
+    if (p.bias) q.bias = p.bias + n0;
+    if (p.C) q.C = p.C + n0;
+    if (p.O) q.O = p.O + n0;
+    q.N = n;
+    return q;
+}
+
+// 256 x 256 tiles in whole rounds over the CUs, and the remainder as 128-row tiles.  With one
+// 256-row block per CU, a tile count that is not a multiple of the CU count leaves a last round in
+// which most CUs idle (C4 gate/up: 384 tiles on 256 CUs = two full-tile times); the columns past the
+// whole rounds go instead to half-height tiles, twice as many blocks of half the work (C4: 256 tiles
+// of 256 x 256 for the first 4096 outputs, then 256 of 128 x 256: one and a half tile times).
+template <bool F16, int EPI>
+int launch_dma_rounds(const GemmParams& p, int cus, hipStream_t st) {
+    constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
+    const int bn = dma::BNW / NW;
+    const int mt = (p.M + 255) / 256, nt = p.N / bn;
+    const long long tiles = (long long)mt * nt;
+    if (cus > 0 && tiles > cus && tiles % cus != 0) {
+        const int nt1 = (int)((tiles / cus) * cus / mt);                // columns of whole 256-row rounds
+        const long long half = (long long)((p.M + 127) / 128) * (nt - nt1);  // 128-row tiles of the rest
+        if (nt1 > 0 && half <= cus) {
+            AR_TRY((launch_dma<F16, EPI, 256>(column_range(p, 0, nt1 * bn), st)));
+            return launch_dma<F16, EPI, 128>(column_range(p, nt1 * bn, (nt - nt1) * bn), st);
+        }
+    }
+    return launch_dma<F16, EPI, 256>(p, st);
 }
 
 template <int EPI, int BMT>
@@ -456,7 +502,10 @@ int launch_bm(const GemmParams& p, bool f16, hipStream_t st) {
 // 51 us, gate/up 163 us with 256-row tiles vs 176 us.
 template <int EPI>
 int launch_t(const GemmParams& p, bool f16, hipStream_t st) {
-    if (use_dma<EPI>(p)) return f16 ? launch_dma<true, EPI>(p, st) : launch_dma<false, EPI>(p, st);
+    if (use_dma<EPI>(p)) {
+        const int cus = ar_device_cus(st);
+        return f16 ? launch_dma_rounds<true, EPI>(p, cus, st) : launch_dma_rounds<false, EPI>(p, cus, st);
+    }
     const long long blocks256 = (long long)((p.M + 255) / 256) * (p.N / BN) * p.ksplit;
     if (blocks256 >= (EPI == GEMV_EPI_SWIGLU ? 256 : 512)) return launch_bm<EPI, 256>(p, f16, st);
     return launch_bm<EPI, 128>(p, f16, st);

@@ -98,6 +98,34 @@ def test_gemm_large_tile_path(ctx, K):
     assert rel_err(o, u * (g / (1 + np.exp(-g)))) <= 8e-3
 
 
+@pytest.mark.parametrize("M,N,K,epi", [(2048, 6144, 2048, "swiglu"), (1100, 16384, 128, "store"),
+                                       (1100, 16384, 128, "residual")])
+def test_gemm_tile_rounds_with_half_height_remainder(ctx, M, N, K, epi):
+    """Tile counts past whole rounds of the CUs: the columns of the last partial round go to
+    128-row tiles (C4 gate/up: 384 tiles of 256 x 256 on 256 CUs; 1100 ragged rows: 320 tiles)."""
+    r = np.random.default_rng(M + N + K)
+    A = bf16(r.standard_normal((M, K)))
+    W = bf16(r.standard_normal((N, K)) * 0.05)
+    Ad, Wd = ctx.to_device(bits(A)), ctx.to_device(bits(W))
+    rows = np.concatenate([np.arange(40), r.choice(M, 40, replace=False), np.arange(M - 40, M)])
+    g = A[rows].astype(np.float64) @ W.astype(np.float64).T
+    if epi == "swiglu":
+        W2 = bf16(r.standard_normal((N, K)) * 0.05)
+        Od = ctx.allocate(M * N * 2)
+        ctx.gemm_bf16(Ad, Wd, M, N, K, hw.GEMM_SWIGLU, W2=ctx.to_device(bits(W2)), O=Od)
+        ctx.synchronize()
+        u = A[rows].astype(np.float64) @ W2.astype(np.float64).T
+        o = (Od.download(np.uint16, M * N).astype(np.uint32) << 16).view(np.float32).reshape(M, N)[rows]
+        assert rel_err(o, u * (g / (1 + np.exp(-g)))) <= 8e-3
+        return
+    C0 = r.standard_normal((M, N)).astype(np.float32) if epi == "residual" else np.zeros((M, N), np.float32)
+    Cd = ctx.to_device(C0)
+    ctx.gemm_bf16(Ad, Wd, M, N, K, hw.GEMM_RESIDUAL if epi == "residual" else hw.GEMM_STORE, C=Cd)
+    ctx.synchronize()
+    got = Cd.download(np.float32, M * N).reshape(M, N)[rows]
+    assert rel_err(got, C0[rows] + g) <= 1e-5
+
+
 def test_gemm_rejects_bad_shapes(ctx):
     z = ctx.allocate(1 << 16)
     with pytest.raises(hw.HardwareException):
