@@ -293,6 +293,8 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
     const int nq = p.heads * fd4, nk = p.kv_heads * fd4;
     float4 q1[QP], q2[QP], k1 = make_float4(0.f, 0.f, 0.f, 0.f), k2 = k1;
     float2 ss = make_float2(0.f, 0.f);
+    // this thread's first v slice, loaded with q and k so its latency overlaps the norms and rotations
+    const float4 v0 = tid < kv_dim / 4 ? reinterpret_cast<const float4*>(v)[tid] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int j = 0; j < QP; j++) {
         const int idx = tid + 256 * j;
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
     }
     for (int i4 = tid; i4 < kv_dim / 4; i4 += 256) {
         const int g = (4 * i4) / hd, i = 4 * i4 - g * hd;
-        const float4 vv = reinterpret_cast<const float4*>(v)[i4];
+        const float4 vv = i4 == tid ? v0 : reinterpret_cast<const float4*>(v)[i4];
         const size_t vofs = (((size_t)b * p.kv_heads + g) * p.S + pos) * hd + i;
         if (p.kv16)
             *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.vcache) + vofs) = pack4h(vv.x, vv.y, vv.z, vv.w, p.rf);
@@ -384,25 +386,36 @@ __global__ __launch_bounds__(256) void qk_prep_v4_kernel(PrepParams p) {
     }
 }
 
-// fp16 Vᵀ tiles of the prompt rows from the fp32 V cache: block (tile of 64 rows, KV head, sequence)
-// reads 64 contiguous cache rows and writes 64 contiguous keys per hd row through LDS (rows past
-// the prompt, up to the grid's last tile, are written as 0).
+// fp16 Vᵀ tiles of the prompt rows from the V cache: block (tile of 64 rows, KV head, sequence)
+// reads 64 contiguous cache rows (16-byte loads) into LDS and writes, per hd row, the 64 keys as
+// eight 16-byte chunks of fp16 (rows past the prompt, up to the grid's last tile, are written as 0).
 template <int HD, typename KVT>
 __global__ __launch_bounds__(256) void vt16_kernel(const KVT* vcache, int S, int p0, int T, int kv_heads,
                                                    uint16_t* vt16, int Tp, int* rf) {
+    constexpr int VEC = 16 / sizeof(KVT);  // cache elements per 16-byte load
     __shared__ float tile[64][HD + 1];
     const int t0 = blockIdx.x * 64, g = blockIdx.y, b = blockIdx.z;
     const size_t head = (size_t)b * kv_heads + g;
     const KVT* src = vcache + (head * S + p0) * HD;
-    for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
-        const int r = idx / HD, i = idx - r * HD;
-        tile[r][i] = t0 + r < T ? (float)src[(size_t)(t0 + r) * HD + i] : 0.f;
+    for (int idx = threadIdx.x; idx < 64 * HD / VEC; idx += 256) {
+        const int r = idx / (HD / VEC), i = (idx - r * (HD / VEC)) * VEC;
+        if (t0 + r < T) {
+            typedef KVT vec_t __attribute__((ext_vector_type(VEC)));
+            const vec_t v = *reinterpret_cast<const vec_t*>(src + (size_t)(t0 + r) * HD + i);
+#pragma unroll
+            for (int e = 0; e < VEC; e++) tile[r][i + e] = (float)v[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; e++) tile[r][i + e] = 0.f;
+        }
     }
     __syncthreads();
     uint16_t* dst = vt16 + head * HD * Tp + t0;
-    for (int idx = threadIdx.x; idx < 64 * HD; idx += 256) {
-        const int i = idx / 64, r = idx - i * 64;
-        dst[(size_t)i * Tp + r] = f2h(tile[r][i], rf);
+    for (int idx = threadIdx.x; idx < HD * 8; idx += 256) {  // (hd row, chunk of 8 keys)
+        const int i = idx >> 3, c = (idx & 7) * 8;
+        const uint2 lo = pack4h(tile[c][i], tile[c + 1][i], tile[c + 2][i], tile[c + 3][i], rf);
+        const uint2 hi = pack4h(tile[c + 4][i], tile[c + 5][i], tile[c + 6][i], tile[c + 7][i], rf);
+        *reinterpret_cast<uint4*>(dst + (size_t)i * Tp + c) = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
 }
 
