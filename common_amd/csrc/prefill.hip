@@ -522,14 +522,21 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
     // Two register sets alternate, so a super-tile's global loads are issued two iterations
     // before the iteration that stores them into LDS.
     u32x4 kreg[2][CPT], vreg[2][CPT];
-    auto load_tile = [&](int set, int k0) {
+    auto load_k = [&](int set, int k0) {
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
             const int c = tid + 512 * i;
             kreg[set][i] = *reinterpret_cast<const u32x4*>(kb + (size_t)(k0 + c / (HD / 8)) * HD + (c % (HD / 8)) * 8);
+        }
+    };
+    auto load_v = [&](int set, int k0) {
+#pragma unroll
+        for (int i = 0; i < CPT; i++) {
+            const int c = tid + 512 * i;
             vreg[set][i] = *reinterpret_cast<const u32x4*>(vb + (size_t)(c / (SK / 8)) * p.Tp + k0 + (c % (SK / 8)) * 8);
         }
     };
+    auto load_tile = [&](int set, int k0) { load_k(set, k0); load_v(set, k0); };
     auto store_tile = [&](int set, int buf) {
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
@@ -624,13 +631,15 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
     for (int t = 0; t < ntiles; t += 2) {
         // (the register set is a compile-time index in each half of the unrolled pair)
         if (t + 1 < ntiles) store_tile(1, 1);
-        if (t + 3 < ntiles) load_tile(1, (t + 3) * SK);
+        if (t + 3 < ntiles) load_k(1, (t + 3) * SK);
         tile(t);
+        if (t + 3 < ntiles) load_v(1, (t + 3) * SK);
         lds_barrier();
         if (t + 1 >= ntiles) break;
         if (t + 2 < ntiles) store_tile(0, 0);
-        if (t + 4 < ntiles) load_tile(0, (t + 4) * SK);
+        if (t + 4 < ntiles) load_k(0, (t + 4) * SK);
         tile(t + 1);
+        if (t + 4 < ntiles) load_v(0, (t + 4) * SK);
         lds_barrier();
     }
     // merge key slices 1 .. KS-1 into slice 0 (the tile buffers are free after the last barrier)
