@@ -8,8 +8,10 @@ then exactly `--steps` tokens are timed with the tokens kept on the device (no h
 trip inside the timed region).  Default: warmup 5 + 251 timed = the config's 256 decode tokens.
 
 Extra fields on the JSON line:
-  roofline      dominant kernel's achieved HBM GB/s, from HIP events bracketing every launch
-                of that kernel class on the model's stream, --probe-steps decode steps per class
+  roofline      dominant kernel's achieved HBM GB/s: its class launched LOOP_ROUNDS times per layer
+                over the layers' weights in one HIP graph, two HIP events around the replay on the
+                model's stream (per-class shares of the step also from HIP events carried in the
+                class's dispatches over --probe-steps decode steps)
   cpu_baseline  the CPU oracle (reference semantics, fp32) on this host, over a bounded sample
   c4            BASELINE config 4 (Qwen3-1.7B shape, bf16 weights): a 2048-token prompt through the
                 MFMA prefill path (tok/s and fraction of the 2.5 PFLOP/s dense bf16/fp16 MFMA peak),
@@ -293,6 +295,7 @@ def traffic_probe(args):
 
 
 PREFILL_PROBE_RUNS = 2
+LOOP_ROUNDS = 8  # loop probe: launches per layer (x layers) for each weight-streaming decode class
 
 
 def prefill_probe(args):
@@ -606,6 +609,24 @@ def main():
                          "share_of_step": round(per_tok_us / (1000.0 * ms), 4)}
         log(f"[bench] {name}: {avg_us:.2f} us/launch x {n_k // per_class}/token"
             + (f" = {b / avg_us / 1e3:.0f} GB/s" if b else ""))
+    # ---- loop probe: each weight-streaming class alone, LOOP_ROUNDS launches per layer cycling
+    # through the 28 layers' weights (so they stream from HBM as in the step), captured into one HIP
+    # graph and timed by two events around its replay: the average launch duration with no event
+    # inside any dispatch (the probe above carries ~1.2 us per dispatch for its events).  It
+    # overwrites the step's activations; the sampling runs below reset the model first.
+    loop_ids = {"qkv_gemv_rmsnorm": q.KT_QKV, "o_gemv_residual": q.KT_O, "gate_up_gemv_swiglu": q.KT_GATE_UP,
+                "down_gemv_residual": q.KT_DOWN, "logits_gemv_argmax": q.KT_LOGITS}
+    for name, which in loop_ids.items():
+        if name not in kernels:
+            continue
+        per_tok = kernels[name]["launches"] // max(per_class, 1)
+        reps = LOOP_ROUNDS * (per_tok if per_tok > 1 else 1)
+        lus = am.kernel_loop(which, reps)
+        b = kernels[name]["bytes_per_launch"]
+        kernels[name].update({"loop_avg_us": round(lus, 3), "loop_launches": reps,
+                              "loop_GBs": round(b / lus / 1e3, 1), "loop_hbm_frac": round(b / lus / 1e3 / HBM_PEAK_GBS, 4),
+                              "loop_share_of_step": round(lus * per_tok / (1000.0 * ms), 4)})
+        log(f"[bench] {name} loop: {lus:.2f} us/launch over {reps} launches = {b / lus / 1e3:.0f} GB/s")
     # The roofline kernel is the weight-streaming class with the largest share of the step (gate/up
     # SwiGLU GEMV at C3); the logits GEMV (the largest single launch) rides along as roofline_logits.
     # The attention class is latency-bound (~1 MB of K/V per layer at C3), not an HBM roofline kernel.
@@ -614,11 +635,17 @@ def main():
     def roof(name):
         kd = kernels[name]
         tr = traffic.get(name, {})
-        return {"bound": "hbm", "kernel": name, "achieved": kd["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr.get("hbm_bytes_per_launch"),
+        looped = "loop_avg_us" in kd
+        us = kd["loop_avg_us"] if looped else kd["avg_us"]
+        gbs = kd["bytes_per_launch"] / us / 1e3
+        return {"bound": "hbm", "kernel": name, "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": tr.get("hbm_bytes_per_launch"),
                 "traffic_source": "profiles/c3_decode_traffic.md" if tr else None,
-                "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": kd["avg_us"],
-                "share_of_step": kd["share_of_step"]}
+                "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": round(us, 3),
+                "timing": ("graph-replayed loop of the class's launches over the layers, two HIP events around it"
+                           if looped else "HIP events inside the class's dispatches"),
+                "probe_avg_launch_us": kd["avg_us"],
+                "share_of_step": kd.get("loop_share_of_step", kd["share_of_step"])}
 
     gemv_classes = [k for k in kernels if k != "attention_decode" and kernels[k]["GBs"]]
     roofline = roof(max(gemv_classes, key=lambda k: kernels[k]["us_per_token"])) if gemv_classes else None

@@ -87,6 +87,7 @@ _SIGS = {
     "ar_hip_qwen3_hidden": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_qwen3_kernel_timing": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_kernel_time": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), _c_int_p]),
+    "ar_hip_qwen3_kernel_loop": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "ar_hip_qwen3_use_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_use_prefetch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),

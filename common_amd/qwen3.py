@@ -120,6 +120,13 @@ class AutoregressiveModel:
         hw.check(hw.lib().ar_hip_qwen3_kernel_time(self.handle, ctypes.byref(ms), ctypes.byref(n)))
         return ms.value, n.value
 
+    def kernel_loop(self, which: int, reps: int) -> float:
+        """Average launch duration (µs) of kernel class `which` over `reps` graph-replayed launches
+        cycling through the layers (ar_hip_qwen3_kernel_loop); call reset() before the next step."""
+        us = ctypes.c_double()
+        hw.check(hw.lib().ar_hip_qwen3_kernel_loop(self.handle, which, reps, ctypes.byref(us)))
+        return us.value
+
 
 class Qwen3:
     """Device-resident Qwen3 built from an HF-keyed state dict (or an iterator of (key, tensor))."""

@@ -264,6 +264,15 @@ int ar_hip_qwen3_hidden(ar_qwen3 *m, float *out);
 #define AR_KT_O 6
 int ar_hip_qwen3_kernel_timing(ar_qwen3 *m, int which);
 int ar_hip_qwen3_kernel_time(ar_qwen3 *m, double *ms, int *launches);
+/* Loop probe of one decode kernel class (AR_KT_QKV, AR_KT_O, AR_KT_GATE_UP, AR_KT_DOWN or
+ * AR_KT_LOGITS): `reps` launches of that class exactly as the decode step issues them, cycling
+ * through the layers' weights (so the weights stream from HBM as in the step), captured into one
+ * HIP graph and replayed between two events (with graphs off, ar_hip_qwen3_use_graph(m, 0): the
+ * launches back to back between the two events); *us_per_launch receives the average launch
+ * duration (no event inside any dispatch).  A measurement aid of the benchmark, like
+ * ar_hip_qwen3_kernel_timing: the launches overwrite the step's activations (the residual classes
+ * add into the residual stream), so the model must be reset before its next step. */
+int ar_hip_qwen3_kernel_loop(ar_qwen3 *m, int which, int reps, double *us_per_launch);
 /* Use a captured HIP graph per decode step (1, default) or plain launches (0). */
 int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
 /* Infinity-Cache prefetch: a second stream reads layer l+1's weights while layer l computes, with

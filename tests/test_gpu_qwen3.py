@@ -277,6 +277,31 @@ def test_long_context_split_attention(ctx, seq_len):
     assert rel_err(logits[0], rl) <= LOGIT_TOL_F32
 
 
+def test_kernel_loop_probe(ctx, c1):
+    """ar_hip_qwen3_kernel_loop: a positive launch time for every weight-streaming class, the attention
+    class refused (it writes cache rows), and after reset() the model decodes what a fresh run does."""
+    from common_amd import qwen3 as q
+    cfg, sd, prompt = c1
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        am.reset()
+        am.set_prompt(prompt)
+        before = am.run(len(prompt) + 8)
+        for graph in (True, False):  # one graph replayed, or the launches back to back
+            am.use_graph(graph)
+            for which in (q.KT_QKV, q.KT_O, q.KT_GATE_UP, q.KT_DOWN, q.KT_LOGITS):
+                us = am.kernel_loop(which, 3 * cfg.layer_count)
+                assert 0.0 < us < 1e4, (graph, which, us)
+        am.use_graph(True)
+        with pytest.raises(hw.HardwareException):
+            am.kernel_loop(q.KT_ATTENTION, 4)
+        with pytest.raises(hw.HardwareException):
+            am.kernel_loop(q.KT_QKV, 0)
+        am.reset()
+        am.set_prompt(prompt)
+        assert np.array_equal(am.run(len(prompt) + 8), before)
+
+
 def test_model_state_errors(ctx, c1):
     cfg, sd, prompt = c1
     with Qwen3(cfg, sd, ctx) as m:
