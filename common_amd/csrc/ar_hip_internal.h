@@ -312,6 +312,33 @@ __host__ __device__ inline void attn_split_plan(int n, int max_splits, int* nspl
 
 // Attention partials + (when the context is split) the combine kernel.
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
+
+// Persistent decode step (decode_persistent.hip): every layer of a batch-1 fp32 decode step in one
+// cooperative launch of one block per CU.  `layers` is a device table of layer_count entries written
+// by decode_persistent_layer_entry; `ll` holds decode_persistent_ll_words() zeroed words at first
+// use; state[0] is the position and state[3] the exchange epoch base, which every launch advances.
+struct DecodePersistentLaunch {
+    const void* layers = nullptr;
+    int layer_count = 0;
+    int dim = 0, hidden_dim = 0, heads = 0, kv_heads = 0, head_dim = 0;
+    float* x = nullptr;        // [dim] the step's input and, after the launch, its output
+    float* kcache = nullptr;   // [L][KV][S][HD] fp32
+    float* vcache = nullptr;
+    int max_seq = 0;
+    const float2* rope_tab = nullptr;
+    int* state = nullptr;
+    uint64_t* ll = nullptr;
+    int* err = nullptr;        // 1: a cross-block wait timed out; 2: position outside the cache
+    float eps = 1e-6f;
+    int per_head_norm = 0;
+};
+size_t decode_persistent_layer_bytes();
+size_t decode_persistent_ll_words(int dim, int F, int heads, int kv_heads, int hd);  // 0: no instantiation
+int decode_persistent_layer_entry(void* dst, const float* wqkv, const float* wo, const float* w1, const float* w3,
+                                  const float* w2, const float* attn_norm, const float* ffn_norm, const float* q_norm,
+                                  const float* k_norm, const float* bqkv);
+bool decode_persistent_supported(int dim, int F, int heads, int kv_heads, int hd);
+int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t stream);
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);
 // Splits for a cache of max_seq rows: about one block per CU, rows per split <= 256 (1040 for an
 // fp16 cache; one split, no combine, for caches of at most 256 rows).

@@ -1,0 +1,747 @@
+// Persistent decode step: every layer of one batch-1 Qwen3 decode step in one cooperative launch.
+//
+// The step the reference builds per layer (engine/ml/.../AttentionFeatures.java:785-929,
+// FeedForwardFeatures.java:147-156, NormalizationLayerFeatures.java:584-595) is five all-to-all
+// dependencies per layer: each GEMV needs the whole output of the previous stage.  Launched as
+// separate kernels, every stage pays a launch, the cold HBM round trip of its first weight loads
+// and an idle tail, which at the 0.6B decode shapes (8-25 MB per GEMV) costs as much as the weight
+// stream itself.  Here one block per CU runs all layers:
+//  * each stage's weight rows for this block are issued into registers before the block waits for
+//    the stage's input, so the HBM latency and stream overlap the cross-block exchange;
+//  * stages exchange their outputs through 64-bit words that carry an epoch next to the fp32
+//    value, stored and loaded at device scope (they bypass the XCD-private L2s): a reader polls
+//    the words it needs until every epoch is the current one, so the data's arrival is the
+//    synchronisation (no counters, no fences, no contention on a shared address);
+//  * every wait is bounded: a block that waits too long flags the error word and stops waiting,
+//    so the grid always drains; the host reports the flag as an error.
+//
+// Stages of layer l (epoch e = base + l + 1, exchange buffers double-buffered by l's parity):
+//   P1 QKV      qkv = Wqkv . (rmsnorm(x) * attn_norm) (+ bias)             rows of all blocks
+//   P2 attention per (KV head, split): QK-norm, RoPE, cache-row write at pos, online softmax over
+//               the split's cache rows -> unnormalised partials (o, max, sum)
+//   P2b merge   per query head (one block each): o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s
+//   P3 O        x_mid = x + Wo . o
+//   P4 gate/up  h = (W3 . xn) * silu(W1 . xn), xn = rmsnorm(x_mid) * ffn_norm
+//   P5 down     x' = x_mid + W2 . h          (the last layer also stores x' for the logits GEMV)
+// The block grid is fixed (one block per CU); the rows of every GEMV divide evenly over it.
+#include <cstdint>
+
+#include "ar_hip_internal.h"
+#include "gemv_impl.h"
+
+namespace {
+
+constexpr int kPB = 256;           // blocks: one per CU
+constexpr int kPT = 512;           // threads per block
+constexpr int kPW = kPT / 64;      // wavefronts per block
+constexpr int kSMax = 8;           // attention splits per KV head
+constexpr int kRowsPerSplit = 32;  // cache rows per split before another split is opened
+constexpr unsigned kSpinLimit = 1u << 18;  // polls before a wait is abandoned (~0.3 s)
+constexpr int kPadLds = 64 * 1024;         // dynamic LDS that keeps a second block off each CU
+
+struct PLayer {
+    const float* wqkv;
+    const float* wo;
+    const float* w1;
+    const float* w3;
+    const float* w2;
+    const float* attn_norm;
+    const float* ffn_norm;
+    const float* q_norm;
+    const float* k_norm;
+    const float* bqkv;
+};
+
+struct PParams {
+    const PLayer* layers;
+    int L;
+    float* x;          // [dim]: the step's input (embedding row) and, after the last layer, its output
+    float* kcache;     // [L][KV][S][HD]
+    float* vcache;
+    int S;
+    const float2* rope_tab;  // [S][HD/2] (cos, sin)
+    int* state;        // [0] position, [3] epoch base (advanced by L at the end of every launch)
+    uint64_t* ll;      // exchange words, two parities
+    int* err;          // set to 1 when a wait timed out
+    float eps;
+    int per_head;      // QK-norm: one RMS per head (else over the whole q / k vector)
+};
+
+__device__ inline void ll_put(uint64_t* p, unsigned ep, float v) {
+    __hip_atomic_store(p, ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t ll_get(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline bool ll_ok(uint64_t w, unsigned ep) { return (unsigned)(w >> 32) == ep; }
+__device__ inline float ll_val(uint64_t w) { return __uint_as_float((unsigned)w); }
+
+// Waits for N words at base[idx[j]] to carry epoch ep (or the block to be marked dead).
+template <int N>
+__device__ inline void ll_wait(const uint64_t* base, const int (&idx)[N], float (&out)[N], unsigned ep,
+                               volatile int* dead, int* err) {
+    uint64_t w[N];
+#pragma unroll
+    for (int j = 0; j < N; j++) w[j] = idx[j] >= 0 ? ll_get(base + idx[j]) : ((uint64_t)ep << 32);
+    unsigned spins = 0;
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < N; j++) ok &= ll_ok(w[j], ep);
+        if (ok || *dead) break;
+        if (++spins > kSpinLimit) {
+            *dead = 1;
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int j = 0; j < N; j++)
+            if (!ll_ok(w[j], ep)) w[j] = ll_get(base + idx[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < N; j++) out[j] = ll_val(w[j]);
+}
+
+// Block barrier over LDS only: waits for this wave's LDS operations, not for its global loads
+// and stores (the prefetched weight rows stay in flight across it).
+__device__ inline void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// A copy of the thread index the compiler cannot see through, taken at the start of every stage: the
+// per-thread addresses are then computed inside the stage instead of being hoisted out of the layer
+// loop and held in registers across all stages.
+#define STAGE_IDS()                                            \
+    int tid = tid0;                                            \
+    asm volatile("" : "+v"(tid));                              \
+    const int lane = tid & 63;                                 \
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); \
+    (void)lane;                                                \
+    (void)wave
+
+// Sum over the block's threads (every thread gets the total, summed in wavefront order).
+__device__ inline float block_sum(float v, float* red, int lane, int wave) {
+    v = gemv::dpp_sum_lane63(v);
+    if (lane == 63) red[wave] = v;
+    lds_barrier();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kPW; w++) t += red[w];
+    return t;
+}
+
+template <int DIM, int F, int H, int KV, int HD>
+__global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
+    constexpr int QD = H * HD, KVD = KV * HD, QKVD = QD + 2 * KVD, G = H / KV, FD = HD / 2;
+    // P1: RPWq rows per wavefront, NCq 256-column chunks per row
+    constexpr int RQ = QKVD / kPB, RPWq = RQ / kPW, NCq = DIM / 256;
+    // P3 / P5: RO (= RD) rows per block, each split over WPR wavefronts
+    constexpr int RO = DIM / kPB, WPR = kPW / RO, NCo = QD / (WPR * 256), NCd = F / (WPR * 256);
+    // P4: RG gate/up row pairs per block; wavefronts 0..kPW/2-1 take gate rows, the rest up rows
+    constexpr int RG = F / kPB, RPWg = 2 * RG / kPW, NCg = DIM / 256;
+    static_assert(QKVD % kPB == 0 && RQ % kPW == 0 && RPWq >= 1, "QKV rows must split over the waves");
+    static_assert(DIM % 256 == 0 && DIM % kPB == 0 && RO >= 1 && kPW % RO == 0, "dim must split over the waves");
+    static_assert(QD % (WPR * 256) == 0 && F % (WPR * 256) == 0, "O / down columns must split over the waves");
+    static_assert(F % kPB == 0 && (2 * RG) % kPW == 0 && RG % RPWg == 0 && 2 * RG <= 64, "gate/up rows");
+    static_assert(HD == 128 || HD == 64, "head size");
+    constexpr int XMAX = QD > F ? (QD > DIM ? QD : DIM) : (F > DIM ? F : DIM);
+    // exchange layout per parity (words)
+    constexpr int OFF_XA = 0, OFF_XM = DIM, OFF_QKV = 2 * DIM, OFF_PART = OFF_QKV + QKVD;
+    constexpr int PART_STRIDE = HD + 2;  // o[HD], max (natural log units), sum
+    constexpr int OFF_A = OFF_PART + KV * kSMax * G * PART_STRIDE;  // merged attention output [QD]
+    constexpr int OFF_H = OFF_A + QD;
+    constexpr int PAR_WORDS = OFF_H + F;
+    static_assert(KV * kSMax <= kPB - H && QD % kPT == 0, "attention and merge blocks must not overlap");
+
+    __shared__ __attribute__((aligned(16))) float xr[DIM];    // layer input x_l
+    __shared__ __attribute__((aligned(16))) float xmr[DIM];   // x_mid (after the O residual)
+    __shared__ __attribute__((aligned(16))) float xin[XMAX];  // the stage's GEMV input
+    __shared__ float red[kPW];
+    __shared__ float rows_s[64];
+    // attention
+    __shared__ __attribute__((aligned(16))) float qraw[G][HD];
+    __shared__ __attribute__((aligned(16))) float q_s[G][HD];
+    __shared__ __attribute__((aligned(16))) float kraw[HD];
+    __shared__ __attribute__((aligned(16))) float k_new[HD];
+    __shared__ __attribute__((aligned(16))) float v_new[HD];
+    __shared__ float rnorm[G + 1];
+    __shared__ float2 red2[kPW];
+    __shared__ __attribute__((aligned(16))) float red_acc[kPW][G][HD];
+    __shared__ float red_m[kPW][G], red_l[kPW][G];
+    __shared__ __attribute__((aligned(16))) float mrg_o[kSMax][HD];  // split merge
+    __shared__ float2 mrg_ml[kSMax];
+    __shared__ int dead_s;
+
+    const int tid0 = threadIdx.x, b = blockIdx.x;
+    volatile int* dead = &dead_s;
+    if (tid0 == 0) dead_s = 0;
+    const int pos = p.state[0];
+    const unsigned base = (unsigned)p.state[3];
+    if (pos < 0 || pos >= p.S) {  // the host never steps past the cache; every block takes this exit
+        if (b == 0 && tid0 == 0) __hip_atomic_store(p.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const int n = pos + 1;
+    int nsplit = (n + kRowsPerSplit - 1) / kRowsPerSplit;
+    nsplit = nsplit < 1 ? 1 : (nsplit > kSMax ? kSMax : nsplit);
+    const int tile = (n + nsplit - 1) / nsplit;
+    const float2* rope_row = p.rope_tab + (size_t)pos * FD;
+    __syncthreads();
+
+    for (int l = 0; l < p.L; l++) {
+        const PLayer Ly = p.layers[l];
+        const unsigned ep = base + (unsigned)l + 1u;
+        uint64_t* cur = p.ll + (size_t)(l & 1) * PAR_WORDS;
+        const uint64_t* prev = p.ll + (size_t)((l + 1) & 1) * PAR_WORDS;
+
+        // ================= P1: QKV =================================================
+        lds_barrier();  // the previous layer's readers of xin / xr are done
+        {
+        STAGE_IDS();
+        float4 wq[RPWq][NCq];
+        {
+            const int r0 = b * RQ + wave * RPWq;
+#pragma unroll
+            for (int i = 0; i < RPWq; i++)
+#pragma unroll
+                for (int c = 0; c < NCq; c++)
+                    wq[i][c] = *reinterpret_cast<const float4*>(Ly.wqkv + (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
+        }
+        {
+            constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+            float xv[NX];
+            if (l == 0) {
+#pragma unroll
+                for (int j = 0; j < NX; j++) xv[j] = tid + j * kPT < DIM ? p.x[tid + j * kPT] : 0.f;
+            } else {
+                int idx[NX];
+#pragma unroll
+                for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XA + tid + j * kPT : -1;
+                ll_wait<NX>(prev, idx, xv, base + (unsigned)l, dead, p.err);
+            }
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < NX; j++) {
+                const int i = tid + j * kPT;
+                if (i < DIM) {
+                    ss = fmaf(xv[j], xv[j], ss);
+                    xr[i] = xv[j];
+                    xin[i] = xv[j] * Ly.attn_norm[i];
+                }
+            }
+            const float tot = block_sum(ss, red, lane, wave);  // (its barrier also publishes xr / xin)
+            const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
+#pragma unroll
+            for (int i = 0; i < RPWq; i++) {
+                float a = 0.f;
+#pragma unroll
+                for (int c = 0; c < NCq; c++) {
+                    const float4 xx = *reinterpret_cast<const float4*>(&xin[c * 256 + lane * 4]);
+                    a = fmaf(wq[i][c].x, xx.x, a);
+                    a = fmaf(wq[i][c].y, xx.y, a);
+                    a = fmaf(wq[i][c].z, xx.z, a);
+                    a = fmaf(wq[i][c].w, xx.w, a);
+                }
+                a = gemv::dpp_sum_lane63(a) * rn;
+                if (lane == 63) {
+                    const int row = b * RQ + wave * RPWq + i;
+                    ll_put(cur + OFF_QKV + row, ep, Ly.bqkv ? a + Ly.bqkv[row] : a);
+                }
+            }
+        }
+        }
+
+        // ================= P2: attention (blocks of (KV head, split)) ==============
+        if (b < KV * nsplit) {
+            STAGE_IDS();
+            constexpr int EPL = HD / 16, NGR = kPT / 16, RU = 2;
+            const int g = b / nsplit, s = b - g * nsplit;
+            const int t0 = s * tile, t1 = min(t0 + tile, n);
+            const int grp = tid >> 4, gl = tid & 15;
+            const size_t head_base = ((size_t)l * KV + g) * (size_t)p.S * HD;
+            float* kc = p.kcache + head_base;
+            float* vc = p.vcache + head_base;
+            auto dim_of = [&](int e) { return 16 * (e & ~3) + gl * 4 + (e & 3); };
+            float kr[RU][EPL], vr[RU][EPL];
+            auto load_rows = [&](float (&dst)[RU][EPL], const float* src, int c) {
+#pragma unroll
+                for (int j = 0; j < RU; j++) {
+                    const int t = min(t0 + grp + NGR * (c * RU + j), t1 - 1);
+#pragma unroll
+                    for (int e = 0; e < EPL; e += 4) {
+                        const float4 v = *reinterpret_cast<const float4*>(src + (size_t)t * HD + 16 * e + gl * 4);
+                        dst[j][e] = v.x; dst[j][e + 1] = v.y; dst[j][e + 2] = v.z; dst[j][e + 3] = v.w;
+                    }
+                }
+            };
+            const int nch = t1 > t0 ? (t1 - t0 + NGR * RU - 1) / (NGR * RU) : 0;
+            if (nch > 0) {  // cache rows before pos are final: issued before the wait for q / k / v
+                load_rows(kr, kc, 0);
+                load_rows(vr, vc, 0);
+            }
+            // this step's q and k (all of both for the whole-vector QK-norm, else the G heads and KV
+            // head g) and v of KV head g
+            {
+                constexpr int NQW = QD + KVD + HD;
+                constexpr int NQ = (NQW + kPT - 1) / kPT;
+                int idx[NQ];
+#pragma unroll
+                for (int j = 0; j < NQ; j++) {
+                    const int i = tid + j * kPT;
+                    int w = -1;
+                    if (i < QD) {
+                        if (!p.per_head || i / (G * HD) == g) w = OFF_QKV + i;
+                    } else if (i < QD + KVD) {
+                        if (!p.per_head || (i - QD) / HD == g) w = OFF_QKV + i;
+                    } else if (i < NQW) {
+                        w = OFF_QKV + QD + KVD + g * HD + (i - QD - KVD);
+                    }
+                    idx[j] = w;
+                }
+                float qv[NQ];
+                ll_wait<NQ>(cur, idx, qv, ep, dead, p.err);
+                float sq = 0.f, sk = 0.f;  // words not waited for read as 0
+#pragma unroll
+                for (int j = 0; j < NQ; j++) {
+                    const int i = tid + j * kPT;
+                    if (i < QD) {
+                        sq = fmaf(qv[j], qv[j], sq);
+                        if (i / (G * HD) == g) qraw[(i - g * G * HD) / HD][i % HD] = qv[j];
+                    } else if (i < QD + KVD) {
+                        sk = fmaf(qv[j], qv[j], sk);
+                        if ((i - QD) / HD == g) kraw[(i - QD) % HD] = qv[j];
+                    } else if (i < NQW) {
+                        v_new[i - QD - KVD] = qv[j];
+                    }
+                }
+                sq = gemv::dpp_sum_lane63(sq);
+                sk = gemv::dpp_sum_lane63(sk);
+                if (lane == 63) red2[wave] = make_float2(sq, sk);
+            }
+            lds_barrier();
+            if (p.per_head) {  // wavefront w reduces vector w (q heads, then k)
+                for (int j = wave; j < G + 1; j += kPW) {
+                    const float* src = j < G ? qraw[j] : kraw;
+                    float sq = 0.f;
+                    for (int i = lane; i < HD; i += 64) sq = fmaf(src[i], src[i], sq);
+                    sq = gemv::dpp_sum_lane63(sq);
+                    if (lane == 63) rnorm[j] = 1.0f / sqrtf(sq / (float)HD + p.eps);
+                }
+            } else if (tid == 0) {  // one RMS over the whole q and the whole k vector
+                float tq = 0.f, tk = 0.f;
+#pragma unroll
+                for (int w = 0; w < kPW; w++) {
+                    tq += red2[w].x;
+                    tk += red2[w].y;
+                }
+                const float rq = 1.0f / sqrtf(tq / (float)QD + p.eps), rk = 1.0f / sqrtf(tk / (float)KVD + p.eps);
+#pragma unroll
+                for (int j = 0; j < G; j++) rnorm[j] = rq;
+                rnorm[G] = rk;
+            }
+            lds_barrier();
+            const bool has_pos = pos >= t0 && pos < t1;
+            // normalised, rotated q (G heads) and k; the block holding pos writes the cache rows
+            for (int idx = tid; idx < (G + 1) * FD; idx += kPT) {
+                const int j = idx / FD, f = idx - j * FD;
+                const float2 cs = rope_row[f];
+                if (j < G) {
+                    float x1 = qraw[j][f], x2 = qraw[j][f + FD];
+                    if (Ly.q_norm) {  // gains span the whole q vector
+                        const float* gq = Ly.q_norm + (size_t)(g * G + j) * HD;
+                        x1 = (gq[f] * x1) * rnorm[j];
+                        x2 = (gq[f + FD] * x2) * rnorm[j];
+                    }
+                    q_s[j][f] = x1 * cs.x - x2 * cs.y;
+                    q_s[j][f + FD] = x2 * cs.x + x1 * cs.y;
+                } else {
+                    float x1 = kraw[f], x2 = kraw[f + FD];
+                    if (Ly.k_norm) {
+                        const float* gk = Ly.k_norm + (size_t)g * HD;
+                        x1 = (gk[f] * x1) * rnorm[G];
+                        x2 = (gk[f + FD] * x2) * rnorm[G];
+                    }
+                    const float o1 = x1 * cs.x - x2 * cs.y, o2 = x2 * cs.x + x1 * cs.y;
+                    k_new[f] = o1;
+                    k_new[f + FD] = o2;
+                    if (has_pos) {
+                        kc[(size_t)pos * HD + f] = o1;
+                        kc[(size_t)pos * HD + f + FD] = o2;
+                    }
+                }
+            }
+            if (has_pos && tid < HD) vc[(size_t)pos * HD + tid] = v_new[tid];
+            lds_barrier();
+
+            const float c2 = 1.4426950408889634f / sqrtf((float)HD);
+            float qf[G][EPL];
+#pragma unroll
+            for (int gg = 0; gg < G; gg++)
+#pragma unroll
+                for (int e = 0; e < EPL; e += 4) {
+                    const float4 t = *reinterpret_cast<const float4*>(&q_s[gg][dim_of(e)]);
+                    qf[gg][e] = t.x * c2; qf[gg][e + 1] = t.y * c2; qf[gg][e + 2] = t.z * c2; qf[gg][e + 3] = t.w * c2;
+                }
+            float m[G], lsum[G], acc[G][EPL];
+#pragma unroll
+            for (int gg = 0; gg < G; gg++) {
+                m[gg] = -INFINITY;
+                lsum[gg] = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) acc[gg][e] = 0.f;
+            }
+            for (int c = 0; c < nch; c++) {
+                if (has_pos) {
+#pragma unroll
+                    for (int j = 0; j < RU; j++)
+                        if (min(t0 + grp + NGR * (c * RU + j), t1 - 1) == pos)
+#pragma unroll
+                            for (int e = 0; e < EPL; e++) {
+                                kr[j][e] = k_new[dim_of(e)];
+                                vr[j][e] = v_new[dim_of(e)];
+                            }
+                }
+                float sc[G][RU];
+#pragma unroll
+                for (int j = 0; j < RU; j++) {
+                    const bool valid = t0 + grp + NGR * (c * RU + j) < t1;
+#pragma unroll
+                    for (int gg = 0; gg < G; gg++) {
+                        float d = 0.f;
+#pragma unroll
+                        for (int e = 0; e < EPL; e++) d = fmaf(qf[gg][e], kr[j][e], d);
+                        // sum over the 16 lanes of the row group (quad swaps, half-row and row mirrors)
+                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0xB1, 0xF, 0xF, true));
+                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x4E, 0xF, 0xF, true));
+                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x141, 0xF, 0xF, true));
+                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x140, 0xF, 0xF, true));
+                        sc[gg][j] = valid ? d : -INFINITY;
+                    }
+                }
+                if (c + 1 < nch) load_rows(kr, kc, c + 1);
+#pragma unroll
+                for (int gg = 0; gg < G; gg++) {
+                    float mc = sc[gg][0];
+#pragma unroll
+                    for (int j = 1; j < RU; j++) mc = fmaxf(mc, sc[gg][j]);
+                    const float mn = fmaxf(m[gg], mc);
+                    if (mn == -INFINITY) continue;
+                    const float alpha = (m[gg] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[gg] - mn);
+                    lsum[gg] *= alpha;
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) acc[gg][e] *= alpha;
+#pragma unroll
+                    for (int j = 0; j < RU; j++) {
+                        const float pj = __builtin_amdgcn_exp2f(sc[gg][j] - mn);
+                        lsum[gg] += pj;
+#pragma unroll
+                        for (int e = 0; e < EPL; e++) acc[gg][e] = fmaf(pj, vr[j][e], acc[gg][e]);
+                    }
+                    m[gg] = mn;
+                }
+                if (c + 1 < nch) load_rows(vr, vc, c + 1);
+            }
+            // merge the row groups: the four of a wavefront by lane swaps, the wavefronts via LDS
+            auto merge_with = [&](int xmask) {
+#pragma unroll
+                for (int gg = 0; gg < G; gg++) {
+                    const float mo = __shfl_xor(m[gg], xmask, 64), lo = __shfl_xor(lsum[gg], xmask, 64);
+                    const float mn = fmaxf(m[gg], mo);
+                    const float a = (m[gg] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[gg] - mn);
+                    const float bo = (mo == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mo - mn);
+                    lsum[gg] = lsum[gg] * a + lo * bo;
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) acc[gg][e] = acc[gg][e] * a + __shfl_xor(acc[gg][e], xmask, 64) * bo;
+                    m[gg] = mn;
+                }
+            };
+            merge_with(16);
+            merge_with(32);
+            if (lane < 16) {
+#pragma unroll
+                for (int gg = 0; gg < G; gg++) {
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) red_acc[wave][gg][dim_of(e)] = acc[gg][e];
+                    if (lane == 0) {
+                        red_m[wave][gg] = m[gg];
+                        red_l[wave][gg] = lsum[gg];
+                    }
+                }
+            }
+            lds_barrier();
+            for (int idx = tid; idx < G * HD; idx += kPT) {
+                const int gg = idx / HD, i = idx - gg * HD;
+                float M = -INFINITY;
+#pragma unroll
+                for (int w = 0; w < kPW; w++) M = fmaxf(M, red_m[w][gg]);
+                float Ls = 0.f, o = 0.f;
+#pragma unroll
+                for (int w = 0; w < kPW; w++) {
+                    const float wt = (red_m[w][gg] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(red_m[w][gg] - M);
+                    Ls = fmaf(red_l[w][gg], wt, Ls);
+                    o = fmaf(red_acc[w][gg][i], wt, o);
+                }
+                uint64_t* slot = cur + OFF_PART + ((g * kSMax + s) * G + gg) * PART_STRIDE;
+                ll_put(slot + i, ep, o);
+                if (i == 0) {
+                    ll_put(slot + HD, ep, M * 0.6931471805599453f);  // natural-log units
+                    ll_put(slot + HD + 1, ep, Ls);
+                }
+            }
+        }
+
+        // ================= P2b: merge the splits of each query head ==================
+        if (b >= kPB - H) {  // one block per query head (never an attention block)
+            STAGE_IDS();
+            // thread t: dimension t % HD of splits (t / HD) * SPT .. + SPT - 1
+            constexpr int SPT = kSMax * HD / kPT;
+            static_assert(kSMax * HD % kPT == 0 && SPT >= 1, "split merge: threads per split");
+            const int h = b - (kPB - H), kvh = h / G, gg = h - kvh * G;
+            const int i = tid % HD, s0 = (tid / HD) * SPT;
+            int idx[3 * SPT];
+#pragma unroll
+            for (int k = 0; k < SPT; k++) {
+                const int s = s0 + k;
+                const int slot = OFF_PART + ((kvh * kSMax + s) * G + gg) * PART_STRIDE;
+                idx[3 * k] = s < nsplit ? slot + i : -1;
+                idx[3 * k + 1] = s < nsplit && i == 0 ? slot + HD : -1;
+                idx[3 * k + 2] = s < nsplit && i == 0 ? slot + HD + 1 : -1;
+            }
+            float v[3 * SPT];
+            ll_wait<3 * SPT>(cur, idx, v, ep, dead, p.err);
+#pragma unroll
+            for (int k = 0; k < SPT; k++) {
+                mrg_o[s0 + k][i] = v[3 * k];
+                if (i == 0) {
+                    mrg_ml[s0 + k] = make_float2(s0 + k < nsplit ? v[3 * k + 1] : -INFINITY, v[3 * k + 2]);
+                }
+            }
+            lds_barrier();
+            if (tid < HD) {
+                float M = -INFINITY;
+#pragma unroll
+                for (int s = 0; s < kSMax; s++)
+                    if (s < nsplit) M = fmaxf(M, mrg_ml[s].x);
+                float Ls = 0.f, o = 0.f;
+#pragma unroll
+                for (int s = 0; s < kSMax; s++)
+                    if (s < nsplit) {
+                        const float w = expf(mrg_ml[s].x - M);
+                        Ls = fmaf(mrg_ml[s].y, w, Ls);
+                        o = fmaf(mrg_o[s][tid], w, o);
+                    }
+                ll_put(cur + OFF_A + h * HD + tid, ep, o / Ls);
+            }
+        }
+
+        // ================= P3: O projection + residual ==============================
+        lds_barrier();  // xin readers (P1) are done
+        {
+            STAGE_IDS();
+            const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
+            float4 wo[NCo];
+#pragma unroll
+            for (int c = 0; c < NCo; c++)
+                wo[c] = *reinterpret_cast<const float4*>(Ly.wo + (size_t)row * QD + col0 + c * 256 + lane * 4);
+            constexpr int NA = QD / kPT;
+            int idx[NA];
+#pragma unroll
+            for (int j = 0; j < NA; j++) idx[j] = OFF_A + tid + j * kPT;
+            float av[NA];
+            ll_wait<NA>(cur, idx, av, ep, dead, p.err);
+#pragma unroll
+            for (int j = 0; j < NA; j++) xin[tid + j * kPT] = av[j];
+            lds_barrier();
+            float a = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCo; c++) {
+                const float4 xx = *reinterpret_cast<const float4*>(&xin[col0 + c * 256 + lane * 4]);
+                a = fmaf(wo[c].x, xx.x, a);
+                a = fmaf(wo[c].y, xx.y, a);
+                a = fmaf(wo[c].z, xx.z, a);
+                a = fmaf(wo[c].w, xx.w, a);
+            }
+            a = gemv::dpp_sum_lane63(a);
+            if (lane == 63) rows_s[wave] = a;
+            lds_barrier();
+            if (tid < RO) {
+                float sum = 0.f;
+#pragma unroll
+                for (int k = 0; k < WPR; k++) sum += rows_s[tid * WPR + k];
+                const int r = b * RO + tid;
+                ll_put(cur + OFF_XM + r, ep, xr[r] + sum);
+            }
+        }
+
+        // ================= P4: gate/up + SwiGLU =====================================
+        lds_barrier();  // xin / rows_s readers (P3) are done
+        {
+            STAGE_IDS();
+            const bool up = wave >= kPW / 2;
+            const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
+            const float* W = up ? Ly.w3 : Ly.w1;
+            float4 wg[RPWg][NCg];
+#pragma unroll
+            for (int i = 0; i < RPWg; i++)
+#pragma unroll
+                for (int c = 0; c < NCg; c++)
+                    wg[i][c] = *reinterpret_cast<const float4*>(W + (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
+            constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+            int idx[NX];
+#pragma unroll
+            for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XM + tid + j * kPT : -1;
+            float xv[NX];
+            ll_wait<NX>(cur, idx, xv, ep, dead, p.err);
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < NX; j++) {
+                const int i = tid + j * kPT;
+                if (i < DIM) {
+                    ss = fmaf(xv[j], xv[j], ss);
+                    xmr[i] = xv[j];
+                    xin[i] = xv[j] * Ly.ffn_norm[i];
+                }
+            }
+            const float tot = block_sum(ss, red, lane, wave);
+            const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
+#pragma unroll
+            for (int i = 0; i < RPWg; i++) {
+                float a = 0.f;
+#pragma unroll
+                for (int c = 0; c < NCg; c++) {
+                    const float4 xx = *reinterpret_cast<const float4*>(&xin[c * 256 + lane * 4]);
+                    a = fmaf(wg[i][c].x, xx.x, a);
+                    a = fmaf(wg[i][c].y, xx.y, a);
+                    a = fmaf(wg[i][c].z, xx.z, a);
+                    a = fmaf(wg[i][c].w, xx.w, a);
+                }
+                a = gemv::dpp_sum_lane63(a) * rn;
+                if (lane == 63) rows_s[wave * RPWg + i] = a;
+            }
+            lds_barrier();
+            if (tid < RG) {
+                const float gt = rows_s[tid], u = rows_s[RG + tid];
+                const float sg = 1.0f / (expf(-gt) + 1.0f);
+                ll_put(cur + OFF_H + b * RG + tid, ep, u * (gt * sg));
+            }
+        }
+
+        // ================= P5: down + residual ======================================
+        lds_barrier();  // xin / rows_s readers (P4) are done
+        {
+            STAGE_IDS();
+            const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (F / WPR);
+            float4 wd[NCd];
+#pragma unroll
+            for (int c = 0; c < NCd; c++)
+                wd[c] = *reinterpret_cast<const float4*>(Ly.w2 + (size_t)row * F + col0 + c * 256 + lane * 4);
+            constexpr int NH = F / kPT > 0 ? (F + kPT - 1) / kPT : 1;
+            int idx[NH];
+#pragma unroll
+            for (int j = 0; j < NH; j++) idx[j] = tid + j * kPT < F ? OFF_H + tid + j * kPT : -1;
+            float hv[NH];
+            ll_wait<NH>(cur, idx, hv, ep, dead, p.err);
+#pragma unroll
+            for (int j = 0; j < NH; j++)
+                if (tid + j * kPT < F) xin[tid + j * kPT] = hv[j];
+            lds_barrier();
+            float a = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCd; c++) {
+                const float4 xx = *reinterpret_cast<const float4*>(&xin[col0 + c * 256 + lane * 4]);
+                a = fmaf(wd[c].x, xx.x, a);
+                a = fmaf(wd[c].y, xx.y, a);
+                a = fmaf(wd[c].z, xx.z, a);
+                a = fmaf(wd[c].w, xx.w, a);
+            }
+            a = gemv::dpp_sum_lane63(a);
+            if (lane == 63) rows_s[wave] = a;
+            lds_barrier();
+            if (tid < RO) {
+                float sum = 0.f;
+#pragma unroll
+                for (int k = 0; k < WPR; k++) sum += rows_s[tid * WPR + k];
+                const int r = b * RO + tid;
+                const float xn = xmr[r] + sum;
+                ll_put(cur + OFF_XA + r, ep, xn);
+                if (l + 1 == p.L) p.x[r] = xn;
+            }
+        }
+    }
+    // every block read the epoch base before block 0 could get here (block 0's last stage waited
+    // for every block's gate/up output), so the next launch's base can be published now
+    if (b == 0 && tid0 == 0) p.state[3] = (int)(base + (unsigned)p.L);
+}
+
+template <int DIM, int F, int H, int KV, int HD>
+constexpr size_t ll_words() {
+    constexpr int QD = H * HD, KVD = KV * HD, G = H / KV;
+    return 2 * (size_t)(2 * DIM + QD + 2 * KVD + KV * kSMax * G * (HD + 2) + QD + F);
+}
+
+template <int DIM, int F, int H, int KV, int HD>
+int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
+    PParams p;
+    p.layers = reinterpret_cast<const PLayer*>(a.layers);
+    p.L = a.layer_count;
+    p.x = a.x; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.max_seq; p.rope_tab = a.rope_tab;
+    p.state = a.state; p.ll = a.ll; p.err = a.err; p.eps = a.eps; p.per_head = a.per_head_norm;
+    auto kern = decode_persistent_kernel<DIM, F, H, KV, HD>;
+    AR_HIP_TRY(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kPadLds));
+    void* args[] = {&p};
+    AR_HIP_TRY(hipLaunchCooperativeKernel((const void*)kern, dim3(kPB), dim3(kPT), args, kPadLds, st));
+    return AR_HIP_OK;
+}
+
+template <int DIM, int F, int H, int KV, int HD>
+int fits_t(int* blocks_per_cu) {
+    auto kern = decode_persistent_kernel<DIM, F, H, KV, HD>;
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kPadLds) != hipSuccess)
+        return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (const void*)kern, kPT, kPadLds) != hipSuccess)
+        return 0;
+    return 1;
+}
+
+}  // namespace
+
+size_t decode_persistent_layer_bytes() { return sizeof(PLayer); }
+
+size_t decode_persistent_ll_words(int dim, int F, int heads, int kv_heads, int hd) {
+    if (dim == 1024 && F == 3072 && heads == 16 && kv_heads == 8 && hd == 128) return ll_words<1024, 3072, 16, 8, 128>();
+    return 0;
+}
+
+int decode_persistent_layer_entry(void* dst, const float* wqkv, const float* wo, const float* w1, const float* w3,
+                                  const float* w2, const float* attn_norm, const float* ffn_norm, const float* q_norm,
+                                  const float* k_norm, const float* bqkv) {
+    PLayer e{wqkv, wo, w1, w3, w2, attn_norm, ffn_norm, q_norm, k_norm, bqkv};
+    __builtin_memcpy(dst, &e, sizeof(e));
+    return AR_HIP_OK;
+}
+
+bool decode_persistent_supported(int dim, int F, int heads, int kv_heads, int hd) {
+    if (decode_persistent_ll_words(dim, F, heads, kv_heads, hd) == 0) return false;
+    int dev = 0, coop = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop) return false;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+    if (!fits_t<1024, 3072, 16, 8, 128>(&per_cu)) return false;
+    return per_cu >= 1 && (long long)per_cu * cus >= kPB;
+}
+
+int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t st) {
+    AR_CHECK_ARG(a.layers && a.x && a.kcache && a.vcache && a.rope_tab && a.state && a.ll && a.err && a.layer_count > 0,
+                 "persistent decode: null argument");
+    AR_CHECK_ARG(a.max_seq > 0, "persistent decode: empty cache");
+    if (a.dim == 1024 && a.hidden_dim == 3072 && a.heads == 16 && a.kv_heads == 8 && a.head_dim == 128)
+        return launch_t<1024, 3072, 16, 8, 128>(a, st);
+    ar_set_error("persistent decode: shape dim %d, hidden %d, heads %d/%d, head size %d has no instantiation", a.dim,
+                 a.hidden_dim, a.heads, a.kv_heads, a.head_dim);
+    return AR_HIP_ERR_INVALID;
+}

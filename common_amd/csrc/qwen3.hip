@@ -134,6 +134,14 @@ struct ar_qwen3 {
     bool pf_w16_in_range = true;  // host copy of pf_flag[1] after the fp16 copies were made
     int pf_by_steps = 0;          // prefill calls that went through the decode step
 
+    // persistent decode step (batch 1, fp32 weights and cache): every layer in one cooperative
+    // launch (decode_persistent.hip) between the step-begin kernel and the logits GEMV
+    bool pk_ok = false;          // shape, dtypes and device qualify; buffers below allocated
+    bool pk_on = true;           // ar_hip_qwen3_use_persistent
+    void* pk_layers = nullptr;   // device table of the layers' weight pointers
+    uint64_t* pk_ll = nullptr;   // exchange words
+    int* pk_err = nullptr;       // timeout / position flag of the last launches
+
     int timed = AR_KT_NONE;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
     size_t events_used = 0;
@@ -161,7 +169,7 @@ void release(ar_qwen3* m) {
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
                     m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->smp_rng, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16,
-                    m->pf_flag};
+                    m->pf_flag, m->pk_layers, m->pk_ll, m->pk_err};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     delete m;
@@ -292,6 +300,13 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
     return AR_HIP_ERR_INVALID;
 }
 
+// The persistent kernel runs the layers of the step unless it is switched off, another kernel class
+// of the multi-launch step is being timed, or the prefetch branch (multi-launch only) is on.
+bool persistent_active(const ar_qwen3* m) {
+    return m->pk_ok && m->pk_on && m->prefetch_blocks == 0 &&
+           (m->timed == AR_KT_NONE || m->timed == AR_KT_LOGITS || m->timed == AR_KT_LAYERS);
+}
+
 int enqueue_step(ar_qwen3* m, bool store_logits) {
     const ar_qwen3_cfg& c = m->cfg;
     hipStream_t st = m->ctx->stream;
@@ -327,6 +342,30 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         return timed_end(which);
     };
 
+    if (persistent_active(m)) {
+        const StepPlanes pl = step_planes(m);
+        AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys,
+                                 m->state, B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, st));
+        DecodePersistentLaunch d;
+        d.layers = m->pk_layers; d.layer_count = c.layer_count; d.dim = dim; d.hidden_dim = c.hidden_dim;
+        d.heads = c.head_count; d.kv_heads = c.kv_head_count; d.head_dim = c.head_size; d.x = m->x;
+        d.kcache = (float*)m->kcache; d.vcache = (float*)m->vcache; d.max_seq = m->S; d.rope_tab = m->rope_tab;
+        d.state = m->state; d.ll = m->pk_ll; d.err = m->pk_err; d.eps = (float)c.epsilon;
+        d.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
+        if (m->timed == AR_KT_LAYERS) {  // events on the stream around the cooperative launch
+            AR_TRY(timed_begin(AR_KT_LAYERS));
+            g_launch_timing = nullptr;
+            AR_HIP_TRY(hipEventRecord(timing.start, st));
+            AR_TRY(launch_decode_persistent(d, st));
+            AR_HIP_TRY(hipEventRecord(timing.stop, st));
+            AR_TRY(timed_end(AR_KT_LAYERS));
+        } else {
+            AR_TRY(launch_decode_persistent(d, st));
+        }
+        AR_TRY(timed_class(AR_KT_LOGITS, 0));
+        if (!sample_is_greedy(m->smp_mode, m->smp_temperature)) AR_TRY(enqueue_sample(m));
+        return AR_HIP_OK;
+    }
     const bool pf = m->prefetch_blocks > 0;
     auto prefetch_layer = [&](int l, int ev) -> int {
         AR_HIP_TRY(hipEventRecord(m->fork_ev[ev], st));
@@ -353,7 +392,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
 
 int run_step(ar_qwen3* m, bool store_logits) {
     hipStream_t st = m->ctx->stream;
-    if (!m->use_graph || m->timed != AR_KT_NONE) return enqueue_step(m, store_logits);
+    // (the persistent step is three launches, enqueued directly: a cooperative launch is not captured)
+    if (!m->use_graph || m->timed != AR_KT_NONE || persistent_active(m)) return enqueue_step(m, store_logits);
     hipGraphExec_t& ex = m->graph[store_logits ? 1 : 0];
     if (!ex) {
         hipGraph_t g = nullptr;
@@ -631,6 +671,45 @@ extern "C" int ar_hip_qwen3_set_weight(ar_qwen3* m, const char* key, const void*
     return AR_HIP_OK;
 }
 
+// Decides whether the persistent decode kernel can run this model's step and, the first time it can,
+// allocates its exchange words, error flag and layer table; the table is rewritten on every finalize.
+static int setup_persistent(ar_qwen3* m) {
+    const ar_qwen3_cfg& c = m->cfg;
+    m->pk_ok = false;
+    if (m->B != 1 || c.weight_dtype != AR_DTYPE_F32 || c.kv_dtype == AR_DTYPE_F16) return AR_HIP_OK;
+    if (!decode_persistent_supported(c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size)) return AR_HIP_OK;
+    const size_t eb = decode_persistent_layer_bytes();
+    if (!m->pk_ll) {
+        const size_t words = decode_persistent_ll_words(c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size);
+        AR_TRY(alloc_zero(m, words * 8, (void**)&m->pk_ll));
+        AR_TRY(alloc_zero(m, 64, (void**)&m->pk_err));
+        AR_TRY(alloc_zero(m, eb * c.layer_count, &m->pk_layers));
+    }
+    std::vector<char> tab(eb * c.layer_count);
+    for (int l = 0; l < c.layer_count; l++) {
+        const Layer& L = m->layers[l];
+        AR_TRY(decode_persistent_layer_entry(tab.data() + l * eb, (const float*)L.wqkv, (const float*)L.wo,
+                                             (const float*)L.w1, (const float*)L.w3, (const float*)L.w2, L.attn_norm,
+                                             L.ffn_norm, L.q_norm, L.k_norm, L.bqkv));
+    }
+    AR_HIP_TRY(hipMemcpyAsync(m->pk_layers, tab.data(), tab.size(), hipMemcpyHostToDevice, m->ctx->stream));
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    m->pk_ok = true;
+    return AR_HIP_OK;
+}
+
+// After a synchronisation: reports (and clears) the persistent kernel's error flag.
+static int check_persistent(ar_qwen3* m) {
+    if (!m->pk_err) return AR_HIP_OK;
+    int e = 0;
+    AR_HIP_TRY(hipMemcpy(&e, m->pk_err, sizeof(int), hipMemcpyDeviceToHost));
+    if (!e) return AR_HIP_OK;
+    AR_HIP_TRY(hipMemset(m->pk_err, 0, sizeof(int)));
+    ar_set_error(e == 1 ? "persistent decode step: a cross-block wait timed out (the step's results are invalid)"
+                        : "persistent decode step: position outside the KV cache");
+    return AR_HIP_ERR_HIP;
+}
+
 extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
     AR_CHECK_ARG(m, "null model");
     for (auto& kv : m->slots) {
@@ -650,6 +729,7 @@ extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
         L.k_norm = ks.filled ? (float*)ks.dst : nullptr;
     }
     AR_TRY(invalidate_graphs(m));
+    AR_TRY(setup_persistent(m));
     m->finalized = true;
     return ar_hip_qwen3_reset(m);
 }
@@ -720,6 +800,7 @@ extern "C" int ar_hip_qwen3_next(ar_qwen3* m, int32_t* tokens_out, float* logits
         AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)m->B * m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
                                   st));
     AR_HIP_TRY(hipStreamSynchronize(st));
+    AR_TRY(check_persistent(m));
     m->host_pos++;
     return AR_HIP_OK;
 }
@@ -735,6 +816,7 @@ extern "C" int ar_hip_qwen3_run(ar_qwen3* m, int steps, int32_t* tokens_out) {
             AR_HIP_TRY(hipMemcpyAsync(tokens_out + (size_t)b * steps, m->tokens + (size_t)b * (m->S + 1) + start,
                                       (size_t)steps * 4, hipMemcpyDeviceToHost, st));
     AR_HIP_TRY(hipStreamSynchronize(st));
+    AR_TRY(check_persistent(m));
     m->host_pos += steps;
     return AR_HIP_OK;
 }
@@ -760,7 +842,7 @@ extern "C" int ar_hip_qwen3_hidden(ar_qwen3* m, float* out) {
 
 extern "C" int ar_hip_qwen3_kernel_timing(ar_qwen3* m, int which) {
     AR_CHECK_ARG(m, "null model");
-    AR_CHECK_ARG(which >= AR_KT_NONE && which <= AR_KT_O, "unknown kernel class %d", which);
+    AR_CHECK_ARG(which >= AR_KT_NONE && which <= AR_KT_LAYERS, "unknown kernel class %d", which);
     AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     m->timed = which;
     m->events_used = 0;
@@ -886,6 +968,19 @@ extern "C" int ar_hip_qwen3_set_sampling(ar_qwen3* m, int mode, double temperatu
     m->smp_mode = mode;
     m->smp_temperature = temperature;
     m->smp_top_p = top_p;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_use_persistent(ar_qwen3* m, int enable) {
+    AR_CHECK_ARG(m, "null model");
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    m->pk_on = enable != 0;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_persistent(ar_qwen3* m, int* active) {
+    AR_CHECK_ARG(m && active, "null argument");
+    *active = persistent_active(m) ? 1 : 0;
     return AR_HIP_OK;
 }
 

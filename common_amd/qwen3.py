@@ -17,7 +17,7 @@ import numpy as np
 from . import hardware as hw
 from .config import DTYPE_BF16, Qwen3Config
 
-KT_NONE, KT_LOGITS, KT_GATE_UP, KT_QKV, KT_ATTENTION, KT_DOWN, KT_O = range(7)
+KT_NONE, KT_LOGITS, KT_GATE_UP, KT_QKV, KT_ATTENTION, KT_DOWN, KT_O, KT_LAYERS = range(8)
 
 
 class _Cfg(ctypes.Structure):
@@ -110,6 +110,18 @@ class AutoregressiveModel:
     def use_prefetch(self, blocks: int):
         """Infinity-Cache prefetch of the next layer's weights on a second stream (0 disables)."""
         hw.check(hw.lib().ar_hip_qwen3_use_prefetch(self.handle, int(blocks)))
+
+    def use_persistent(self, enable: bool):
+        """Run the layers of each decode step as one persistent launch when the model qualifies
+        (batch 1, fp32 weights and cache; default on) or as separate launches."""
+        hw.check(hw.lib().ar_hip_qwen3_use_persistent(self.handle, int(enable)))
+
+    @property
+    def persistent(self) -> bool:
+        """Whether the next decode steps run their layers in the persistent kernel."""
+        a = ctypes.c_int()
+        hw.check(hw.lib().ar_hip_qwen3_persistent(self.handle, ctypes.byref(a)))
+        return bool(a.value)
 
     def kernel_timing(self, which: int):
         hw.check(hw.lib().ar_hip_qwen3_kernel_timing(self.handle, which))

@@ -260,6 +260,31 @@ def test_c3_prompt_steps_vs_oracle(ctx):
     assert n >= 130 and distinct >= 16, (n, distinct)
 
 
+def test_c3_persistent_step_matches_multi_launch(ctx):
+    """The persistent decode kernel (every layer of a step in one cooperative launch, stages
+    exchanging epoch-tagged words) against the same steps as separate launches, on one C3-shape
+    model: the 128-token prompt token by token, then 24 greedy steps (positions 0..151: one to five
+    attention splits per KV head).  Tokens equal (up to a near-tie of the multi-launch logits) and
+    logits within 1e-5 relative at every step; the model reports the persistent kernel active only
+    while it is switched on."""
+    cfg = C.C3_0_6B
+    prompt = synthetic.prompt_ids(C.C3_PROMPT, cfg.vocab_size, seed=3)
+    sd = synthetic.state_dict(cfg, seed=3)
+    with Qwen3(cfg, sd, ctx) as m:
+        del sd
+        am = m.model
+        assert am.persistent
+        fed_p, lg_p = gpu_generate(m, prompt, 24)
+        am.use_persistent(False)
+        assert not am.persistent
+        fed_m, lg_m = gpu_generate(m, prompt, 24)
+        am.use_persistent(True)
+        assert am.persistent
+    stop = compare_tokens(fed_p[0], fed_m[0], lg_m[0], len(prompt))
+    assert stop == fed_m.shape[1], f"near-tie at step {stop}"
+    assert rel_err(lg_p[0], lg_m[0]) <= 1e-5
+
+
 @pytest.mark.parametrize("seq_len", [3000, 4500])
 def test_long_context_split_attention(ctx, seq_len):
     """Caches long enough that the decode step cuts the context into up to 128 splits of up to 24 /
