@@ -331,6 +331,12 @@ struct DecodePersistentLaunch {
     int* err = nullptr;        // 1: a cross-block wait timed out; 2: position outside the cache
     float eps = 1e-6f;
     int per_head_norm = 0;
+    // after the last layer: final RMSNorm, logits (stored when logits is non-null) and greedy keys
+    const float* final_norm = nullptr;
+    const float* lm_head = nullptr;
+    int vocab = 0;
+    float* logits = nullptr;
+    unsigned long long* keys = nullptr;  // [kArgmaxSlots], zero before the launch
 };
 size_t decode_persistent_layer_bytes();
 size_t decode_persistent_ll_words(int dim, int F, int heads, int kv_heads, int hd);  // 0: no instantiation

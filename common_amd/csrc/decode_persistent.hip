@@ -1,4 +1,4 @@
-// Persistent decode step: every layer of one batch-1 Qwen3 decode step in one cooperative launch.
+// Persistent decode step: every layer of one batch-1 Qwen3 decode step, then its logits, in one launch.
 //
 // The step the reference builds per layer (engine/ml/.../AttentionFeatures.java:785-929,
 // FeedForwardFeatures.java:147-156, NormalizationLayerFeatures.java:584-595) is five all-to-all
@@ -22,7 +22,8 @@
 //   P2b merge   per query head (one block each): o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s
 //   P3 O        x_mid = x + Wo . o
 //   P4 gate/up  h = (W3 . xn) * silu(W1 . xn), xn = rmsnorm(x_mid) * ffn_norm
-//   P5 down     x' = x_mid + W2 . h          (the last layer also stores x' for the logits GEMV)
+//   P5 down     x' = x_mid + W2 . h          (the last layer also stores x' in the model's x)
+// then once: P6 final RMSNorm, logits (stored when asked), greedy-token keys.
 // The block grid is fixed (one block per CU); the rows of every GEMV divide evenly over it.
 #include <cstdint>
 
@@ -38,6 +39,7 @@ constexpr int kSMax = 8;           // attention splits per KV head
 constexpr int kRowsPerSplit = 32;  // cache rows per split before another split is opened
 constexpr unsigned kSpinLimit = 1u << 18;  // polls before a wait is abandoned (~0.3 s)
 constexpr int kPadLds = 64 * 1024;         // dynamic LDS that keeps a second block off each CU
+constexpr int kMaxLayers = 64;             // layer table held in LDS
 
 struct PLayer {
     const float* wqkv;
@@ -65,7 +67,40 @@ struct PParams {
     int* err;          // set to 1 when a wait timed out
     float eps;
     int per_head;      // QK-norm: one RMS per head (else over the whole q / k vector)
+    // after the last layer: final RMSNorm, logits and greedy-token keys
+    const float* final_norm;
+    const float* lm_head;  // [vocab][dim]
+    int vocab;
+    float* logits;         // [vocab], or null: not stored
+    unsigned long long* keys;  // [kArgmaxSlots] packed (value, index) maxima, zero before the launch
 };
+
+// Loads through pointers read from the layer table.  The compiler sees those pointers as generic,
+// and a generic (flat) load counts against the LDS counter as well as the vector-memory counter (every
+// LDS wait behind it would also wait for the weight rows); they point to device memory, so they are
+// loaded as global.  The base is cast before the offset is added (a cast of a finished per-lane
+// address folds back into a generic load); the host pass compiles these bodies without running them.
+typedef const __attribute__((address_space(1))) float gfloat;
+__device__ inline float4 gld4(const float* base, size_t off) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef float v4 __attribute__((ext_vector_type(4)));
+    const v4 v = *(const __attribute__((address_space(1))) v4*)((gfloat*)base + off);
+    return make_float4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const float4*>(base + off);
+#endif
+}
+__device__ inline float gld(const float* base, size_t off) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return ((gfloat*)base)[off];
+#else
+    return base[off];
+#endif
+}
+// The block's "stop waiting" flag in LDS, through relaxed workgroup-scope atomics (LDS accesses the
+// compiler neither caches in a register nor turns into generic ones).
+__device__ inline int dead_get(int* d) { return __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ inline void dead_set(int* d) { __hip_atomic_store(d, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 
 __device__ inline void ll_put(uint64_t* p, unsigned ep, float v) {
     __hip_atomic_store(p, ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
@@ -80,7 +115,7 @@ __device__ inline float ll_val(uint64_t w) { return __uint_as_float((unsigned)w)
 // Waits for N words at base[idx[j]] to carry epoch ep (or the block to be marked dead).
 template <int N>
 __device__ inline void ll_wait(const uint64_t* base, const int (&idx)[N], float (&out)[N], unsigned ep,
-                               volatile int* dead, int* err) {
+                               int* dead, int* err) {
     uint64_t w[N];
 #pragma unroll
     for (int j = 0; j < N; j++) w[j] = idx[j] >= 0 ? ll_get(base + idx[j]) : ((uint64_t)ep << 32);
@@ -89,9 +124,9 @@ __device__ inline void ll_wait(const uint64_t* base, const int (&idx)[N], float 
         bool ok = true;
 #pragma unroll
         for (int j = 0; j < N; j++) ok &= ll_ok(w[j], ep);
-        if (ok || *dead) break;
+        if (ok || dead_get(dead)) break;
         if (++spins > kSpinLimit) {
-            *dead = 1;
+            dead_set(dead);
             __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
@@ -176,9 +211,12 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     __shared__ __attribute__((aligned(16))) float mrg_o[kSMax][HD];  // split merge
     __shared__ float2 mrg_ml[kSMax];
     __shared__ int dead_s;
+    // the layer table, read from LDS: a global load of it inside the loop would make the wavefront
+    // wait for every weight load it has in flight
+    __shared__ PLayer lay_s[kMaxLayers];
 
     const int tid0 = threadIdx.x, b = blockIdx.x;
-    volatile int* dead = &dead_s;
+    int* dead = &dead_s;
     if (tid0 == 0) dead_s = 0;
     const int pos = p.state[0];
     const unsigned base = (unsigned)p.state[3];
@@ -191,10 +229,12 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     nsplit = nsplit < 1 ? 1 : (nsplit > kSMax ? kSMax : nsplit);
     const int tile = (n + nsplit - 1) / nsplit;
     const float2* rope_row = p.rope_tab + (size_t)pos * FD;
+    for (int i = tid0; i < p.L * (int)(sizeof(PLayer) / 8); i += kPT)
+        reinterpret_cast<uint64_t*>(lay_s)[i] = reinterpret_cast<const uint64_t*>(p.layers)[i];
     __syncthreads();
 
     for (int l = 0; l < p.L; l++) {
-        const PLayer Ly = p.layers[l];
+        const PLayer& Ly = lay_s[l];
         const unsigned ep = base + (unsigned)l + 1u;
         uint64_t* cur = p.ll + (size_t)(l & 1) * PAR_WORDS;
         const uint64_t* prev = p.ll + (size_t)((l + 1) & 1) * PAR_WORDS;
@@ -210,10 +250,14 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             for (int i = 0; i < RPWq; i++)
 #pragma unroll
                 for (int c = 0; c < NCq; c++)
-                    wq[i][c] = *reinterpret_cast<const float4*>(Ly.wqkv + (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
+                    wq[i][c] = gld4(Ly.wqkv, (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
         }
         {
             constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+            // the gains are loaded before the wait, so the wait's completion covers them
+            float gv[NX];
+#pragma unroll
+            for (int j = 0; j < NX; j++) gv[j] = tid + j * kPT < DIM ? gld(Ly.attn_norm, tid + j * kPT) : 0.f;
             float xv[NX];
             if (l == 0) {
 #pragma unroll
@@ -231,7 +275,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 if (i < DIM) {
                     ss = fmaf(xv[j], xv[j], ss);
                     xr[i] = xv[j];
-                    xin[i] = xv[j] * Ly.attn_norm[i];
+                    xin[i] = xv[j] * gv[j];
                 }
             }
             const float tot = block_sum(ss, red, lane, wave);  // (its barrier also publishes xr / xin)
@@ -250,7 +294,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 a = gemv::dpp_sum_lane63(a) * rn;
                 if (lane == 63) {
                     const int row = b * RQ + wave * RPWq + i;
-                    ll_put(cur + OFF_QKV + row, ep, Ly.bqkv ? a + Ly.bqkv[row] : a);
+                    ll_put(cur + OFF_QKV + row, ep, Ly.bqkv ? a + gld(Ly.bqkv, row) : a);
                 }
             }
         }
@@ -284,6 +328,21 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 load_rows(kr, kc, 0);
                 load_rows(vr, vc, 0);
             }
+            // this thread's rotation pair and QK-norm gains, also ahead of the wait
+            static_assert((G + 1) * FD <= kPT, "one rotation pair per thread");
+            const int rj = tid / FD, rf = tid - rj * FD;
+            float2 rcs = make_float2(1.f, 0.f);
+            float rg1 = 1.f, rg2 = 1.f;
+            if (tid < (G + 1) * FD) {
+                rcs = rope_row[rf];
+                const float* gn = rj < G ? Ly.q_norm : Ly.k_norm;
+                const size_t o = rj < G ? (size_t)(g * G + rj) * HD : (size_t)g * HD;
+                if (gn) {
+                    rg1 = gld(gn, o + rf);
+                    rg2 = gld(gn, o + rf + FD);
+                }
+            }
+            asm volatile("" ::: "memory");  // (keeps these loads ahead of the polls)
             // this step's q and k (all of both for the whole-vector QK-norm, else the G heads and KV
             // head g) and v of KV head g
             {
@@ -347,24 +406,22 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             lds_barrier();
             const bool has_pos = pos >= t0 && pos < t1;
             // normalised, rotated q (G heads) and k; the block holding pos writes the cache rows
-            for (int idx = tid; idx < (G + 1) * FD; idx += kPT) {
-                const int j = idx / FD, f = idx - j * FD;
-                const float2 cs = rope_row[f];
+            if (tid < (G + 1) * FD) {
+                const int j = rj, f = rf;
+                const float2 cs = rcs;
                 if (j < G) {
                     float x1 = qraw[j][f], x2 = qraw[j][f + FD];
                     if (Ly.q_norm) {  // gains span the whole q vector
-                        const float* gq = Ly.q_norm + (size_t)(g * G + j) * HD;
-                        x1 = (gq[f] * x1) * rnorm[j];
-                        x2 = (gq[f + FD] * x2) * rnorm[j];
+                        x1 = (rg1 * x1) * rnorm[j];
+                        x2 = (rg2 * x2) * rnorm[j];
                     }
                     q_s[j][f] = x1 * cs.x - x2 * cs.y;
                     q_s[j][f + FD] = x2 * cs.x + x1 * cs.y;
                 } else {
                     float x1 = kraw[f], x2 = kraw[f + FD];
                     if (Ly.k_norm) {
-                        const float* gk = Ly.k_norm + (size_t)g * HD;
-                        x1 = (gk[f] * x1) * rnorm[G];
-                        x2 = (gk[f + FD] * x2) * rnorm[G];
+                        x1 = (rg1 * x1) * rnorm[G];
+                        x2 = (rg2 * x2) * rnorm[G];
                     }
                     const float o1 = x1 * cs.x - x2 * cs.y, o2 = x2 * cs.x + x1 * cs.y;
                     k_new[f] = o1;
@@ -547,7 +604,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             float4 wo[NCo];
 #pragma unroll
             for (int c = 0; c < NCo; c++)
-                wo[c] = *reinterpret_cast<const float4*>(Ly.wo + (size_t)row * QD + col0 + c * 256 + lane * 4);
+                wo[c] = gld4(Ly.wo, (size_t)row * QD + col0 + c * 256 + lane * 4);
             constexpr int NA = QD / kPT;
             int idx[NA];
 #pragma unroll
@@ -590,8 +647,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             for (int i = 0; i < RPWg; i++)
 #pragma unroll
                 for (int c = 0; c < NCg; c++)
-                    wg[i][c] = *reinterpret_cast<const float4*>(W + (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
+                    wg[i][c] = gld4(W, (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
             constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+            float gv[NX];
+#pragma unroll
+            for (int j = 0; j < NX; j++) gv[j] = tid + j * kPT < DIM ? gld(Ly.ffn_norm, tid + j * kPT) : 0.f;
             int idx[NX];
 #pragma unroll
             for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XM + tid + j * kPT : -1;
@@ -604,7 +664,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 if (i < DIM) {
                     ss = fmaf(xv[j], xv[j], ss);
                     xmr[i] = xv[j];
-                    xin[i] = xv[j] * Ly.ffn_norm[i];
+                    xin[i] = xv[j] * gv[j];
                 }
             }
             const float tot = block_sum(ss, red, lane, wave);
@@ -639,7 +699,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             float4 wd[NCd];
 #pragma unroll
             for (int c = 0; c < NCd; c++)
-                wd[c] = *reinterpret_cast<const float4*>(Ly.w2 + (size_t)row * F + col0 + c * 256 + lane * 4);
+                wd[c] = gld4(Ly.w2, (size_t)row * F + col0 + c * 256 + lane * 4);
             constexpr int NH = F / kPT > 0 ? (F + kPT - 1) / kPT : 1;
             int idx[NH];
 #pragma unroll
@@ -673,8 +733,86 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
         }
     }
+
+    // ================= P6: final RMSNorm + logits + greedy keys ======================
+    // (Qwen3.java:401-405; the tied head reads the embedding rows.)  Wavefront gw of the grid takes
+    // RB consecutive vocabulary rows at a time, batches kPB * kPW * RB rows apart (all wavefronts
+    // stream neighbouring rows together), the next batch in flight while one is used (the first
+    // before the wait for x).
+    lds_barrier();
+    {
+        STAGE_IDS();
+        constexpr int RB = 4, NCl = DIM / 256;
+        const int r1 = p.vocab;
+        const int gw = b * kPW + wave;
+        float4 wa[RB][NCl], wb[RB][NCl];
+        auto load_batch = [&](float4 (&w)[RB][NCl], int rbase) {
+#pragma unroll
+            for (int i = 0; i < RB; i++) {
+                const int r = min(rbase + i, r1 - 1);
+#pragma unroll
+                for (int c = 0; c < NCl; c++) w[i][c] = gld4(p.lm_head, (size_t)r * DIM + c * 256 + lane * 4);
+            }
+        };
+        const int first = gw * RB;
+        if (first < r1) load_batch(wa, first);
+        constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+        float gv[NX];
+#pragma unroll
+        for (int j = 0; j < NX; j++) gv[j] = tid + j * kPT < DIM ? gld(p.final_norm, tid + j * kPT) : 0.f;
+        int idx[NX];
+#pragma unroll
+        for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XA + tid + j * kPT : -1;
+        float xv[NX];
+        ll_wait<NX>(p.ll + (size_t)((p.L - 1) & 1) * PAR_WORDS, idx, xv, base + (unsigned)p.L, dead, p.err);
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NX; j++) {
+            const int i = tid + j * kPT;
+            if (i < DIM) {
+                ss = fmaf(xv[j], xv[j], ss);
+                xin[i] = xv[j] * gv[j];
+            }
+        }
+        const float tot = block_sum(ss, red, lane, wave);
+        const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
+        float4 xq[NCl];
+#pragma unroll
+        for (int c = 0; c < NCl; c++) xq[c] = *reinterpret_cast<const float4*>(&xin[c * 256 + lane * 4]);
+        unsigned long long best = 0ull;  // (lane 63)
+        auto use_batch = [&](const float4 (&w)[RB][NCl], int rbase) {
+#pragma unroll
+            for (int i = 0; i < RB; i++) {
+                float a = 0.f;
+#pragma unroll
+                for (int c = 0; c < NCl; c++) {
+                    a = fmaf(w[i][c].x, xq[c].x, a);
+                    a = fmaf(w[i][c].y, xq[c].y, a);
+                    a = fmaf(w[i][c].z, xq[c].z, a);
+                    a = fmaf(w[i][c].w, xq[c].w, a);
+                }
+                a = gemv::dpp_sum_lane63(a) * rn;
+                const int r = rbase + i;
+                if (lane == 63 && r < r1) {
+                    if (p.logits) p.logits[r] = a;
+                    const unsigned long long k = gemv::argmax_key(a, r);
+                    best = k > best ? k : best;
+                }
+            }
+        };
+        constexpr int STEP = RB * kPB * kPW;
+        for (int rb = first; rb < r1; rb += 2 * STEP) {
+            if (rb + STEP < r1) load_batch(wb, rb + STEP);
+            use_batch(wa, rb);
+            if (rb + STEP >= r1) break;
+            if (rb + 2 * STEP < r1) load_batch(wa, rb + 2 * STEP);
+            use_batch(wb, rb + STEP);
+        }
+        if (lane == 63 && best) atomicMax(p.keys + ((b * kPW + wave) & (kArgmaxSlots - 1)), best);
+    }
+
     // every block read the epoch base before block 0 could get here (block 0's last stage waited
-    // for every block's gate/up output), so the next launch's base can be published now
+    // for every block's last output), so the next launch's base can be published now
     if (b == 0 && tid0 == 0) p.state[3] = (int)(base + (unsigned)p.L);
 }
 
@@ -691,10 +829,14 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     p.L = a.layer_count;
     p.x = a.x; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.max_seq; p.rope_tab = a.rope_tab;
     p.state = a.state; p.ll = a.ll; p.err = a.err; p.eps = a.eps; p.per_head = a.per_head_norm;
-    auto kern = decode_persistent_kernel<DIM, F, H, KV, HD>;
-    AR_HIP_TRY(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kPadLds));
-    void* args[] = {&p};
-    AR_HIP_TRY(hipLaunchCooperativeKernel((const void*)kern, dim3(kPB), dim3(kPT), args, kPadLds, st));
+    p.final_norm = a.final_norm; p.lm_head = a.lm_head; p.vocab = a.vocab; p.logits = a.logits; p.keys = a.keys;
+    auto kern = decode_persistent_kernel<DIM, F, H, KV, HD>;  // (its LDS attribute is set by fits_t)
+    // A plain launch (a cooperative one measured ~20 us longer per step): every block must be resident
+    // at once, which decode_persistent_supported checks (one 512-thread block per CU, kPB CUs) and
+    // which holds while nothing else runs on the device; if some block were not, the others' waits
+    // time out, the error flag is set and the launch still completes.
+    hipLaunchKernelGGL(kern, dim3(kPB), dim3(kPT), kPadLds, st, p);
+    AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
 
@@ -727,18 +869,20 @@ int decode_persistent_layer_entry(void* dst, const float* wqkv, const float* wo,
 
 bool decode_persistent_supported(int dim, int F, int heads, int kv_heads, int hd) {
     if (decode_persistent_ll_words(dim, F, heads, kv_heads, hd) == 0) return false;
-    int dev = 0, coop = 0, cus = 0, per_cu = 0;
+    int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
-    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop) return false;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
     if (!fits_t<1024, 3072, 16, 8, 128>(&per_cu)) return false;
     return per_cu >= 1 && (long long)per_cu * cus >= kPB;
 }
 
 int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t st) {
-    AR_CHECK_ARG(a.layers && a.x && a.kcache && a.vcache && a.rope_tab && a.state && a.ll && a.err && a.layer_count > 0,
+    AR_CHECK_ARG(a.layers && a.x && a.kcache && a.vcache && a.rope_tab && a.state && a.ll && a.err && a.layer_count > 0 &&
+                     a.final_norm && a.lm_head && a.keys,
                  "persistent decode: null argument");
+    AR_CHECK_ARG(a.vocab >= kPB, "persistent decode: vocabulary %d below %d rows", a.vocab, kPB);
     AR_CHECK_ARG(a.max_seq > 0, "persistent decode: empty cache");
+    AR_CHECK_ARG(a.layer_count <= kMaxLayers, "persistent decode: %d layers exceed %d", a.layer_count, kMaxLayers);
     if (a.dim == 1024 && a.hidden_dim == 3072 && a.heads == 16 && a.kv_heads == 8 && a.head_dim == 128)
         return launch_t<1024, 3072, 16, 8, 128>(a, st);
     ar_set_error("persistent decode: shape dim %d, hidden %d, heads %d/%d, head size %d has no instantiation", a.dim,

@@ -134,8 +134,8 @@ struct ar_qwen3 {
     bool pf_w16_in_range = true;  // host copy of pf_flag[1] after the fp16 copies were made
     int pf_by_steps = 0;          // prefill calls that went through the decode step
 
-    // persistent decode step (batch 1, fp32 weights and cache): every layer in one cooperative
-    // launch (decode_persistent.hip) between the step-begin kernel and the logits GEMV
+    // persistent decode step (batch 1, fp32 weights and cache): every layer, the final RMSNorm, the
+    // logits and the greedy keys in one launch (decode_persistent.hip) after the step-begin kernel
     bool pk_ok = false;          // shape, dtypes and device qualify; buffers below allocated
     bool pk_on = true;           // ar_hip_qwen3_use_persistent
     void* pk_layers = nullptr;   // device table of the layers' weight pointers
@@ -300,11 +300,10 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
     return AR_HIP_ERR_INVALID;
 }
 
-// The persistent kernel runs the layers of the step unless it is switched off, another kernel class
-// of the multi-launch step is being timed, or the prefetch branch (multi-launch only) is on.
+// The persistent kernel runs the layers and the logits of the step unless it is switched off, a kernel
+// class of the multi-launch step is being timed, or the prefetch branch (multi-launch only) is on.
 bool persistent_active(const ar_qwen3* m) {
-    return m->pk_ok && m->pk_on && m->prefetch_blocks == 0 &&
-           (m->timed == AR_KT_NONE || m->timed == AR_KT_LOGITS || m->timed == AR_KT_LAYERS);
+    return m->pk_ok && m->pk_on && m->prefetch_blocks == 0 && (m->timed == AR_KT_NONE || m->timed == AR_KT_LAYERS);
 }
 
 int enqueue_step(ar_qwen3* m, bool store_logits) {
@@ -352,7 +351,10 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         d.kcache = (float*)m->kcache; d.vcache = (float*)m->vcache; d.max_seq = m->S; d.rope_tab = m->rope_tab;
         d.state = m->state; d.ll = m->pk_ll; d.err = m->pk_err; d.eps = (float)c.epsilon;
         d.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
-        if (m->timed == AR_KT_LAYERS) {  // events on the stream around the cooperative launch
+        const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
+        d.final_norm = m->final_norm; d.lm_head = (const float*)m->lm_head; d.vocab = c.vocab_size;
+        d.logits = (store_logits || sampling) ? m->logits : nullptr; d.keys = m->am_keys;
+        if (m->timed == AR_KT_LAYERS) {  // events on the stream around the launch
             AR_TRY(timed_begin(AR_KT_LAYERS));
             g_launch_timing = nullptr;
             AR_HIP_TRY(hipEventRecord(timing.start, st));
@@ -362,8 +364,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         } else {
             AR_TRY(launch_decode_persistent(d, st));
         }
-        AR_TRY(timed_class(AR_KT_LOGITS, 0));
-        if (!sample_is_greedy(m->smp_mode, m->smp_temperature)) AR_TRY(enqueue_sample(m));
+        if (sampling) AR_TRY(enqueue_sample(m));
         return AR_HIP_OK;
     }
     const bool pf = m->prefetch_blocks > 0;
@@ -392,8 +393,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
 
 int run_step(ar_qwen3* m, bool store_logits) {
     hipStream_t st = m->ctx->stream;
-    // (the persistent step is three launches, enqueued directly: a cooperative launch is not captured)
-    if (!m->use_graph || m->timed != AR_KT_NONE || persistent_active(m)) return enqueue_step(m, store_logits);
+    if (!m->use_graph || m->timed != AR_KT_NONE) return enqueue_step(m, store_logits);
     hipGraphExec_t& ex = m->graph[store_logits ? 1 : 0];
     if (!ex) {
         hipGraph_t g = nullptr;
@@ -974,6 +974,7 @@ extern "C" int ar_hip_qwen3_set_sampling(ar_qwen3* m, int mode, double temperatu
 extern "C" int ar_hip_qwen3_use_persistent(ar_qwen3* m, int enable) {
     AR_CHECK_ARG(m, "null model");
     AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    if (m->pk_on != (enable != 0)) AR_TRY(invalidate_graphs(m));  // the captured step holds either form
     m->pk_on = enable != 0;
     return AR_HIP_OK;
 }

@@ -262,9 +262,9 @@ int ar_hip_qwen3_hidden(ar_qwen3 *m, float *out);
 #define AR_KT_ATTENTION 4
 #define AR_KT_DOWN 5
 #define AR_KT_O 6
-#define AR_KT_LAYERS 7      /* the persistent decode kernel (all layers of the step in one launch) */
-/* Timing a per-layer class (QKV, attention, O, gate/up, down) runs the step as separate launches;
- * AR_KT_LAYERS times the persistent kernel when it runs the step (ar_hip_qwen3_persistent). */
+#define AR_KT_LAYERS 7      /* the persistent decode kernel (layers + logits of the step in one launch) */
+/* Timing one of the classes 1..6 runs the step as separate launches; AR_KT_LAYERS times the
+ * persistent kernel when it runs the step (ar_hip_qwen3_persistent). */
 int ar_hip_qwen3_kernel_timing(ar_qwen3 *m, int which);
 int ar_hip_qwen3_kernel_time(ar_qwen3 *m, double *ms, int *launches);
 /* Loop probe of one decode kernel class (AR_KT_QKV, AR_KT_O, AR_KT_GATE_UP, AR_KT_DOWN or
@@ -279,13 +279,14 @@ int ar_hip_qwen3_kernel_loop(ar_qwen3 *m, int which, int reps, double *us_per_la
 /* Use a captured HIP graph per decode step (1, default) or plain launches (0). */
 int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
 /* Persistent decode step.  For batch 1 with fp32 weights and an fp32 KV cache (on a device that can
- * hold one 512-thread block per CU on every CU at once), the layers of each decode step run as one
- * cooperative launch whose stages exchange data through device-scope words tagged with an epoch,
- * instead of five launches per layer; the step-begin kernel and the logits GEMV stay separate, and
- * the step is not captured into a graph.  No counterpart in the reference (its backend runs the
- * compiled operation list); a throughput option only: results match the multi-launch step within
- * float rounding.  enable 1 (default) or 0; ar_hip_qwen3_persistent reports whether the next steps
- * use it.  A cross-block wait that times out makes the next ar_hip_qwen3_next / run fail with
+ * hold one 512-thread block per CU on 256 CUs at once), the layers and the logits of each decode step
+ * run as one launch whose stages exchange data through device-scope words tagged with an epoch,
+ * instead of five launches per layer and one for the logits; the step-begin kernel stays separate,
+ * and the step is captured into a graph like the multi-launch one.  No counterpart in the reference
+ * (its backend runs the compiled operation list); a throughput option only: results match the
+ * multi-launch step within float rounding.  enable 1 (default) or 0; ar_hip_qwen3_persistent reports
+ * whether the next steps use it.  A cross-block wait that times out (possible only if another
+ * kernel occupied CUs during the step) makes the next ar_hip_qwen3_next / run fail with
  * AR_HIP_ERR_HIP. */
 int ar_hip_qwen3_use_persistent(ar_qwen3 *m, int enable);
 int ar_hip_qwen3_persistent(ar_qwen3 *m, int *active);
