@@ -8,10 +8,14 @@ then exactly `--steps` tokens are timed with the tokens kept on the device (no h
 trip inside the timed region).  Default: warmup 5 + 251 timed = the config's 256 decode tokens.
 
 Extra fields on the JSON line:
-  roofline      dominant kernel's achieved HBM GB/s: its class launched LOOP_ROUNDS times per layer
-                over the layers' weights in one HIP graph, two HIP events around the replay on the
-                model's stream (per-class shares of the step also from HIP events carried in the
-                class's dispatches over --probe-steps decode steps)
+  roofline      dominant kernel's achieved HBM GB/s: the persistent decode kernel (every layer, the
+                final norm, the logits and the greedy keys of a step in one launch), its average
+                launch timed by HIP events on the model's stream over --probe-steps eager steps,
+                against the step's algorithmic bytes
+  multi_launch  the same decode as separate launches per layer (tok/s over MULTI_STEPS steps), each
+                kernel class timed by HIP events carried in its dispatches and by a graph-replayed
+                loop of its launches over the layers (roofline of its dominant class and of its
+                logits GEMV)
   cpu_baseline  the CPU oracle (reference semantics, fp32) on this host, over a bounded sample
   c4            BASELINE config 4 (Qwen3-1.7B shape, bf16 weights): a 2048-token prompt through the
                 MFMA prefill path (tok/s and fraction of the 2.5 PFLOP/s dense bf16/fp16 MFMA peak),
@@ -268,8 +272,9 @@ TRAFFIC_STEPS = 8
 def traffic_probe(args):
     """Workload for the rocprofv3 FETCH_SIZE / WRITE_SIZE passes behind roofline.traffic: one plain
     256 MiB device copy (the counter scale: known bytes), the C3 prompt (128 tokens) through the
-    prefill, then TRAFFIC_STEPS eager C3 decode steps at positions 128.., so every launch of every
-    decode kernel class is its own dispatch."""
+    prefill, then TRAFFIC_STEPS eager C3 decode steps at positions 128.. with the persistent kernel
+    (when the model runs it) and TRAFFIC_STEPS more as separate launches, so every launch of every
+    decode kernel is its own dispatch."""
     from common_amd import config as C
     from common_amd import hardware as hw
     from common_amd import synthetic
@@ -289,12 +294,16 @@ def traffic_probe(args):
             am.set_prompt(prompt)
             am.prefill()
             am.run(TRAFFIC_STEPS)
+            am.use_persistent(False)
+            am.run(TRAFFIC_STEPS)
+            am.use_persistent(True)
             ctx.synchronize()
     print(json.dumps({"traffic_probe": {"copy_bytes": nbytes, "prompt": C.C3_PROMPT, "decode_steps": TRAFFIC_STEPS}}),
           flush=True)
 
 
 PREFILL_PROBE_RUNS = 2
+MULTI_STEPS = 64  # timed steps of the multi-launch comparison run
 LOOP_ROUNDS = 8  # loop probe: launches per layer (x layers) for each weight-streaming decode class
 
 
@@ -330,6 +339,7 @@ def prefill_probe(args):
 
 # kernel-name prefixes of the C3 decode classes in a rocprofv3 trace (batch 1, fp32 weights)
 C3_CLASS_KERNELS = {
+    "decode_persistent": "decode_persistent_kernel",
     "qkv_gemv_rmsnorm": "gemv_rx_kernel<float, 2, 4, 0>",
     "o_gemv_residual": "gemv_rx_kernel<float, 1, 8, 1>",
     "gate_up_gemv_swiglu": "gemv_rx_kernel<float, 2, 4, 2>",
@@ -348,6 +358,8 @@ def c3_class_bytes(cfg, name, pos):
           "down_gemv_residual": q.KT_DOWN, "logits_gemv_argmax": q.KT_LOGITS}
     if name in kt:
         return kernel_bytes(cfg, kt[name])
+    if name == "decode_persistent":  # the whole step but the step-begin kernel (which reads the embedding row)
+        return algorithmic_bytes_per_token(cfg, pos)
     if name == "attention_decode":  # K and V rows 0..pos read, row pos written, q/k/v and gains in, out
         return 2 * (pos + 1) * cfg.kv_dim * 4 + 2 * cfg.kv_dim * 4 + (cfg.q_dim + 2 * cfg.kv_dim) * 4 * 2 + cfg.q_dim * 4
     return None
@@ -371,7 +383,8 @@ def traffic_summary(fetch_dir, write_dir):
 
     out = {"classes": {}}
     cfg = C.C3_0_6B
-    pos_mean = C.C3_PROMPT + (TRAFFIC_STEPS - 1) / 2
+    pos_mean = C.C3_PROMPT + (TRAFFIC_STEPS - 1) / 2  # the persistent steps come first
+    pos_mean_multi = pos_mean + TRAFFIC_STEPS
     for counter, d, key in (("FETCH_SIZE", fetch_dir, "fetch"), ("WRITE_SIZE", write_dir, "write")):
         rows = read(d, counter)
         copy = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
@@ -386,7 +399,7 @@ def traffic_summary(fetch_dir, write_dir):
                 e[f"{key}_bytes_per_launch"] = round(sum(vals) / len(vals))
                 e["launches"] = len(vals)
     for name, e in out["classes"].items():
-        alg = c3_class_bytes(cfg, name, pos_mean)
+        alg = c3_class_bytes(cfg, name, pos_mean if name == "decode_persistent" else pos_mean_multi)
         e["hbm_bytes_per_launch"] = e.get("fetch_bytes_per_launch", 0) + e.get("write_bytes_per_launch", 0)
         e["algorithmic_bytes_per_launch"] = round(alg) if alg else None
         e["traffic_over_algorithmic"] = round(e["hbm_bytes_per_launch"] / alg, 4) if alg else None
@@ -527,8 +540,8 @@ def main():
 
     cfg = C.C3_0_6B
     n_prompt = C.C3_PROMPT
-    n_classes = 6  # kernel classes timed by the probe pass below
-    total = n_prompt + args.warmup + args.steps + args.probe_steps * n_classes
+    n_classes = 6  # kernel classes of the multi-launch step timed by the probe pass below
+    total = n_prompt + args.warmup + args.steps + args.probe_steps * (n_classes + 1) + MULTI_STEPS + 2
     if total > cfg.seq_len:
         import dataclasses
         cfg = dataclasses.replace(cfg, seq_len=total)
@@ -583,15 +596,58 @@ def main():
     log(f"[bench] decode {args.steps} tokens: {ms:.3f} ms/token, {tok_s:.1f} tok/s, "
         f"{e2e_gbs:.0f} GB/s algorithmic ({100 * e2e_gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
 
-    # ---- per-kernel probe: events inside the dispatches of one kernel class -------------
-    # (hipExtLaunchKernel records the class's start / stop events as part of its kernels' dispatches,
-    # so each interval is kernel execution, as rocprofv3's kernel trace measures it)
+    traffic = load_traffic()
+    persistent = am.persistent
     kernels = {}
+    roofline = None
+    # ---- the persistent kernel: HIP events on the model's stream before and after each launch ----
+    # (eager steps while the probe is on; one launch per step covers the 28 layers, the final norm,
+    # the logits and the greedy keys, so its algorithmic bytes are the step's)
+    probe_pos0 = pos0 + args.steps
+    if persistent:
+        am.kernel_timing(q.KT_LAYERS)
+        am.run(args.probe_steps)
+        ms_k, n_k = am.kernel_time()
+        am.kernel_timing(q.KT_NONE)
+        avg_us = 1000.0 * ms_k / max(n_k, 1)
+        b = float(np.mean([c3_class_bytes(cfg, "decode_persistent", p) for p in range(probe_pos0, probe_pos0 + n_k)]))
+        gbs = b / avg_us / 1e3
+        tr = traffic.get("decode_persistent", {})
+        kernels["decode_persistent"] = {"avg_us": round(avg_us, 3), "launches": n_k, "bytes_per_launch": round(b),
+                                        "GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                                        "share_of_step": round(avg_us / (1000.0 * ms), 4)}
+        roofline = {"bound": "hbm", "kernel": "decode_persistent_kernel (28 layers + final RMSNorm + logits + "
+                    "greedy keys, one launch per step)", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": tr.get("hbm_bytes_per_launch"),
+                    "traffic_source": "profiles/c3_decode_traffic.md" if tr else None, "bytes_per_launch": round(b),
+                    "avg_launch_us": round(avg_us, 3), "launches_timed": n_k,
+                    "timing": "HIP events on the model's stream before and after each launch, eager steps",
+                    "share_of_step": round(avg_us / (1000.0 * ms), 4)}
+        log(f"[bench] persistent decode kernel: {avg_us:.1f} us/launch = {gbs:.0f} GB/s "
+            f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak), {100 * avg_us / (1000.0 * ms):.1f}% of the step")
+        probe_pos0 += n_k
+        am.use_persistent(False)  # the comparison below runs the step as separate launches
+
+    # ---- the step as separate launches: its tok/s, and each kernel class timed ---------------
+    # (per class: a start / stop HIP event pair carried inside the class's own dispatches
+    # (hipExtLaunchKernel), so each interval is kernel execution as rocprofv3's trace measures it)
+    multi = None
+    n_multi = min(MULTI_STEPS, cfg.seq_len - probe_pos0 - args.probe_steps * n_classes)
+    if n_multi > 0:
+        am.run(2)  # (captures the multi-launch step graph)
+        model.ctx.synchronize()
+        tm = time.perf_counter()
+        am.run(n_multi)
+        el = time.perf_counter() - tm
+        multi = {"tok_s": round(n_multi / el, 1), "ms_per_step": round(1000.0 * el / n_multi, 4), "steps": n_multi,
+                 "positions": f"{probe_pos0 + 2}..{probe_pos0 + 2 + n_multi - 1}"}
+        probe_pos0 += 2 + n_multi
+        log(f"[bench] the same decode as separate launches: {multi['ms_per_step']} ms/token, {multi['tok_s']} tok/s")
     names = {q.KT_LOGITS: "logits_gemv_argmax", q.KT_GATE_UP: "gate_up_gemv_swiglu", q.KT_QKV: "qkv_gemv_rmsnorm",
              q.KT_DOWN: "down_gemv_residual", q.KT_O: "o_gemv_residual", q.KT_ATTENTION: "attention_decode"}
-    probe_left = cfg.seq_len - (pos0 + args.steps)
     assert len(names) == n_classes
-    per_class = min(args.probe_steps, probe_left // n_classes)
+    per_class = min(args.probe_steps, (cfg.seq_len - probe_pos0) // n_classes)
+    ms_multi = multi["ms_per_step"] if multi else ms
     for which, name in names.items():
         if per_class == 0:
             break
@@ -601,12 +657,12 @@ def main():
         am.kernel_timing(q.KT_NONE)
         avg_us = 1000.0 * ms_k / max(n_k, 1)
         per_tok_us = 1000.0 * ms_k / per_class
-        probe_pos = pos0 + args.steps + len(kernels) * per_class + (per_class - 1) / 2
+        probe_pos = probe_pos0 + (len(kernels) - int(persistent)) * per_class + (per_class - 1) / 2
         b = c3_class_bytes(cfg, name, probe_pos)
         kernels[name] = {"avg_us": round(avg_us, 3), "launches": n_k, "us_per_token": round(per_tok_us, 2),
                          "bytes_per_launch": round(b) if b else None, "GBs": round(b / avg_us / 1e3, 1) if b else None,
                          "hbm_frac": round(b / avg_us / 1e3 / HBM_PEAK_GBS, 4) if b else None,
-                         "share_of_step": round(per_tok_us / (1000.0 * ms), 4)}
+                         "share_of_multi_launch_step": round(per_tok_us / (1000.0 * ms_multi), 4)}
         log(f"[bench] {name}: {avg_us:.2f} us/launch x {n_k // per_class}/token"
             + (f" = {b / avg_us / 1e3:.0f} GB/s" if b else ""))
     # ---- loop probe: each weight-streaming class alone, LOOP_ROUNDS launches per layer cycling
@@ -625,14 +681,11 @@ def main():
         b = kernels[name]["bytes_per_launch"]
         kernels[name].update({"loop_avg_us": round(lus, 3), "loop_launches": reps,
                               "loop_GBs": round(b / lus / 1e3, 1), "loop_hbm_frac": round(b / lus / 1e3 / HBM_PEAK_GBS, 4),
-                              "loop_share_of_step": round(lus * per_tok / (1000.0 * ms), 4)})
+                              "loop_share_of_multi_launch_step": round(lus * per_tok / (1000.0 * ms_multi), 4)})
         log(f"[bench] {name} loop: {lus:.2f} us/launch over {reps} launches = {b / lus / 1e3:.0f} GB/s")
-    # The roofline kernel is the weight-streaming class with the largest share of the step (gate/up
-    # SwiGLU GEMV at C3); the logits GEMV (the largest single launch) rides along as roofline_logits.
-    # The attention class is latency-bound (~1 MB of K/V per layer at C3), not an HBM roofline kernel.
-    traffic = load_traffic()
+    am.use_persistent(True)
 
-    def roof(name):
+    def roof(name):  # a kernel of the multi-launch step (its loop-probe duration where there is one)
         kd = kernels[name]
         tr = traffic.get(name, {})
         looped = "loop_avg_us" in kd
@@ -644,12 +697,14 @@ def main():
                 "bytes_per_launch": kd["bytes_per_launch"], "avg_launch_us": round(us, 3),
                 "timing": ("graph-replayed loop of the class's launches over the layers, two HIP events around it"
                            if looped else "HIP events inside the class's dispatches"),
-                "probe_avg_launch_us": kd["avg_us"],
-                "share_of_step": kd.get("loop_share_of_step", kd["share_of_step"])}
+                "probe_avg_launch_us": kd["avg_us"]}
 
-    gemv_classes = [k for k in kernels if k != "attention_decode" and kernels[k]["GBs"]]
-    roofline = roof(max(gemv_classes, key=lambda k: kernels[k]["us_per_token"])) if gemv_classes else None
+    gemv_classes = [k for k in names.values() if k in kernels and k != "attention_decode" and kernels[k]["GBs"]]
+    # the multi-launch step's dominant weight-streaming class (gate/up + SwiGLU at C3) and its logits GEMV
+    roofline_multi = roof(max(gemv_classes, key=lambda k: kernels[k]["us_per_token"])) if gemv_classes else None
     roofline_logits = roof("logits_gemv_argmax") if "logits_gemv_argmax" in kernels else None
+    if roofline is None:
+        roofline = roofline_multi
 
     # ---- the same decode with on-device sampling instead of greedy selection ----------------
     sampled = {}
@@ -713,7 +768,7 @@ def main():
         "config": {"workload": "C3: Qwen3-0.6B shape fp32 (d1024, 28L, 16Q/8KV, hd128, F3072, V151936), "
                                "batch 1, prompt 128, greedy decode",
                    "decode_positions": f"{pos0}..{pos0 + args.steps - 1}", "graph": not args.no_graph,
-                   "prefetch_blocks": args.prefetch},
+                   "prefetch_blocks": args.prefetch, "persistent_kernel": persistent},
         "hbm": {"algorithmic_bytes_per_token": round(mean_bytes), "achieved_GBs": round(e2e_gbs, 1),
                 "frac_of_peak": round(e2e_gbs / HBM_PEAK_GBS, 4)},
         "sampled_c3": sampled,
@@ -728,7 +783,7 @@ def main():
         "c2": c2_section(args) if "c2" in sections and not args.no_c2 else None,
         "llama2": llama2_section(args) if "llama2" in sections and not args.no_llama2 else None,
         "roofline": roofline,
-        "roofline_logits": roofline_logits,
+        "multi_launch": dict(multi or {}, roofline=roofline_multi, roofline_logits=roofline_logits),
         "kernels": kernels,
         "cpu_baseline": cpu,
         "parity": parity,

@@ -282,7 +282,7 @@ int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
  * hold one 512-thread block per CU on 256 CUs at once), the layers and the logits of each decode step
  * run as one launch whose stages exchange data through device-scope words tagged with an epoch,
  * instead of five launches per layer and one for the logits; the step-begin kernel stays separate,
- * and the step is captured into a graph like the multi-launch one.  No counterpart in the reference
+ * and the two launches are enqueued directly (a graph replay of them measured slower).  No counterpart in the reference
  * (its backend runs the compiled operation list); a throughput option only: results match the
  * multi-launch step within float rounding.  enable 1 (default) or 0; ar_hip_qwen3_persistent reports
  * whether the next steps use it.  A cross-block wait that times out (possible only if another
