@@ -40,6 +40,7 @@ constexpr int kRowsPerSplit = 32;  // cache rows per split before another split 
 constexpr unsigned kSpinLimit = 1u << 18;  // polls before a wait is abandoned (~0.3 s)
 constexpr int kPadLds = 64 * 1024;         // dynamic LDS that keeps a second block off each CU
 constexpr int kMaxLayers = 64;             // layer table held in LDS
+constexpr unsigned kGateUpDelay = 250;     // wall-clock ticks (10 ns): see the O stage
 
 struct PLayer {
     const float* wqkv;
@@ -300,6 +301,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         }
         }
 
+        const unsigned long long t_p1 = wall_clock64();  // (100 MHz)
         // ================= P2: attention (blocks of (KV head, split)) ==============
         if (b < KV * nsplit) {
             STAGE_IDS();
@@ -598,6 +600,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 
         // ================= P3: O projection + residual ==============================
         lds_barrier();  // xin readers (P1) are done
+        float4 wg[RPWg][NCg];
         {
             STAGE_IDS();
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
@@ -605,6 +608,25 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 #pragma unroll
             for (int c = 0; c < NCo; c++)
                 wo[c] = gld4(Ly.wo, (size_t)row * QD + col0 + c * 256 + lane * 4);
+            // The gate/up rows (the largest stage, 24 MB at C3) are issued here, with the O rows, so
+            // they stream while the attention chain runs instead of at the start of their own stage.
+            // The blocks that reach this point right after QKV (no attention, no merge) hold them back
+            // kGateUpDelay after their QKV stage: issued at once they queue in HBM ahead of the
+            // attention's cache rows and exchanges (measured at C3, ms per step: at once 0.711,
+            // after 1.5 / 2 / 2.5 / 3 / 4 us 0.699 / 0.696 / 0.696 / 0.696 / 0.709, in their own
+            // stage 0.712; the down rows issued here as well, after 4-5.5 us: 0.709-0.716).
+            if (b >= KV * nsplit && b < kPB - H)
+                while (wall_clock64() < t_p1 + kGateUpDelay) __builtin_amdgcn_s_sleep(4);
+            {
+                const bool up = wave >= kPW / 2;
+                const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
+                const float* W = up ? Ly.w3 : Ly.w1;
+#pragma unroll
+                for (int i = 0; i < RPWg; i++)
+#pragma unroll
+                    for (int c = 0; c < NCg; c++)
+                        wg[i][c] = gld4(W, (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
+            }
             constexpr int NA = QD / kPT;
             int idx[NA];
 #pragma unroll
@@ -639,15 +661,6 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         lds_barrier();  // xin / rows_s readers (P3) are done
         {
             STAGE_IDS();
-            const bool up = wave >= kPW / 2;
-            const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
-            const float* W = up ? Ly.w3 : Ly.w1;
-            float4 wg[RPWg][NCg];
-#pragma unroll
-            for (int i = 0; i < RPWg; i++)
-#pragma unroll
-                for (int c = 0; c < NCg; c++)
-                    wg[i][c] = gld4(W, (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
             constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
             float gv[NX];
 #pragma unroll
