@@ -604,15 +604,15 @@ int pick_g(const AttnLaunch& a, hipStream_t s) {
 // Causal attention of prompt rows in fp32, the attention of the fp32-weight prefill: row t of
 // sequence b (block (b*T + t, g)) attends cache rows 0..p0+t of KV head g for the G query heads of
 // the group, with the decode kernel's arithmetic (queries pre-scaled by log2(e)/sqrt(hd), online
-// softmax in base 2, 16-lane groups each streaming every 16th row, group states merged by lane swaps
-// and through LDS).  The cache rows of the prompt are written beforehand (qk_prep), so every row
+// softmax in base 2, 16-lane groups each streaming every 16th row in chunks of RU rows loaded
+// together, group states merged by lane swaps and through LDS).  The cache rows of the prompt are written beforehand (qk_prep), so every row
 // reads finished rows only.  q32: [B*T][heads*hd] normalised, rotated queries; caches fp32
 // [B][KV][S][hd]; out: [B*T][heads*hd].
 template <int HD, int G>
 __global__ __launch_bounds__(256) void attn_prefill_f32_kernel(const float* q32, const float* kcache,
                                                                 const float* vcache, float* out, int T, int p0,
                                                                 int S, int heads, int kv_heads) {
-    constexpr int EPL = HD / 16, NGR = 16, NWV = 4;
+    constexpr int EPL = HD / 16, NGR = 16, NWV = 4, RU = 4;
     __shared__ __attribute__((aligned(16))) float red_acc[NWV][G][HD];
     __shared__ float red_m[NWV][G], red_l[NWV][G];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = tid >> 4, gl = tid & 15;
@@ -646,40 +646,60 @@ __global__ __launch_bounds__(256) void attn_prefill_f32_kernel(const float* q32,
             dst[e] = v.x; dst[e + 1] = v.y; dst[e + 2] = v.z; dst[e + 3] = v.w;
         }
     };
-    float kr[EPL], vr[EPL];
-    int row = grp;
-    if (row < n) {
-        load_row(kr, kc, row);
-        load_row(vr, vc, row);
-    }
-    for (; row < n; row += NGR) {
-        float kn[EPL], vn[EPL];
-        const bool more = row + NGR < n;
-        if (more) {  // the group's next row, in flight while this one is used
-            load_row(kn, kc, row + NGR);
-            load_row(vn, vc, row + NGR);
+    // chunk c: rows c*NGR*RU + grp + NGR*j (j < RU) of each 16-lane group, loaded together (rows past
+    // n re-read row n-1 and score -inf); the next chunk is in flight while one is used
+    float ka[RU][EPL], va[RU][EPL], kb[RU][EPL], vb[RU][EPL];
+    auto load_chunk = [&](float (&kd)[RU][EPL], float (&vd)[RU][EPL], int c) {
+#pragma unroll
+        for (int j = 0; j < RU; j++) {
+            const int row = min(c * NGR * RU + grp + NGR * j, n - 1);
+            load_row(kd[j], kc, row);
+            load_row(vd[j], vc, row);
+        }
+    };
+    auto use_chunk = [&](const float (&kd)[RU][EPL], const float (&vd)[RU][EPL], int c) {
+        float sc[G][RU];
+#pragma unroll
+        for (int j = 0; j < RU; j++) {
+            const bool valid = c * NGR * RU + grp + NGR * j < n;
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) d = fmaf(qf[h][e], kd[j][e], d);
+                d = row16_sum(d);
+                sc[h][j] = valid ? d : -INFINITY;
+            }
         }
 #pragma unroll
         for (int h = 0; h < G; h++) {
-            float d = 0.f;
+            float mc = sc[h][0];
 #pragma unroll
-            for (int e = 0; e < EPL; e++) d = fmaf(qf[h][e], kr[e], d);
-            d = row16_sum(d);
-            const float mn = fmaxf(m[h], d);
+            for (int j = 1; j < RU; j++) mc = fmaxf(mc, sc[h][j]);
+            const float mn = fmaxf(m[h], mc);
+            if (mn == -INFINITY) continue;
             const float alpha = (m[h] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[h] - mn);
-            const float pj = __builtin_amdgcn_exp2f(d - mn);
-            l[h] = l[h] * alpha + pj;
+            l[h] *= alpha;
 #pragma unroll
-            for (int e = 0; e < EPL; e++) acc[h][e] = fmaf(pj, vr[e], acc[h][e] * alpha);
+            for (int e = 0; e < EPL; e++) acc[h][e] *= alpha;
+#pragma unroll
+            for (int j = 0; j < RU; j++) {
+                const float pj = __builtin_amdgcn_exp2f(sc[h][j] - mn);
+                l[h] += pj;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) acc[h][e] = fmaf(pj, vd[j][e], acc[h][e]);
+            }
             m[h] = mn;
         }
-        if (more) {
-#pragma unroll
-            for (int e = 0; e < EPL; e++) {
-                kr[e] = kn[e];
-                vr[e] = vn[e];
-            }
-        }
+    };
+    const int nch = (n + NGR * RU - 1) / (NGR * RU);
+    load_chunk(ka, va, 0);
+    for (int c = 0; c < nch; c += 2) {
+        if (c + 1 < nch) load_chunk(kb, vb, c + 1);
+        use_chunk(ka, va, c);
+        if (c + 1 >= nch) break;
+        if (c + 2 < nch) load_chunk(ka, va, c + 2);
+        use_chunk(kb, vb, c + 1);
     }
     auto merge_with = [&](auto partner) {
 #pragma unroll

@@ -5,10 +5,9 @@
 // LayerFeatures.dense (domain/graph/.../LayerFeatures.java:785-830) for prompt rows, which the
 // reference feeds one per step (engine/ml/.../AutoregressiveModel.java:295-308).
 //
-// Block tile (32*WM) x (32*WN), one 32 x 32 output block per wavefront, k in tiles of 32 staged
-// k-major in LDS (row k holds the tile's rows / columns contiguously, so lanes 0-31 read 32
-// consecutive floats of row k and lanes 32-63 of row k+1 -- the two k values of one MFMA -- without
-// bank conflicts), the next k tile loaded into registers during the current tile's MFMAs.
+// The products are small in rows (a 128-token prompt), so a block of 32 (or 64) rows x 64 columns
+// splits its k range over KS groups of wavefronts (two wavefronts per SIMD at KS = 4) and each
+// wavefront streams its weight rows straight into registers one iteration ahead (see the kernel).
 // Epilogues: STORE (+ bias), RESIDUAL (C += product), SWIGLU (C = (A.W2^T) * silu(A.W^T)), and
 // k-slices stored separately for the consumer to add in a fixed order.
 #include "ar_hip_internal.h"
@@ -16,8 +15,10 @@
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float f4 __attribute__((ext_vector_type(4)));  // (a native vector: stays in registers)
 
-constexpr int BK = 32;
+constexpr int BK = 32;  // k granularity every launch accepts
+constexpr int kPadLds = 64 * 1024;
 
 struct Params {
     const float* A;   // [M][lda]
@@ -27,10 +28,6 @@ struct Params {
     float* C;         // [M][ldc] (ksplit > 1: slice s at C + s*M*ldc)
     int M, N, K, lda, ldw, ldc, ksplit;
 };
-
-// LDS row stride (floats) of a k-major tile of `cols` columns: 32 columns pad to 32 (the two lane
-// halves read rows k and k+1, 32 banks apart), multiples of 64 pad by 32 for the same reason.
-constexpr int lds_stride(int cols) { return cols % 64 == 0 ? cols + 32 : cols; }
 
 // Output tile of block `bid`: consecutive blocks (one XCD takes every 8th) walk m fastest within
 // groups of 8 n-tiles, so blocks running together on an XCD share W column tiles in its L2.
@@ -42,132 +39,207 @@ __device__ inline void tile_of(int bid, int mt, int nt, int* mi, int* ni) {
     *ni = t / mt;
 }
 
-template <int WM, int WN, int EPI>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_f32_kernel(Params p, int mt, int nt) {
-    constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
-    constexpr int BM = 32 * WM, BN = 32 * WN, NT = 64 * WM * WN;
-    constexpr int SA = lds_stride(BM), SW = lds_stride(BN);
-    // global -> register staging: thread t loads float4 j = t / rows of row t % rows of a tile
-    constexpr int AL = BM * (BK / 4) / NT, WL = BN * (BK / 4) / NT;  // float4 loads per thread
-    static_assert(AL >= 1 && WL >= 1 && BM * (BK / 4) % NT == 0 && BN * (BK / 4) % NT == 0, "tile / thread shape");
-    __shared__ float As[2][BK * SA];
-    __shared__ float Ws[NW][2][BK * SW];
+// Block barrier over LDS only: the weight loads of the next iteration stay in flight across it.
+__device__ inline void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave % WM, wn = wave / WM;
+// Block tile (32*WM) x 64: two column wavefronts x KS k-groups.  Wavefront (kg, wn) computes the WM
+// 32 x 32 output blocks of rows 0..32*WM-1 and columns wn*32..wn*32+31 over k-group kg's share of
+// every iteration's BKG*KS k values; the KS partial sums meet in LDS at the end (added in group
+// order) and group 0 runs the epilogue.  Operands of one MFMA step: lanes 0-31 supply k = 8q + c,
+// lanes 32-63 k = 8q + 4 + c, for component c of the float4 each lane holds of chunk q (A from LDS,
+// W straight from global memory into registers, one iteration ahead), so the 32x32x2 MFMA pairs
+// equal k values of A and W.  The A tile (32*WM rows x BKG*KS) is staged row-major in LDS (row
+// stride BKG*KS + 4 floats: the eight lanes of one 16-byte read phase hit eight different bank
+// groups), its next iteration prefetched in registers.
+template <int WM, int KS, int BKG, int EPI>
+__global__ __launch_bounds__(128 * KS) void gemm_f32_kernel(Params p, int mt, int nt) {
+    constexpr int WN = 2;
+    constexpr int NW = (EPI == GEMV_EPI_SWIGLU) ? 2 : 1;
+    constexpr int BM = 32 * WM, BN = 32 * WN, NT = 64 * WN * KS;
+    constexpr int BKI = BKG * KS;          // k values per iteration (all groups)
+    constexpr int SA = BKI + 4;            // LDS row stride (floats) of the A tile
+    constexpr int QG = BKG / 8;            // float4 chunks per lane per iteration
+    constexpr int AL = BM * BKI / 4 / NT;  // float4 A loads per thread per iteration
+    static_assert(AL >= 1 && (BM * BKI / 4) % NT == 0 && BKG % 8 == 0, "tile / thread shape");
+    constexpr int A_FLOATS = BM * SA;
+    constexpr int RED_FLOATS = (KS - 1) * WN * NW * WM * 1024;
+    __shared__ __attribute__((aligned(16))) float sm[A_FLOATS > RED_FLOATS ? A_FLOATS : RED_FLOATS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = wave / WN, wn = wave - kg * WN;
     const int tiles = mt * nt;
     const int ks = blockIdx.x / tiles;
     int mi, ni;
     tile_of(blockIdx.x - ks * tiles, mt, nt, &mi, &ni);
     const int m0 = mi * BM, n0 = ni * BN;
-    const int kper = p.K / p.ksplit, kbase = ks * kper, nkt = kper / BK;
+    const int kper = p.K / p.ksplit, kbase = ks * kper, nit = kper / BKI;
+    const int h = lane >> 5, l32 = lane & 31;
 
-    float4 ra[AL], rw[NW][WL];
-    auto load_tile = [&](int kt) {
-        const int k0 = kbase + kt * BK;
+    f4 ra[AL];
+    auto load_a = [&](int it) __attribute__((always_inline)) {
+        const int k0 = kbase + it * BKI;
 #pragma unroll
         for (int i = 0; i < AL; i++) {
-            const int e = tid + i * NT, r = e % BM, j = e / BM;
+            const int e = tid + i * NT, r = e / (BKI / 4), c = e - r * (BKI / 4);
             const int row = min(m0 + r, p.M - 1);  // rows past M re-read the last row (never stored)
-            ra[i] = *reinterpret_cast<const float4*>(p.A + (size_t)row * p.lda + k0 + 4 * j);
-        }
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float* Wm = w ? p.W2 : p.W;
-#pragma unroll
-            for (int i = 0; i < WL; i++) {
-                const int e = tid + i * NT, c = e % BN, j = e / BN;
-                rw[w][i] = *reinterpret_cast<const float4*>(Wm + (size_t)(n0 + c) * p.ldw + k0 + 4 * j);
-            }
+            ra[i] = *reinterpret_cast<const f4*>(p.A + (size_t)row * p.lda + k0 + 4 * c);
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_a = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < AL; i++) {
-            const int e = tid + i * NT, r = e % BM, j = e / BM;
-            float* d = &As[buf][(4 * j) * SA + r];
-            d[0] = ra[i].x; d[SA] = ra[i].y; d[2 * SA] = ra[i].z; d[3 * SA] = ra[i].w;
+            const int e = tid + i * NT, r = e / (BKI / 4), c = e - r * (BKI / 4);
+            *reinterpret_cast<f4*>(&sm[r * SA + 4 * c]) = ra[i];
         }
+    };
+    const float* wrow[NW];
+    wrow[0] = p.W + (size_t)(n0 + wn * 32 + l32) * p.ldw + kbase + kg * BKG + 4 * h;
+    if constexpr (NW == 2) wrow[NW - 1] = p.W2 + (size_t)(n0 + wn * 32 + l32) * p.ldw + kbase + kg * BKG + 4 * h;
+    f4 wa[NW][QG], wb[NW][QG];
+    auto load_w = [&](f4 (&w)[NW][QG], int it) __attribute__((always_inline)) {
 #pragma unroll
-        for (int w = 0; w < NW; w++)
+        for (int x = 0; x < NW; x++)
 #pragma unroll
-            for (int i = 0; i < WL; i++) {
-                const int e = tid + i * NT, c = e % BN, j = e / BN;
-                float* d = &Ws[w][buf][(4 * j) * SW + c];
-                d[0] = rw[w][i].x; d[SW] = rw[w][i].y; d[2 * SW] = rw[w][i].z; d[3 * SW] = rw[w][i].w;
+            for (int q = 0; q < QG; q++) w[x][q] = *reinterpret_cast<const f4*>(wrow[x] + it * BKI + 8 * q);
+    };
+
+    floatx16 acc[NW][WM];
+#pragma unroll
+    for (int x = 0; x < NW; x++)
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[x][i][r] = 0.f;
+    auto compute = [&](const f4 (&w)[NW][QG]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < QG; q++)
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+                const f4 a = *reinterpret_cast<const f4*>(&sm[(i * 32 + l32) * SA + kg * BKG + 8 * q + 4 * h]);
+#pragma unroll
+                for (int x = 0; x < NW; x++) {
+                    acc[x][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, w[x][q].x, acc[x][i], 0, 0, 0);
+                    acc[x][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, w[x][q].y, acc[x][i], 0, 0, 0);
+                    acc[x][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, w[x][q].z, acc[x][i], 0, 0, 0);
+                    acc[x][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, w[x][q].w, acc[x][i], 0, 0, 0);
+                }
             }
     };
 
-    floatx16 acc[NW];
-#pragma unroll
-    for (int w = 0; w < NW; w++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[w][r] = 0.f;
-
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    const int am = wm * 32 + (lane & 31), bn = wn * 32 + (lane & 31), kh = lane >> 5;
-    for (int kt = 0; kt < nkt; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < nkt) load_tile(kt + 1);
-        const float* as = &As[buf][kh * SA + am];
-#pragma unroll
-        for (int kp = 0; kp < BK / 2; kp++) {
-            const float a = as[2 * kp * SA];
-#pragma unroll
-            for (int w = 0; w < NW; w++) {
-                const float b = Ws[w][buf][(2 * kp + kh) * SW + bn];
-                acc[w] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[w], 0, 0, 0);
-            }
-        }
-        if (kt + 1 < nkt) store_tile(buf ^ 1);
-        __syncthreads();
+    // iteration it multiplies the A tile in LDS with W registers set (it & 1); the next iteration's
+    // A rows (registers) and W chunks are loaded before it (the last iteration reloads its own tile,
+    // a cache hit, so the loads stay unconditional)
+    load_a(0);
+    load_w(wa, 0);
+    store_a();
+    lds_barrier();
+    for (int it = 0;;) {
+        load_a(min(it + 1, nit - 1));
+        load_w(wb, min(it + 1, nit - 1));
+        __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink the loads below the MFMAs)
+        compute(wa);
+        lds_barrier();
+        if (++it >= nit) break;
+        store_a();
+        lds_barrier();
+        load_a(min(it + 1, nit - 1));
+        load_w(wa, min(it + 1, nit - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(wb);
+        lds_barrier();
+        if (++it >= nit) break;
+        store_a();
+        lds_barrier();
     }
 
-    // output block of this wave: lane holds column (lane & 31), rows (r>>2)*8 + (lane>>5)*4 + (r&3)
-    const int col = n0 + wn * 32 + (lane & 31);
+    // k-groups 1..KS-1 hand their sums to group 0, which adds them in group order
+    if constexpr (KS > 1) {
+        if (kg > 0) {
+#pragma unroll
+            for (int x = 0; x < NW; x++)
+#pragma unroll
+                for (int i = 0; i < WM; i++) {
+                    float* d = &sm[((((kg - 1) * WN + wn) * NW + x) * WM + i) * 1024 + lane];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) d[r * 64] = acc[x][i][r];
+                }
+        }
+        lds_barrier();
+        if (kg > 0) return;
+#pragma unroll
+        for (int g = 1; g < KS; g++)
+#pragma unroll
+            for (int x = 0; x < NW; x++)
+#pragma unroll
+                for (int i = 0; i < WM; i++) {
+                    const float* s = &sm[((((g - 1) * WN + wn) * NW + x) * WM + i) * 1024 + lane];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[x][i][r] += s[r * 64];
+                }
+    }
+
+    // output block (i) of this wave: lane holds column (lane & 31), rows (r>>2)*8 + (lane>>5)*4 + (r&3)
+    const int col = n0 + wn * 32 + l32;
     float* const Cs = p.C + (size_t)ks * p.M * p.ldc;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (row >= p.M) continue;
-        float* c = Cs + (size_t)row * p.ldc + col;
-        if (EPI == GEMV_EPI_STORE) {
-            *c = p.bias ? acc[0][r] + p.bias[col] : acc[0][r];
-        } else if (EPI == GEMV_EPI_RESIDUAL) {
-            *c = *c + acc[0][r];
-        } else {
-            const float g = acc[0][r], u = acc[NW - 1][r];
-            const float sg = 1.0f / (expf(-g) + 1.0f);
-            *c = u * (g * sg);
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = m0 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+            if (row >= p.M) continue;
+            float* c = Cs + (size_t)row * p.ldc + col;
+            if (EPI == GEMV_EPI_STORE) {
+                *c = p.bias ? acc[0][i][r] + p.bias[col] : acc[0][i][r];
+            } else if (EPI == GEMV_EPI_RESIDUAL) {
+                *c = *c + acc[0][i][r];
+            } else {
+                const float g = acc[0][i][r], u = acc[NW - 1][i][r];
+                const float sg = 1.0f / (expf(-g) + 1.0f);
+                *c = u * (g * sg);
+            }
         }
-    }
 }
 
-template <int WM, int WN, int EPI>
+template <int WM, int KS, int BKG, int EPI>
 int launch_t(const Params& p, hipStream_t st) {
-    const int mt = (p.M + 32 * WM - 1) / (32 * WM), nt = p.N / (32 * WN);
+    const int mt = (p.M + 32 * WM - 1) / (32 * WM), nt = p.N / 64;
     const long long blocks = (long long)mt * nt * p.ksplit;
     AR_CHECK_ARG(blocks <= 0x7fffffffLL, "GEMM f32: too many blocks");
-    hipLaunchKernelGGL((gemm_f32_kernel<WM, WN, EPI>), dim3((unsigned)blocks), dim3(64 * WM * WN), 0, st, p, mt, nt);
+    // dynamic LDS that keeps a second block off a CU: the blocks of a product that fills the CUs
+    // once then spread one per CU instead of doubling up on some while others idle
+    hipLaunchKernelGGL((gemm_f32_kernel<WM, KS, BKG, EPI>), dim3((unsigned)blocks), dim3(128 * KS), kPadLds, st, p, mt,
+                       nt);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }
 
+// 64-row tiles once there are enough rows to fill the CUs with them (the W registers then feed two
+// output blocks), else 32-row tiles; as many k-groups as the k-slice divides into
 template <int EPI>
 int launch_epi(const Params& p, hipStream_t st) {
-    // 64-row tiles once there are enough rows to fill the CUs with them, else 32-row tiles
-    if (p.M >= 512) return launch_t<2, 2, EPI>(p, st);
-    return launch_t<1, 2, EPI>(p, st);
+    const int kper = p.K / p.ksplit;
+    if (p.M >= 512) {
+        if (kper % 128 == 0) return launch_t<2, 2, 64, EPI>(p, st);
+        return launch_t<2, 1, 32, EPI>(p, st);
+    }
+    if (kper % 256 == 0) return launch_t<1, 4, 64, EPI>(p, st);
+    if (kper % 128 == 0) return launch_t<1, 2, 64, EPI>(p, st);
+    return launch_t<1, 1, 32, EPI>(p, st);
 }
 
 }  // namespace
 
 int gemm_f32_ksplit(int M, int N, int K, int cus) {
-    const long long tiles = (long long)((M + 31) / 32) * (N / 64);
+    const int bm = M >= 512 ? 64 : 32;
+    const long long tiles = (long long)((M + bm - 1) / bm) * (N / 64);
     int s = 1;
-    while (s < 8 && tiles * s < 2LL * cus && K % (BK * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
+    while (s < 8 && tiles * s * 2 <= cus && K % (256 * s * 2) == 0) s *= 2;
     return s;
 }
 

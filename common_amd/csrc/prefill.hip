@@ -237,6 +237,51 @@ __device__ inline float2 block_sum2(float2 v, float2* scratch) {
     return t;
 }
 
+// fp32 output form of the fold + row RMSNorm (the fp32-weight prefill's GEMM input): 16-byte
+// accesses, the row in registers, every part of a value loaded before the adds (x, then the parts
+// in slice order, nparts <= 4); n % 4 == 0, n <= NV * 1024.
+template <int NV>
+__global__ __launch_bounds__(256) void fold_rmsnorm_rows_f32_v4_kernel(float* x, const float* parts, int nparts,
+                                                                        size_t part_stride, const float* w, float* out,
+                                                                        int n, float eps) {
+    __shared__ float scratch[4];
+    const int n4 = n >> 2;
+    const size_t row = (size_t)blockIdx.x * n;
+    float4* xr = reinterpret_cast<float4*>(x + row);
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n4) {
+            float4 q[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+                if (s < nparts) q[s] = reinterpret_cast<const float4*>(parts + s * part_stride + row)[i];
+            float4 a = xr[i];
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+                if (s < nparts) {
+                    a.x += q[s].x; a.y += q[s].y; a.z += q[s].z; a.w += q[s].w;
+                }
+            if (nparts) xr[i] = a;
+            v[j] = a;
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        }
+    }
+    ss = block_sum(ss, scratch);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    float4* orow = reinterpret_cast<float4*>(out + row);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < n4) {
+            const float4 g = reinterpret_cast<const float4*>(w)[i];
+            orow[i] = make_float4((g.x * v[j].x) * r, (g.y * v[j].y) * r, (g.z * v[j].z) * r, (g.w * v[j].w) * r);
+        }
+    }
+}
+
 // The fold + row RMSNorm above with 16-byte accesses and the row held in registers (one read of x
 // and of each part, one write of x and of the fp16 row): n % 4 == 0, n <= NV * 1024.  Each value
 // is folded in the same order (x, then parts in slice order).
@@ -732,8 +777,21 @@ int launch_fold_rmsnorm_rows_f32(float* x, const float* parts, int nparts, const
                                  int n, float eps, hipStream_t stream) {
     AR_CHECK_ARG(x && w && out && rows > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0),
                  "fold rmsnorm rows: bad arguments");
-    hipLaunchKernelGGL(fold_rmsnorm_rows_f32_kernel, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
-                       (size_t)rows * n, w, out, n, eps);
+    const bool v4 = n % 4 == 0 && n <= 4096 && nparts <= 4 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                    (nparts == 0 || (reinterpret_cast<uintptr_t>(parts) & 15) == 0);
+    if (v4 && n <= 1024)
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f32_v4_kernel<1>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
+    else if (v4 && n <= 2048)
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f32_v4_kernel<2>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
+    else if (v4)
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f32_v4_kernel<4>, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
+    else
+        hipLaunchKernelGGL(fold_rmsnorm_rows_f32_kernel, dim3(rows), dim3(256), 0, stream, x, parts, nparts,
+                           (size_t)rows * n, w, out, n, eps);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -173,10 +173,12 @@ def test_prefill_matches_sequential_decode_and_oracle(ctx, per_head, batch):
             assert after_prefill[b, s] == rf[T + s] == after_seq[b, s]
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 64, 32), (16, 512, 256), (100, 768, 1024), (128, 4096, 1024), (600, 1024, 3072)])
+@pytest.mark.parametrize("M,N,K", [(1, 64, 32), (16, 512, 256), (33, 64, 96), (40, 128, 768), (100, 768, 1024),
+                                   (128, 4096, 1024), (600, 1024, 3072), (520, 128, 160)])
 def test_gemm_f32_vs_float64(ctx, M, N, K):
-    """fp32 MFMA projection (ar_hip_gemm_f32): 32- and 64-row tiles, ragged M, all three epilogues,
-    against float64 products of the same fp32 operands (1e-5 relative)."""
+    """fp32 MFMA projection (ar_hip_gemm_f32): 32- and 64-row tiles, ragged M, 1 / 2 / 4 k-groups per
+    block with odd and even iteration counts, all three epilogues, against float64 products of the
+    same fp32 operands (1e-5 relative)."""
     r = np.random.default_rng(M + N + K)
     A = r.standard_normal((M, K)).astype(np.float32)
     W = (r.standard_normal((N, K)) * 0.05).astype(np.float32)
