@@ -320,6 +320,7 @@ int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
 struct DecodePersistentLaunch {
     const void* layers = nullptr;
     int layer_count = 0;
+    int wdtype = AR_DTYPE_F32;  // projection / head weights: AR_DTYPE_F32 or AR_DTYPE_BF16
     int dim = 0, hidden_dim = 0, heads = 0, kv_heads = 0, head_dim = 0;
     float* x = nullptr;        // [dim] the step's input and, after the launch, its output
     float* kcache = nullptr;   // [L][KV][S][HD] fp32
@@ -333,17 +334,17 @@ struct DecodePersistentLaunch {
     int per_head_norm = 0;
     // after the last layer: final RMSNorm, logits (stored when logits is non-null) and greedy keys
     const float* final_norm = nullptr;
-    const float* lm_head = nullptr;
+    const void* lm_head = nullptr;  // weight type
     int vocab = 0;
     float* logits = nullptr;
     unsigned long long* keys = nullptr;  // [kArgmaxSlots], zero before the launch
 };
 size_t decode_persistent_layer_bytes();
-size_t decode_persistent_ll_words(int dim, int F, int heads, int kv_heads, int hd);  // 0: no instantiation
-int decode_persistent_layer_entry(void* dst, const float* wqkv, const float* wo, const float* w1, const float* w3,
-                                  const float* w2, const float* attn_norm, const float* ffn_norm, const float* q_norm,
+size_t decode_persistent_ll_words(int wdtype, int dim, int F, int heads, int kv_heads, int hd);  // 0: none
+int decode_persistent_layer_entry(void* dst, const void* wqkv, const void* wo, const void* w1, const void* w3,
+                                  const void* w2, const float* attn_norm, const float* ffn_norm, const float* q_norm,
                                   const float* k_norm, const float* bqkv);
-bool decode_persistent_supported(int dim, int F, int heads, int kv_heads, int hd);
+bool decode_persistent_supported(int wdtype, int dim, int F, int heads, int kv_heads, int hd);
 int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t stream);
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);
 // Splits for a cache of max_seq rows: about one block per CU, rows per split <= 256 (1040 for an

@@ -35,7 +35,6 @@ namespace {
 constexpr int kPB = 256;           // blocks: one per CU
 constexpr int kPT = 512;           // threads per block
 constexpr int kPW = kPT / 64;      // wavefronts per block
-constexpr int kSMax = 8;           // attention splits per KV head
 constexpr int kRowsPerSplit = 32;  // cache rows per split before another split is opened
 constexpr unsigned kSpinLimit = 1u << 18;  // polls before a wait is abandoned (~0.3 s)
 constexpr int kPadLds = 64 * 1024;         // dynamic LDS that keeps a second block off each CU
@@ -43,11 +42,11 @@ constexpr int kMaxLayers = 64;             // layer table held in LDS
 constexpr unsigned kGateUpDelay = 250;     // wall-clock ticks (10 ns): see the O stage
 
 struct PLayer {
-    const float* wqkv;
-    const float* wo;
-    const float* w1;
-    const float* w3;
-    const float* w2;
+    const void* wqkv;  // projection weights in the model's weight type (fp32 or bf16)
+    const void* wo;
+    const void* w1;
+    const void* w3;
+    const void* w2;
     const float* attn_norm;
     const float* ffn_norm;
     const float* q_norm;
@@ -70,7 +69,7 @@ struct PParams {
     int per_head;      // QK-norm: one RMS per head (else over the whole q / k vector)
     // after the last layer: final RMSNorm, logits and greedy-token keys
     const float* final_norm;
-    const float* lm_head;  // [vocab][dim]
+    const void* lm_head;   // [vocab][dim], weight type
     int vocab;
     float* logits;         // [vocab], or null: not stored
     unsigned long long* keys;  // [kArgmaxSlots] packed (value, index) maxima, zero before the launch
@@ -98,6 +97,53 @@ __device__ inline float gld(const float* base, size_t off) {
     return base[off];
 #endif
 }
+// Weight rows in 16-byte loads: fp32 (4 values) or bf16 (8 values, widened exactly by a shift), dotted
+// with fp32 inputs in the same order as the fp32 rows.
+typedef const __attribute__((address_space(1))) uint32_t guint;
+__device__ inline uint4 gld4u(const void* base, size_t off16) {  // off16: offset in 16-byte units
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4 v = *(const __attribute__((address_space(1))) u4*)((guint*)base + 4 * off16);
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return reinterpret_cast<const uint4*>(base)[off16];
+#endif
+}
+template <typename TW>
+struct WRow;
+template <>
+struct WRow<float> {
+    static constexpr int V = 4;  // values per 16-byte load
+    typedef float4 raw;
+    __device__ static raw load(const void* base, size_t off) { return gld4((const float*)base, off); }
+    __device__ static float dot(const raw& w, const float* x, float a) {
+        a = fmaf(w.x, x[0], a);
+        a = fmaf(w.y, x[1], a);
+        a = fmaf(w.z, x[2], a);
+        a = fmaf(w.w, x[3], a);
+        return a;
+    }
+};
+template <>
+struct WRow<uint16_t> {
+    static constexpr int V = 8;
+    typedef uint4 raw;
+    __device__ static raw load(const void* base, size_t off) { return gld4u(base, off / 8); }
+    __device__ static float lo(uint32_t u) { return __uint_as_float(u << 16); }
+    __device__ static float hi(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
+    __device__ static float dot(const raw& w, const float* x, float a) {
+        a = fmaf(lo(w.x), x[0], a);
+        a = fmaf(hi(w.x), x[1], a);
+        a = fmaf(lo(w.y), x[2], a);
+        a = fmaf(hi(w.y), x[3], a);
+        a = fmaf(lo(w.z), x[4], a);
+        a = fmaf(hi(w.z), x[5], a);
+        a = fmaf(lo(w.w), x[6], a);
+        a = fmaf(hi(w.w), x[7], a);
+        return a;
+    }
+};
+
 // The block's "stop waiting" flag in LDS, through relaxed workgroup-scope atomics (LDS accesses the
 // compiler neither caches in a register nor turns into generic ones).
 __device__ inline int dead_get(int* d) { return __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
@@ -171,28 +217,31 @@ __device__ inline float block_sum(float v, float* red, int lane, int wave) {
     return t;
 }
 
-template <int DIM, int F, int H, int KV, int HD>
+template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
 __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
+    using WR = WRow<TW>;
+    typedef typename WR::raw wraw;
+    constexpr int CW = 64 * WR::V;  // columns per 16-byte load of a wavefront
     constexpr int QD = H * HD, KVD = KV * HD, QKVD = QD + 2 * KVD, G = H / KV, FD = HD / 2;
-    // P1: RPWq rows per wavefront, NCq 256-column chunks per row
-    constexpr int RQ = QKVD / kPB, RPWq = RQ / kPW, NCq = DIM / 256;
+    // P1: RPWq rows per wavefront, NCq CW-column chunks per row
+    constexpr int RQ = QKVD / kPB, RPWq = RQ / kPW, NCq = DIM / CW;
     // P3 / P5: RO (= RD) rows per block, each split over WPR wavefronts
-    constexpr int RO = DIM / kPB, WPR = kPW / RO, NCo = QD / (WPR * 256), NCd = F / (WPR * 256);
+    constexpr int RO = DIM / kPB, WPR = kPW / RO, NCo = QD / (WPR * CW), NCd = F / (WPR * CW);
     // P4: RG gate/up row pairs per block; wavefronts 0..kPW/2-1 take gate rows, the rest up rows
-    constexpr int RG = F / kPB, RPWg = 2 * RG / kPW, NCg = DIM / 256;
+    constexpr int RG = F / kPB, RPWg = 2 * RG / kPW, NCg = DIM / CW;
     static_assert(QKVD % kPB == 0 && RQ % kPW == 0 && RPWq >= 1, "QKV rows must split over the waves");
-    static_assert(DIM % 256 == 0 && DIM % kPB == 0 && RO >= 1 && kPW % RO == 0, "dim must split over the waves");
-    static_assert(QD % (WPR * 256) == 0 && F % (WPR * 256) == 0, "O / down columns must split over the waves");
+    static_assert(DIM % CW == 0 && DIM % kPB == 0 && RO >= 1 && kPW % RO == 0, "dim must split over the waves");
+    static_assert(QD % (WPR * CW) == 0 && F % (WPR * CW) == 0, "O / down columns must split over the waves");
     static_assert(F % kPB == 0 && (2 * RG) % kPW == 0 && RG % RPWg == 0 && 2 * RG <= 64, "gate/up rows");
     static_assert(HD == 128 || HD == 64, "head size");
     constexpr int XMAX = QD > F ? (QD > DIM ? QD : DIM) : (F > DIM ? F : DIM);
     // exchange layout per parity (words)
     constexpr int OFF_XA = 0, OFF_XM = DIM, OFF_QKV = 2 * DIM, OFF_PART = OFF_QKV + QKVD;
     constexpr int PART_STRIDE = HD + 2;  // o[HD], max (natural log units), sum
-    constexpr int OFF_A = OFF_PART + KV * kSMax * G * PART_STRIDE;  // merged attention output [QD]
+    constexpr int OFF_A = OFF_PART + KV * SMAX * G * PART_STRIDE;  // merged attention output [QD]
     constexpr int OFF_H = OFF_A + QD;
     constexpr int PAR_WORDS = OFF_H + F;
-    static_assert(KV * kSMax <= kPB - H && QD % kPT == 0, "attention and merge blocks must not overlap");
+    static_assert(KV * SMAX <= kPB - H && QD % kPT == 0, "attention and merge blocks must not overlap");
 
     __shared__ __attribute__((aligned(16))) float xr[DIM];    // layer input x_l
     __shared__ __attribute__((aligned(16))) float xmr[DIM];   // x_mid (after the O residual)
@@ -209,8 +258,8 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     __shared__ float2 red2[kPW];
     __shared__ __attribute__((aligned(16))) float red_acc[kPW][G][HD];
     __shared__ float red_m[kPW][G], red_l[kPW][G];
-    __shared__ __attribute__((aligned(16))) float mrg_o[kSMax][HD];  // split merge
-    __shared__ float2 mrg_ml[kSMax];
+    __shared__ __attribute__((aligned(16))) float mrg_o[SMAX][HD];  // split merge
+    __shared__ float2 mrg_ml[SMAX];
     __shared__ int dead_s;
     // the layer table, read from LDS: a global load of it inside the loop would make the wavefront
     // wait for every weight load it has in flight
@@ -227,7 +276,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     }
     const int n = pos + 1;
     int nsplit = (n + kRowsPerSplit - 1) / kRowsPerSplit;
-    nsplit = nsplit < 1 ? 1 : (nsplit > kSMax ? kSMax : nsplit);
+    nsplit = nsplit < 1 ? 1 : (nsplit > SMAX ? SMAX : nsplit);
     const int tile = (n + nsplit - 1) / nsplit;
     const float2* rope_row = p.rope_tab + (size_t)pos * FD;
     for (int i = tid0; i < p.L * (int)(sizeof(PLayer) / 8); i += kPT)
@@ -236,13 +285,13 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 
     // QKV rows: layer 0's before the loop, layer l+1's at the start of layer l's gate/up stage (whose
     // own rows are in by then; issued in the QKV stage itself: 0.697 vs 0.689 ms per C3 step)
-    float4 wq[RPWq][NCq];
-    auto load_wq = [&](const float* W, int wave, int lane) {
+    wraw wq[RPWq][NCq];
+    auto load_wq = [&](const void* W, int wave, int lane) {
         const int r0 = b * RQ + wave * RPWq;
 #pragma unroll
         for (int i = 0; i < RPWq; i++)
 #pragma unroll
-            for (int c = 0; c < NCq; c++) wq[i][c] = gld4(W, (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
+            for (int c = 0; c < NCq; c++) wq[i][c] = WR::load(W, (size_t)(r0 + i) * DIM + c * CW + lane * WR::V);
     };
     {
         STAGE_IDS();
@@ -290,13 +339,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             for (int i = 0; i < RPWq; i++) {
                 float a = 0.f;
 #pragma unroll
-                for (int c = 0; c < NCq; c++) {
-                    const float4 xx = *reinterpret_cast<const float4*>(&xin[c * 256 + lane * 4]);
-                    a = fmaf(wq[i][c].x, xx.x, a);
-                    a = fmaf(wq[i][c].y, xx.y, a);
-                    a = fmaf(wq[i][c].z, xx.z, a);
-                    a = fmaf(wq[i][c].w, xx.w, a);
-                }
+                for (int c = 0; c < NCq; c++) a = WR::dot(wq[i][c], &xin[c * CW + lane * WR::V], a);
                 a = gemv::dpp_sum_lane63(a) * rn;
                 if (lane == 63) {
                     const int row = b * RQ + wave * RPWq + i;
@@ -550,7 +593,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                     Ls = fmaf(red_l[w][gg], wt, Ls);
                     o = fmaf(red_acc[w][gg][i], wt, o);
                 }
-                uint64_t* slot = cur + OFF_PART + ((g * kSMax + s) * G + gg) * PART_STRIDE;
+                uint64_t* slot = cur + OFF_PART + ((g * SMAX + s) * G + gg) * PART_STRIDE;
                 ll_put(slot + i, ep, o);
                 if (i == 0) {
                     ll_put(slot + HD, ep, M * 0.6931471805599453f);  // natural-log units
@@ -563,15 +606,15 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         if (b >= kPB - H) {  // one block per query head (never an attention block)
             STAGE_IDS();
             // thread t: dimension t % HD of splits (t / HD) * SPT .. + SPT - 1
-            constexpr int SPT = kSMax * HD / kPT;
-            static_assert(kSMax * HD % kPT == 0 && SPT >= 1, "split merge: threads per split");
+            constexpr int SPT = SMAX * HD / kPT;
+            static_assert(SMAX * HD % kPT == 0 && SPT >= 1, "split merge: threads per split");
             const int h = b - (kPB - H), kvh = h / G, gg = h - kvh * G;
             const int i = tid % HD, s0 = (tid / HD) * SPT;
             int idx[3 * SPT];
 #pragma unroll
             for (int k = 0; k < SPT; k++) {
                 const int s = s0 + k;
-                const int slot = OFF_PART + ((kvh * kSMax + s) * G + gg) * PART_STRIDE;
+                const int slot = OFF_PART + ((kvh * SMAX + s) * G + gg) * PART_STRIDE;
                 idx[3 * k] = s < nsplit ? slot + i : -1;
                 idx[3 * k + 1] = s < nsplit && i == 0 ? slot + HD : -1;
                 idx[3 * k + 2] = s < nsplit && i == 0 ? slot + HD + 1 : -1;
@@ -589,11 +632,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             if (tid < HD) {
                 float M = -INFINITY;
 #pragma unroll
-                for (int s = 0; s < kSMax; s++)
+                for (int s = 0; s < SMAX; s++)
                     if (s < nsplit) M = fmaxf(M, mrg_ml[s].x);
                 float Ls = 0.f, o = 0.f;
 #pragma unroll
-                for (int s = 0; s < kSMax; s++)
+                for (int s = 0; s < SMAX; s++)
                     if (s < nsplit) {
                         const float w = expf(mrg_ml[s].x - M);
                         Ls = fmaf(mrg_ml[s].y, w, Ls);
@@ -605,14 +648,14 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 
         // ================= P3: O projection + residual ==============================
         lds_barrier();  // xin readers (P1) are done
-        float4 wg[RPWg][NCg];
+        wraw wg[RPWg][NCg];
         {
             STAGE_IDS();
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
-            float4 wo[NCo];
+            wraw wo[NCo];
 #pragma unroll
             for (int c = 0; c < NCo; c++)
-                wo[c] = gld4(Ly.wo, (size_t)row * QD + col0 + c * 256 + lane * 4);
+                wo[c] = WR::load(Ly.wo, (size_t)row * QD + col0 + c * CW + lane * WR::V);
             // The gate/up rows (the largest stage, 24 MB at C3) are issued here, with the O rows, so
             // they stream while the attention chain runs instead of at the start of their own stage.
             // The blocks that reach this point right after QKV (no attention, no merge) hold them back
@@ -625,12 +668,12 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             {
                 const bool up = wave >= kPW / 2;
                 const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
-                const float* W = up ? Ly.w3 : Ly.w1;
+                const void* W = up ? Ly.w3 : Ly.w1;
 #pragma unroll
                 for (int i = 0; i < RPWg; i++)
 #pragma unroll
                     for (int c = 0; c < NCg; c++)
-                        wg[i][c] = gld4(W, (size_t)(r0 + i) * DIM + c * 256 + lane * 4);
+                        wg[i][c] = WR::load(W, (size_t)(r0 + i) * DIM + c * CW + lane * WR::V);
             }
             constexpr int NA = QD / kPT;
             int idx[NA];
@@ -643,13 +686,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             lds_barrier();
             float a = 0.f;
 #pragma unroll
-            for (int c = 0; c < NCo; c++) {
-                const float4 xx = *reinterpret_cast<const float4*>(&xin[col0 + c * 256 + lane * 4]);
-                a = fmaf(wo[c].x, xx.x, a);
-                a = fmaf(wo[c].y, xx.y, a);
-                a = fmaf(wo[c].z, xx.z, a);
-                a = fmaf(wo[c].w, xx.w, a);
-            }
+            for (int c = 0; c < NCo; c++) a = WR::dot(wo[c], &xin[col0 + c * CW + lane * WR::V], a);
             a = gemv::dpp_sum_lane63(a);
             if (lane == 63) rows_s[wave] = a;
             lds_barrier();
@@ -692,13 +729,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             for (int i = 0; i < RPWg; i++) {
                 float a = 0.f;
 #pragma unroll
-                for (int c = 0; c < NCg; c++) {
-                    const float4 xx = *reinterpret_cast<const float4*>(&xin[c * 256 + lane * 4]);
-                    a = fmaf(wg[i][c].x, xx.x, a);
-                    a = fmaf(wg[i][c].y, xx.y, a);
-                    a = fmaf(wg[i][c].z, xx.z, a);
-                    a = fmaf(wg[i][c].w, xx.w, a);
-                }
+                for (int c = 0; c < NCg; c++) a = WR::dot(wg[i][c], &xin[c * CW + lane * WR::V], a);
                 a = gemv::dpp_sum_lane63(a) * rn;
                 if (lane == 63) rows_s[wave * RPWg + i] = a;
             }
@@ -715,10 +746,10 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         {
             STAGE_IDS();
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (F / WPR);
-            float4 wd[NCd];
+            wraw wd[NCd];
 #pragma unroll
             for (int c = 0; c < NCd; c++)
-                wd[c] = gld4(Ly.w2, (size_t)row * F + col0 + c * 256 + lane * 4);
+                wd[c] = WR::load(Ly.w2, (size_t)row * F + col0 + c * CW + lane * WR::V);
             constexpr int NH = F / kPT > 0 ? (F + kPT - 1) / kPT : 1;
             int idx[NH];
 #pragma unroll
@@ -731,13 +762,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             lds_barrier();
             float a = 0.f;
 #pragma unroll
-            for (int c = 0; c < NCd; c++) {
-                const float4 xx = *reinterpret_cast<const float4*>(&xin[col0 + c * 256 + lane * 4]);
-                a = fmaf(wd[c].x, xx.x, a);
-                a = fmaf(wd[c].y, xx.y, a);
-                a = fmaf(wd[c].z, xx.z, a);
-                a = fmaf(wd[c].w, xx.w, a);
-            }
+            for (int c = 0; c < NCd; c++) a = WR::dot(wd[c], &xin[col0 + c * CW + lane * WR::V], a);
             a = gemv::dpp_sum_lane63(a);
             if (lane == 63) rows_s[wave] = a;
             lds_barrier();
@@ -761,16 +786,16 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     lds_barrier();
     {
         STAGE_IDS();
-        constexpr int RB = 4, NCl = DIM / 256;
+        constexpr int RB = 4, NCl = DIM / CW;
         const int r1 = p.vocab;
         const int gw = b * kPW + wave;
-        float4 wa[RB][NCl], wb[RB][NCl];
-        auto load_batch = [&](float4 (&w)[RB][NCl], int rbase) {
+        wraw wa[RB][NCl], wb[RB][NCl];
+        auto load_batch = [&](wraw (&w)[RB][NCl], int rbase) {
 #pragma unroll
             for (int i = 0; i < RB; i++) {
                 const int r = min(rbase + i, r1 - 1);
 #pragma unroll
-                for (int c = 0; c < NCl; c++) w[i][c] = gld4(p.lm_head, (size_t)r * DIM + c * 256 + lane * 4);
+                for (int c = 0; c < NCl; c++) w[i][c] = WR::load(p.lm_head, (size_t)r * DIM + c * CW + lane * WR::V);
             }
         };
         const int first = gw * RB;
@@ -795,21 +820,21 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         }
         const float tot = block_sum(ss, red, lane, wave);
         const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
-        float4 xq[NCl];
+        float xq[NCl][WR::V];
 #pragma unroll
-        for (int c = 0; c < NCl; c++) xq[c] = *reinterpret_cast<const float4*>(&xin[c * 256 + lane * 4]);
+        for (int c = 0; c < NCl; c++)
+#pragma unroll
+            for (int v = 0; v < WR::V; v += 4) {
+                const float4 t = *reinterpret_cast<const float4*>(&xin[c * CW + lane * WR::V + v]);
+                xq[c][v] = t.x; xq[c][v + 1] = t.y; xq[c][v + 2] = t.z; xq[c][v + 3] = t.w;
+            }
         unsigned long long best = 0ull;  // (lane 63)
-        auto use_batch = [&](const float4 (&w)[RB][NCl], int rbase) {
+        auto use_batch = [&](const wraw (&w)[RB][NCl], int rbase) {
 #pragma unroll
             for (int i = 0; i < RB; i++) {
                 float a = 0.f;
 #pragma unroll
-                for (int c = 0; c < NCl; c++) {
-                    a = fmaf(w[i][c].x, xq[c].x, a);
-                    a = fmaf(w[i][c].y, xq[c].y, a);
-                    a = fmaf(w[i][c].z, xq[c].z, a);
-                    a = fmaf(w[i][c].w, xq[c].w, a);
-                }
+                for (int c = 0; c < NCl; c++) a = WR::dot(w[i][c], xq[c], a);
                 a = gemv::dpp_sum_lane63(a) * rn;
                 const int r = rbase + i;
                 if (lane == 63 && r < r1) {
@@ -835,13 +860,13 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     if (b == 0 && tid0 == 0) p.state[3] = (int)(base + (unsigned)p.L);
 }
 
-template <int DIM, int F, int H, int KV, int HD>
+template <int DIM, int F, int H, int KV, int HD, int SMAX>
 constexpr size_t ll_words() {
     constexpr int QD = H * HD, KVD = KV * HD, G = H / KV;
-    return 2 * (size_t)(2 * DIM + QD + 2 * KVD + KV * kSMax * G * (HD + 2) + QD + F);
+    return 2 * (size_t)(2 * DIM + QD + 2 * KVD + KV * SMAX * G * (HD + 2) + QD + F);
 }
 
-template <int DIM, int F, int H, int KV, int HD>
+template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
 int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     PParams p;
     p.layers = reinterpret_cast<const PLayer*>(a.layers);
@@ -849,7 +874,7 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     p.x = a.x; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.max_seq; p.rope_tab = a.rope_tab;
     p.state = a.state; p.ll = a.ll; p.err = a.err; p.eps = a.eps; p.per_head = a.per_head_norm;
     p.final_norm = a.final_norm; p.lm_head = a.lm_head; p.vocab = a.vocab; p.logits = a.logits; p.keys = a.keys;
-    auto kern = decode_persistent_kernel<DIM, F, H, KV, HD>;  // (its LDS attribute is set by fits_t)
+    auto kern = decode_persistent_kernel<TW, DIM, F, H, KV, HD, SMAX>;  // (its LDS attribute is set by fits_t)
     // A plain launch (a cooperative one measured ~20 us longer per step): every block must be resident
     // at once, which decode_persistent_supported checks (one 512-thread block per CU, kPB CUs) and
     // which holds while nothing else runs on the device; if some block were not, the others' waits
@@ -859,9 +884,9 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     return AR_HIP_OK;
 }
 
-template <int DIM, int F, int H, int KV, int HD>
+template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
 int fits_t(int* blocks_per_cu) {
-    auto kern = decode_persistent_kernel<DIM, F, H, KV, HD>;
+    auto kern = decode_persistent_kernel<TW, DIM, F, H, KV, HD, SMAX>;
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kPadLds) != hipSuccess)
         return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (const void*)kern, kPT, kPadLds) != hipSuccess)
@@ -869,30 +894,44 @@ int fits_t(int* blocks_per_cu) {
     return 1;
 }
 
+// The instantiated shapes: (weight type, dim, FFN, heads, KV heads, head size, attention splits per KV
+// head).  Qwen3-0.6B with fp32 weights (contexts of a few hundred rows: 8 splits), Qwen3-1.7B with bf16
+// weights (2K-row contexts: 28 splits of ~80 rows, 224 attention blocks).
+#define AR_PERSISTENT_SHAPES(X)                         \
+    X(AR_DTYPE_F32, float, 1024, 3072, 16, 8, 128, 8)  \
+    X(AR_DTYPE_BF16, uint16_t, 2048, 6144, 16, 8, 128, 28)
+
 }  // namespace
 
 size_t decode_persistent_layer_bytes() { return sizeof(PLayer); }
 
-size_t decode_persistent_ll_words(int dim, int F, int heads, int kv_heads, int hd) {
-    if (dim == 1024 && F == 3072 && heads == 16 && kv_heads == 8 && hd == 128) return ll_words<1024, 3072, 16, 8, 128>();
+size_t decode_persistent_ll_words(int wdtype, int dim, int F, int heads, int kv_heads, int hd) {
+#define AR_X(DT, TW, D, FF, HH, KK, HDD, SM) \
+    if (wdtype == DT && dim == D && F == FF && heads == HH && kv_heads == KK && hd == HDD) return ll_words<D, FF, HH, KK, HDD, SM>();
+    AR_PERSISTENT_SHAPES(AR_X)
+#undef AR_X
     return 0;
 }
 
-int decode_persistent_layer_entry(void* dst, const float* wqkv, const float* wo, const float* w1, const float* w3,
-                                  const float* w2, const float* attn_norm, const float* ffn_norm, const float* q_norm,
+int decode_persistent_layer_entry(void* dst, const void* wqkv, const void* wo, const void* w1, const void* w3,
+                                  const void* w2, const float* attn_norm, const float* ffn_norm, const float* q_norm,
                                   const float* k_norm, const float* bqkv) {
     PLayer e{wqkv, wo, w1, w3, w2, attn_norm, ffn_norm, q_norm, k_norm, bqkv};
     __builtin_memcpy(dst, &e, sizeof(e));
     return AR_HIP_OK;
 }
 
-bool decode_persistent_supported(int dim, int F, int heads, int kv_heads, int hd) {
-    if (decode_persistent_ll_words(dim, F, heads, kv_heads, hd) == 0) return false;
+bool decode_persistent_supported(int wdtype, int dim, int F, int heads, int kv_heads, int hd) {
+    if (decode_persistent_ll_words(wdtype, dim, F, heads, kv_heads, hd) == 0) return false;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
-    if (!fits_t<1024, 3072, 16, 8, 128>(&per_cu)) return false;
-    return per_cu >= 1 && (long long)per_cu * cus >= kPB;
+    int ok = 0;
+#define AR_X(DT, TW, D, FF, HH, KK, HDD, SM) \
+    if (wdtype == DT && dim == D && F == FF && heads == HH && kv_heads == KK && hd == HDD) ok = fits_t<TW, D, FF, HH, KK, HDD, SM>(&per_cu);
+    AR_PERSISTENT_SHAPES(AR_X)
+#undef AR_X
+    return ok && per_cu >= 1 && (long long)per_cu * cus >= kPB;
 }
 
 int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t st) {
@@ -902,9 +941,12 @@ int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t st) {
     AR_CHECK_ARG(a.vocab >= kPB, "persistent decode: vocabulary %d below %d rows", a.vocab, kPB);
     AR_CHECK_ARG(a.max_seq > 0, "persistent decode: empty cache");
     AR_CHECK_ARG(a.layer_count <= kMaxLayers, "persistent decode: %d layers exceed %d", a.layer_count, kMaxLayers);
-    if (a.dim == 1024 && a.hidden_dim == 3072 && a.heads == 16 && a.kv_heads == 8 && a.head_dim == 128)
-        return launch_t<1024, 3072, 16, 8, 128>(a, st);
-    ar_set_error("persistent decode: shape dim %d, hidden %d, heads %d/%d, head size %d has no instantiation", a.dim,
-                 a.hidden_dim, a.heads, a.kv_heads, a.head_dim);
+#define AR_X(DT, TW, D, FF, HH, KK, HDD, SM)                                                                          \
+    if (a.wdtype == DT && a.dim == D && a.hidden_dim == FF && a.heads == HH && a.kv_heads == KK && a.head_dim == HDD) \
+        return launch_t<TW, D, FF, HH, KK, HDD, SM>(a, st);
+    AR_PERSISTENT_SHAPES(AR_X)
+#undef AR_X
+    ar_set_error("persistent decode: weight type %d, dim %d, hidden %d, heads %d/%d, head size %d has no instantiation",
+                 a.wdtype, a.dim, a.hidden_dim, a.heads, a.kv_heads, a.head_dim);
     return AR_HIP_ERR_INVALID;
 }

@@ -134,7 +134,7 @@ struct ar_qwen3 {
     bool pf_w16_in_range = true;  // host copy of pf_flag[1] after the fp16 copies were made
     int pf_by_steps = 0;          // prefill calls that went through the decode step
 
-    // persistent decode step (batch 1, fp32 weights and cache): every layer, the final RMSNorm, the
+    // persistent decode step (batch 1, fp32 or bf16 weights, fp32 cache): every layer, the final RMSNorm, the
     // logits and the greedy keys in one launch (decode_persistent.hip) after the step-begin kernel
     bool pk_ok = false;          // shape, dtypes and device qualify; buffers below allocated
     bool pk_on = true;           // ar_hip_qwen3_use_persistent
@@ -346,13 +346,14 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys,
                                  m->state, B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, st));
         DecodePersistentLaunch d;
-        d.layers = m->pk_layers; d.layer_count = c.layer_count; d.dim = dim; d.hidden_dim = c.hidden_dim;
+        d.layers = m->pk_layers; d.layer_count = c.layer_count; d.wdtype = c.weight_dtype; d.dim = dim;
+        d.hidden_dim = c.hidden_dim;
         d.heads = c.head_count; d.kv_heads = c.kv_head_count; d.head_dim = c.head_size; d.x = m->x;
         d.kcache = (float*)m->kcache; d.vcache = (float*)m->vcache; d.max_seq = m->S; d.rope_tab = m->rope_tab;
         d.state = m->state; d.ll = m->pk_ll; d.err = m->pk_err; d.eps = (float)c.epsilon;
         d.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
         const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
-        d.final_norm = m->final_norm; d.lm_head = (const float*)m->lm_head; d.vocab = c.vocab_size;
+        d.final_norm = m->final_norm; d.lm_head = m->lm_head; d.vocab = c.vocab_size;
         d.logits = (store_logits || sampling) ? m->logits : nullptr; d.keys = m->am_keys;
         if (m->timed == AR_KT_LAYERS) {  // events on the stream around the launch
             AR_TRY(timed_begin(AR_KT_LAYERS));
@@ -678,11 +679,13 @@ extern "C" int ar_hip_qwen3_set_weight(ar_qwen3* m, const char* key, const void*
 static int setup_persistent(ar_qwen3* m) {
     const ar_qwen3_cfg& c = m->cfg;
     m->pk_ok = false;
-    if (m->B != 1 || c.weight_dtype != AR_DTYPE_F32 || c.kv_dtype == AR_DTYPE_F16) return AR_HIP_OK;
-    if (!decode_persistent_supported(c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size)) return AR_HIP_OK;
+    if (m->B != 1 || c.kv_dtype == AR_DTYPE_F16) return AR_HIP_OK;
+    if (!decode_persistent_supported(c.weight_dtype, c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size))
+        return AR_HIP_OK;
     const size_t eb = decode_persistent_layer_bytes();
     if (!m->pk_ll) {
-        const size_t words = decode_persistent_ll_words(c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size);
+        const size_t words =
+            decode_persistent_ll_words(c.weight_dtype, c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size);
         AR_TRY(alloc_zero(m, words * 8, (void**)&m->pk_ll));
         AR_TRY(alloc_zero(m, 64, (void**)&m->pk_err));
         AR_TRY(alloc_zero(m, eb * c.layer_count, &m->pk_layers));
@@ -690,8 +693,7 @@ static int setup_persistent(ar_qwen3* m) {
     std::vector<char> tab(eb * c.layer_count);
     for (int l = 0; l < c.layer_count; l++) {
         const Layer& L = m->layers[l];
-        AR_TRY(decode_persistent_layer_entry(tab.data() + l * eb, (const float*)L.wqkv, (const float*)L.wo,
-                                             (const float*)L.w1, (const float*)L.w3, (const float*)L.w2, L.attn_norm,
+        AR_TRY(decode_persistent_layer_entry(tab.data() + l * eb, L.wqkv, L.wo, L.w1, L.w3, L.w2, L.attn_norm,
                                              L.ffn_norm, L.q_norm, L.k_norm, L.bqkv));
     }
     AR_HIP_TRY(hipMemcpyAsync(m->pk_layers, tab.data(), tab.size(), hipMemcpyHostToDevice, m->ctx->stream));

@@ -115,3 +115,46 @@ def test_c4_workload_2048_vs_oracle(ctx):
         assert len(set(fed.tolist())) >= 3, f"degenerate reference stream {fed.tolist()}"
         compared = _check_against(f"C4 seq {b} vs oracle", lp[b], toks[b], lgs[b], fed, rl)
         assert len(compared) >= 2, compared
+
+
+def test_c4_workload_batch1_persistent_vs_oracle_and_multi_launch(ctx):
+    """The persistent decode kernel with bf16 weights (the Qwen3-1.7B layer shape at batch 1, the C4
+    decode configuration): a 2048-token prompt through the batched prefill, then 16 greedy steps in
+    the persistent kernel (28 attention splits per KV head over the 2K-row cache), against the FP32
+    oracle; the same steps as separate launches agree within float rounding (1e-5).  A 40-token
+    prompt fed one token per step covers the short-context splits (1-2 per KV head) the same way."""
+    T, steps = C.C4_PROMPT, 16
+    cfg = dataclasses.replace(C.C4_1_7B, layer_count=2, vocab_size=4096, shared_weights=False,
+                              seq_len=T + steps + 8, max_batch=1)
+    sd = synthetic.state_dict(cfg, seed=21)
+    prompt = synthetic.prompt_ids(T, cfg.vocab_size, seed=22)
+    short = synthetic.prompt_ids(40, cfg.vocab_size, seed=23)
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        assert am.persistent, "the bf16 C4 shape should run the persistent decode kernel"
+        runs = {}
+        for persistent in (True, False):
+            am.use_persistent(persistent)
+            assert am.persistent == persistent
+            am.reset()
+            am.set_prompt(prompt)
+            lp = am.prefill(return_logits=True)
+            toks, lgs = [], []
+            for _ in range(steps):
+                t, lg = am.next(return_logits=True)
+                toks.append(t)
+                lgs.append(lg)
+            am.reset()
+            am.set_prompt(short)
+            sl = [am.next(return_logits=True)[1] for _ in range(len(short) + 8)]
+            runs[persistent] = (lp, np.stack(toks, axis=1), np.stack(lgs, axis=1), np.stack(sl, axis=1))
+        am.use_persistent(True)
+    lp, toks, lgs, sl = runs[True]
+    fed, rl = _oracle_stream(cfg, sd, prompt, steps)
+    assert len(set(fed.tolist())) >= 3, f"degenerate reference stream {fed.tolist()}"
+    compared = _check_against("C4 batch 1 persistent vs oracle", lp[0], toks[0], lgs[0], fed, rl)
+    assert len(compared) >= 2, compared
+    lp_m, toks_m, lgs_m, sl_m = runs[False]
+    assert np.array_equal(toks, toks_m)
+    assert rel_err(lgs[0], lgs_m[0]) <= 1e-5, rel_err(lgs[0], lgs_m[0])
+    assert rel_err(sl[0], sl_m[0]) <= 1e-5, rel_err(sl[0], sl_m[0])
