@@ -164,6 +164,18 @@ __host__ __device__ inline void bf16_planes(float v, uint16_t* hi, uint16_t* lo)
 
 constexpr int kArgmaxSlots = 1024;
 
+// The value held by lane ^ 16 (permlane16_swap of v with itself: the first result holds the even
+// rows in both halves of each row pair, the second the odd rows), without the LDS crossbar.
+__device__ inline float xor16(float v, int lane) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((lane & 16) ? r[0] : r[1]);
+}
+// The value held by lane ^ 32 (permlane32_swap: lower half in the first result, upper in the second).
+__device__ inline float xor32(float v, int lane) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((lane & 32) ? r[0] : r[1]);
+}
+
 // fp32 values from 65520 up (and infinities) round to an infinite fp16.  The prefill path stores
 // its MFMA operands as fp16; every conversion checks this and marks *range_flag (when given), so the
 // caller can recompute without fp16 operands instead of carrying an infinity.

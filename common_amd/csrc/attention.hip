@@ -106,17 +106,6 @@ __device__ inline float wave_max_lane63(float v) {
     v = dpp_max_step<0x143, 0xC>(v);
     return v;
 }
-// the value held by lane ^ 16 (permlane16_swap of v with itself: the first result holds the
-// even rows in both halves of each row pair, the second the odd rows)
-__device__ inline float xor16(float v, int lane) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float((lane & 16) ? r[0] : r[1]);
-}
-// the value held by lane ^ 32 (permlane32_swap: lower half in the first result, upper in the second)
-__device__ inline float xor32(float v, int lane) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float((lane & 32) ? r[0] : r[1]);
-}
 
 // (cos, sin) of pos * exp(f * -2 ln(theta) / hd): from the table the model precomputes in
 // double on the host, or evaluated here in double when no table is given.

@@ -240,7 +240,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     constexpr int PART_STRIDE = HD + 2;  // o[HD], max (natural log units), sum
     constexpr int OFF_A = OFF_PART + KV * SMAX * G * PART_STRIDE;  // merged attention output [QD]
     constexpr int OFF_H = OFF_A + QD;
-    constexpr int PAR_WORDS = OFF_H + F;
+    // sums of squares of each QKV block's rows (q blocks, then k blocks) for the QK-norm
+    constexpr int NSQ = QD / RQ, NSK = KVD / RQ;
+    constexpr int OFF_SS = OFF_H + F;
+    constexpr int PAR_WORDS = OFF_SS + NSQ + NSK;
+    static_assert(QD % RQ == 0 && KVD % RQ == 0 && HD % RQ == 0, "a QKV block's rows lie in one head");
     static_assert(KV * SMAX <= kPB - H && QD % kPT == 0, "attention and merge blocks must not overlap");
 
     __shared__ __attribute__((aligned(16))) float xr[DIM];    // layer input x_l
@@ -249,12 +253,10 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     __shared__ float red[kPW];
     __shared__ float rows_s[64];
     // attention
-    __shared__ __attribute__((aligned(16))) float qraw[G][HD];
     __shared__ __attribute__((aligned(16))) float q_s[G][HD];
-    __shared__ __attribute__((aligned(16))) float kraw[HD];
     __shared__ __attribute__((aligned(16))) float k_new[HD];
     __shared__ __attribute__((aligned(16))) float v_new[HD];
-    __shared__ float rnorm[G + 1];
+    __shared__ float ss_s[(G + 1) * (HD / RQ)];  // per-head QK-norm: the partial sums of the block's heads
     __shared__ float2 red2[kPW];
     __shared__ __attribute__((aligned(16))) float red_acc[kPW][G][HD];
     __shared__ float red_m[kPW][G], red_l[kPW][G];
@@ -335,6 +337,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
             const float tot = block_sum(ss, red, lane, wave);  // (its barrier also publishes xr / xin)
             const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
+            float ssq = 0.f;
 #pragma unroll
             for (int i = 0; i < RPWq; i++) {
                 float a = 0.f;
@@ -343,7 +346,21 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 a = gemv::dpp_sum_lane63(a) * rn;
                 if (lane == 63) {
                     const int row = b * RQ + wave * RPWq + i;
-                    ll_put(cur + OFF_QKV + row, ep, Ly.bqkv ? a + gld(Ly.bqkv, row) : a);
+                    const float v = Ly.bqkv ? a + gld(Ly.bqkv, row) : a;
+                    ll_put(cur + OFF_QKV + row, ep, v);
+                    ssq = fmaf(v, v, ssq);
+                }
+            }
+            // a block of q or k rows also publishes their sum of squares: the attention blocks then
+            // wait for NSQ + NSK partial sums instead of every q and k value
+            if (b < NSQ + NSK) {
+                if (lane == 63) rows_s[wave] = ssq;
+                lds_barrier();
+                if (tid == 0) {
+                    float t = 0.f;
+#pragma unroll
+                    for (int w = 0; w < kPW; w++) t += rows_s[w];
+                    ll_put(cur + OFF_SS + b, ep, t);
                 }
             }
         }
@@ -378,14 +395,17 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 load_rows(kr, kc, 0);
                 load_rows(vr, vc, 0);
             }
+            // thread layout: q rotation pairs of the G heads, k pairs, v values, QK-norm partial sums
+            constexpr int RPH = HD / RQ;                           // QKV blocks per head
+            constexpr int T_K = G * FD, T_V = T_K + FD, T_S = T_V + HD;
+            static_assert(T_S + NSQ + NSK <= kPT && T_S + (G + 1) * RPH <= kPT, "attention thread layout");
             // this thread's rotation pair and QK-norm gains, also ahead of the wait
-            static_assert((G + 1) * FD <= kPT, "one rotation pair per thread");
-            const int rj = tid / FD, rf = tid - rj * FD;
+            const int rj = tid / FD, rf = tid - rj * FD;  // (tid < T_V: vector rj = q head g*G+rj, or k)
             float2 rcs = make_float2(1.f, 0.f);
             float rg1 = 1.f, rg2 = 1.f;
-            if (tid < (G + 1) * FD) {
+            const float* gn = rj < G ? Ly.q_norm : Ly.k_norm;
+            if (tid < T_V) {
                 rcs = rope_row[rf];
-                const float* gn = rj < G ? Ly.q_norm : Ly.k_norm;
                 const size_t o = rj < G ? (size_t)(g * G + rj) * HD : (size_t)g * HD;
                 if (gn) {
                     rg1 = gld(gn, o + rf);
@@ -393,96 +413,69 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 }
             }
             asm volatile("" ::: "memory");  // (keeps these loads ahead of the polls)
-            // this step's q and k (all of both for the whole-vector QK-norm, else the G heads and KV
-            // head g) and v of KV head g
-            {
-                constexpr int NQW = QD + KVD + HD;
-                constexpr int NQ = (NQW + kPT - 1) / kPT;
-                int idx[NQ];
-#pragma unroll
-                for (int j = 0; j < NQ; j++) {
-                    const int i = tid + j * kPT;
-                    int w = -1;
-                    if (i < QD) {
-                        if (!p.per_head || i / (G * HD) == g) w = OFF_QKV + i;
-                    } else if (i < QD + KVD) {
-                        if (!p.per_head || (i - QD) / HD == g) w = OFF_QKV + i;
-                    } else if (i < NQW) {
-                        w = OFF_QKV + QD + KVD + g * HD + (i - QD - KVD);
-                    }
-                    idx[j] = w;
-                }
-                float qv[NQ];
-                ll_wait<NQ>(cur, idx, qv, ep, dead, p.err);
-                float sq = 0.f, sk = 0.f;  // words not waited for read as 0
-#pragma unroll
-                for (int j = 0; j < NQ; j++) {
-                    const int i = tid + j * kPT;
-                    if (i < QD) {
-                        sq = fmaf(qv[j], qv[j], sq);
-                        if (i / (G * HD) == g) qraw[(i - g * G * HD) / HD][i % HD] = qv[j];
-                    } else if (i < QD + KVD) {
-                        sk = fmaf(qv[j], qv[j], sk);
-                        if ((i - QD) / HD == g) kraw[(i - QD) % HD] = qv[j];
-                    } else if (i < NQW) {
-                        v_new[i - QD - KVD] = qv[j];
-                    }
-                }
+            int idx[2] = {-1, -1};
+            if (tid < T_K) {
+                idx[0] = OFF_QKV + (g * G + rj) * HD + rf;
+                idx[1] = idx[0] + FD;
+            } else if (tid < T_V) {
+                idx[0] = OFF_QKV + QD + g * HD + rf;
+                idx[1] = idx[0] + FD;
+            } else if (tid < T_S) {
+                idx[0] = OFF_QKV + QD + KVD + g * HD + (tid - T_V);
+            } else if (p.per_head) {  // the partial sums of heads g*G .. g*G+G-1 and of KV head g
+                const int i = tid - T_S, h = i / RPH, k = i - h * RPH;
+                if (h < G) idx[0] = OFF_SS + (g * G + h) * RPH + k;
+                else if (h == G) idx[0] = OFF_SS + NSQ + g * RPH + k;
+            } else if (tid - T_S < NSQ + NSK) {  // every q and k partial: one RMS over each vector
+                idx[0] = OFF_SS + (tid - T_S);
+            }
+            float qv[2];
+            ll_wait<2>(cur, idx, qv, ep, dead, p.err);  // (words not waited for read as 0)
+            if (p.per_head) {
+                if (tid >= T_S && tid - T_S < (G + 1) * RPH) ss_s[tid - T_S] = qv[0];
+            } else {
+                const bool isq = tid >= T_S && tid - T_S < NSQ;
+                float sq = isq ? qv[0] : 0.f, sk = (tid >= T_S && !isq) ? qv[0] : 0.f;
                 sq = gemv::dpp_sum_lane63(sq);
                 sk = gemv::dpp_sum_lane63(sk);
                 if (lane == 63) red2[wave] = make_float2(sq, sk);
             }
-            lds_barrier();
-            if (p.per_head) {  // wavefront w reduces vector w (q heads, then k)
-                for (int j = wave; j < G + 1; j += kPW) {
-                    const float* src = j < G ? qraw[j] : kraw;
-                    float sq = 0.f;
-                    for (int i = lane; i < HD; i += 64) sq = fmaf(src[i], src[i], sq);
-                    sq = gemv::dpp_sum_lane63(sq);
-                    if (lane == 63) rnorm[j] = 1.0f / sqrtf(sq / (float)HD + p.eps);
-                }
-            } else if (tid == 0) {  // one RMS over the whole q and the whole k vector
-                float tq = 0.f, tk = 0.f;
-#pragma unroll
-                for (int w = 0; w < kPW; w++) {
-                    tq += red2[w].x;
-                    tk += red2[w].y;
-                }
-                const float rq = 1.0f / sqrtf(tq / (float)QD + p.eps), rk = 1.0f / sqrtf(tk / (float)KVD + p.eps);
-#pragma unroll
-                for (int j = 0; j < G; j++) rnorm[j] = rq;
-                rnorm[G] = rk;
-            }
+            if (tid >= T_V && tid < T_S) v_new[tid - T_V] = qv[0];
             lds_barrier();
             const bool has_pos = pos >= t0 && pos < t1;
-            // normalised, rotated q (G heads) and k; the block holding pos writes the cache rows
-            if (tid < (G + 1) * FD) {
-                const int j = rj, f = rf;
-                const float2 cs = rcs;
-                if (j < G) {
-                    float x1 = qraw[j][f], x2 = qraw[j][f + FD];
-                    if (Ly.q_norm) {  // gains span the whole q vector
-                        x1 = (rg1 * x1) * rnorm[j];
-                        x2 = (rg2 * x2) * rnorm[j];
-                    }
-                    q_s[j][f] = x1 * cs.x - x2 * cs.y;
-                    q_s[j][f + FD] = x2 * cs.x + x1 * cs.y;
+            // normalised, rotated q (G heads) and k from the pair this thread holds; the block holding
+            // pos writes the cache rows
+            if (tid < T_V) {
+                float tot = 0.f;
+                if (p.per_head) {
+#pragma unroll
+                    for (int k = 0; k < RPH; k++) tot += ss_s[rj * RPH + k];
                 } else {
-                    float x1 = kraw[f], x2 = kraw[f + FD];
-                    if (Ly.k_norm) {
-                        x1 = (rg1 * x1) * rnorm[G];
-                        x2 = (rg2 * x2) * rnorm[G];
-                    }
-                    const float o1 = x1 * cs.x - x2 * cs.y, o2 = x2 * cs.x + x1 * cs.y;
-                    k_new[f] = o1;
-                    k_new[f + FD] = o2;
+#pragma unroll
+                    for (int w = 0; w < kPW; w++) tot += rj < G ? red2[w].x : red2[w].y;
+                }
+                const float nv = p.per_head ? (float)HD : (rj < G ? (float)QD : (float)KVD);
+                const float r = 1.0f / sqrtf(tot / nv + p.eps);
+                float x1 = qv[0], x2 = qv[1];
+                if (gn) {  // (q gains span the whole q vector, as the k gains the k vector)
+                    x1 = (rg1 * x1) * r;
+                    x2 = (rg2 * x2) * r;
+                }
+                const float o1 = x1 * rcs.x - x2 * rcs.y, o2 = x2 * rcs.x + x1 * rcs.y;
+                if (rj < G) {
+                    q_s[rj][rf] = o1;
+                    q_s[rj][rf + FD] = o2;
+                } else {
+                    k_new[rf] = o1;
+                    k_new[rf + FD] = o2;
                     if (has_pos) {
-                        kc[(size_t)pos * HD + f] = o1;
-                        kc[(size_t)pos * HD + f + FD] = o2;
+                        kc[(size_t)pos * HD + rf] = o1;
+                        kc[(size_t)pos * HD + rf + FD] = o2;
                     }
                 }
+            } else if (tid < T_S && has_pos) {
+                vc[(size_t)pos * HD + (tid - T_V)] = qv[0];
             }
-            if (has_pos && tid < HD) vc[(size_t)pos * HD + tid] = v_new[tid];
             lds_barrier();
 
             const float c2 = 1.4426950408889634f / sqrtf((float)HD);
@@ -554,21 +547,21 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 if (c + 1 < nch) load_rows(vr, vc, c + 1);
             }
             // merge the row groups: the four of a wavefront by lane swaps, the wavefronts via LDS
-            auto merge_with = [&](int xmask) {
+            auto merge_with = [&](auto partner) {
 #pragma unroll
                 for (int gg = 0; gg < G; gg++) {
-                    const float mo = __shfl_xor(m[gg], xmask, 64), lo = __shfl_xor(lsum[gg], xmask, 64);
+                    const float mo = partner(m[gg]), lo = partner(lsum[gg]);
                     const float mn = fmaxf(m[gg], mo);
                     const float a = (m[gg] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[gg] - mn);
                     const float bo = (mo == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mo - mn);
                     lsum[gg] = lsum[gg] * a + lo * bo;
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) acc[gg][e] = acc[gg][e] * a + __shfl_xor(acc[gg][e], xmask, 64) * bo;
+                    for (int e = 0; e < EPL; e++) acc[gg][e] = acc[gg][e] * a + partner(acc[gg][e]) * bo;
                     m[gg] = mn;
                 }
             };
-            merge_with(16);
-            merge_with(32);
+            merge_with([&](float v) { return xor16(v, lane); });
+            merge_with([&](float v) { return xor32(v, lane); });
             if (lane < 16) {
 #pragma unroll
                 for (int gg = 0; gg < G; gg++) {
@@ -602,9 +595,39 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
         }
 
+        // O rows and gate/up rows of this block (held from their issue to the O and gate/up stages)
+        wraw wo[NCo];
+        wraw wg[RPWg][NCg];
+        auto issue_o_gu = [&](int wave, int lane) {
+            const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
+#pragma unroll
+            for (int c = 0; c < NCo; c++)
+                wo[c] = WR::load(Ly.wo, (size_t)row * QD + col0 + c * CW + lane * WR::V);
+            // The blocks that are not busy with attention hold the gate/up rows back kGateUpDelay
+            // after their QKV stage: issued at once they queue in HBM ahead of the attention's cache
+            // rows and exchanges (measured at C3, ms per step: at once 0.711, after 1.5 / 2 / 2.5 /
+            // 3 / 4 us 0.699 / 0.696 / 0.696 / 0.696 / 0.709, in their own stage 0.712; the down rows
+            // issued here as well, after 4-5.5 us: 0.709-0.716).
+            if (b >= KV * nsplit)
+                while (wall_clock64() < t_p1 + kGateUpDelay) __builtin_amdgcn_s_sleep(4);
+            const bool up = wave >= kPW / 2;
+            const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
+            const void* W = up ? Ly.w3 : Ly.w1;
+#pragma unroll
+            for (int i = 0; i < RPWg; i++)
+#pragma unroll
+                for (int c = 0; c < NCg; c++) wg[i][c] = WR::load(W, (size_t)(r0 + i) * DIM + c * CW + lane * WR::V);
+        };
+
         // ================= P2b: merge the splits of each query head ==================
+        // The merge blocks' O and gate/up rows stream while the attention runs: issued after the
+        // merge, they arrive last of all and hold up every block's gate/up input (C3: 0.668 ->
+        // 0.635 ms per step).  Where the rows and the merge's words do not fit in registers together
+        // (bf16 at d 2048: 96 VGPRs of gate/up rows, 28 splits), they follow the merge.
+        constexpr bool kMergeIssuesEarly = RPWg * NCg <= 12;
         if (b >= kPB - H) {  // one block per query head (never an attention block)
             STAGE_IDS();
+            if (kMergeIssuesEarly) issue_o_gu(wave, lane);
             // thread t: dimension t % HD of splits (t / HD) * SPT .. + SPT - 1
             constexpr int SPT = SMAX * HD / kPT;
             static_assert(SMAX * HD % kPT == 0 && SPT >= 1, "split merge: threads per split");
@@ -648,33 +671,13 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 
         // ================= P3: O projection + residual ==============================
         lds_barrier();  // xin readers (P1) are done
-        wraw wg[RPWg][NCg];
         {
             STAGE_IDS();
-            const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
-            wraw wo[NCo];
-#pragma unroll
-            for (int c = 0; c < NCo; c++)
-                wo[c] = WR::load(Ly.wo, (size_t)row * QD + col0 + c * CW + lane * WR::V);
-            // The gate/up rows (the largest stage, 24 MB at C3) are issued here, with the O rows, so
-            // they stream while the attention chain runs instead of at the start of their own stage.
-            // The blocks that reach this point right after QKV (no attention, no merge) hold them back
-            // kGateUpDelay after their QKV stage: issued at once they queue in HBM ahead of the
-            // attention's cache rows and exchanges (measured at C3, ms per step: at once 0.711,
-            // after 1.5 / 2 / 2.5 / 3 / 4 us 0.699 / 0.696 / 0.696 / 0.696 / 0.709, in their own
-            // stage 0.712; the down rows issued here as well, after 4-5.5 us: 0.709-0.716).
-            if (b >= KV * nsplit && b < kPB - H)
-                while (wall_clock64() < t_p1 + kGateUpDelay) __builtin_amdgcn_s_sleep(4);
-            {
-                const bool up = wave >= kPW / 2;
-                const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
-                const void* W = up ? Ly.w3 : Ly.w1;
-#pragma unroll
-                for (int i = 0; i < RPWg; i++)
-#pragma unroll
-                    for (int c = 0; c < NCg; c++)
-                        wg[i][c] = WR::load(W, (size_t)(r0 + i) * DIM + c * CW + lane * WR::V);
-            }
+            const int col0 = (wave % WPR) * (QD / WPR);
+            // The gate/up rows (the largest stage, 24 MB at C3) are issued with the O rows, so they
+            // stream while the attention chain runs instead of at the start of their own stage (the
+            // merge blocks issued both before their merge).
+            if (b < kPB - H || !kMergeIssuesEarly) issue_o_gu(wave, lane);
             constexpr int NA = QD / kPT;
             int idx[NA];
 #pragma unroll
@@ -863,7 +866,8 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 template <int DIM, int F, int H, int KV, int HD, int SMAX>
 constexpr size_t ll_words() {
     constexpr int QD = H * HD, KVD = KV * HD, G = H / KV;
-    return 2 * (size_t)(2 * DIM + QD + 2 * KVD + KV * SMAX * G * (HD + 2) + QD + F);
+    constexpr int RQ = (QD + 2 * KVD) / kPB;
+    return 2 * (size_t)(2 * DIM + QD + 2 * KVD + KV * SMAX * G * (HD + 2) + QD + F + (QD + KVD) / RQ);
 }
 
 template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
