@@ -164,6 +164,46 @@ __host__ __device__ inline void bf16_planes(float v, uint16_t* hi, uint16_t* lo)
 
 constexpr int kArgmaxSlots = 1024;
 
+// Cross-lane steps without the LDS crossbar (ds_bpermute): DPP within 16-lane rows, gfx950's
+// permlane swaps across rows (below).
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, true));
+}
+// sum over each 16-lane row, in every lane of the row: quad swaps, half-row mirror, row mirror
+__device__ inline float row16_sum(float v) {
+    v += dpp_mov<0xB1, 0xF>(v);   // quad_perm 1,0,3,2
+    v += dpp_mov<0x4E, 0xF>(v);   // quad_perm 2,3,0,1
+    v += dpp_mov<0x141, 0xF>(v);  // row_half_mirror: the other quad of the half row
+    v += dpp_mov<0x140, 0xF>(v);  // row_mirror: the other half row
+    return v;
+}
+// total over the 64 lanes, in lane 63 only (row shifts, then row broadcasts)
+__device__ inline float wave_sum_lane63(float v) {
+    v += dpp_mov<0xB1, 0xF>(v);
+    v += dpp_mov<0x4E, 0xF>(v);
+    v += dpp_mov<0x114, 0xF>(v);  // row_shr:4
+    v += dpp_mov<0x118, 0xF>(v);  // row_shr:8
+    v += dpp_mov<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_mov<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+// maximum over the 64 lanes, in lane 63 only (lanes without a source read -inf)
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_max_step(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), CTRL,
+                                                               ROW_MASK, 0xF, false)));
+}
+__device__ inline float wave_max_lane63(float v) {
+    v = dpp_max_step<0xB1, 0xF>(v);
+    v = dpp_max_step<0x4E, 0xF>(v);
+    v = dpp_max_step<0x114, 0xF>(v);
+    v = dpp_max_step<0x118, 0xF>(v);
+    v = dpp_max_step<0x142, 0xA>(v);
+    v = dpp_max_step<0x143, 0xC>(v);
+    return v;
+}
+
 // The value held by lane ^ 16 (permlane16_swap of v with itself: the first result holds the even
 // rows in both halves of each row pair, the second the odd rows), without the LDS crossbar.
 __device__ inline float xor16(float v, int lane) {

@@ -283,8 +283,8 @@ __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f32_v4_kernel(float* x,
 }
 
 // The fold + row RMSNorm above with 16-byte accesses and the row held in registers (one read of x
-// and of each part, one write of x and of the fp16 row): n % 4 == 0, n <= NV * 1024.  Each value
-// is folded in the same order (x, then parts in slice order).
+// and of each part, one write of x and of the fp16 row): n % 4 == 0, n <= NV * 1024, nparts <= 4.
+// Each value is folded in the same order (x, then parts in slice order), its parts loaded together.
 template <int NV>
 __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_v4_kernel(float* x, const float* parts, int nparts,
                                                                         size_t part_stride, const float* w,
@@ -299,11 +299,16 @@ __global__ __launch_bounds__(256) void fold_rmsnorm_rows_f16_v4_kernel(float* x,
     for (int j = 0; j < NV; j++) {
         const int i = threadIdx.x + 256 * j;
         if (i < n4) {
+            float4 q[4];  // every part loaded before the adds (nparts <= 4)
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+                if (s < nparts) q[s] = reinterpret_cast<const float4*>(parts + s * part_stride + row)[i];
             float4 a = xr[i];
-            for (int s = 0; s < nparts; s++) {
-                const float4 q = reinterpret_cast<const float4*>(parts + s * part_stride + row)[i];
-                a.x += q.x; a.y += q.y; a.z += q.z; a.w += q.w;
-            }
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+                if (s < nparts) {
+                    a.x += q[s].x; a.y += q[s].y; a.z += q[s].z; a.w += q[s].w;
+                }
             if (nparts) xr[i] = a;
             v[j] = a;
             ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
@@ -754,7 +759,7 @@ int launch_fold_rmsnorm_rows_f16(float* x, const float* parts, int nparts, const
                                  int n, float eps, int* range_flag, hipStream_t stream) {
     AR_CHECK_ARG(x && w && out && rows > 0 && n > 0 && nparts >= 0 && (parts || nparts == 0),
                  "fold rmsnorm rows: bad arguments");
-    const bool v4 = n % 4 == 0 && n <= 4096 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+    const bool v4 = n % 4 == 0 && n <= 4096 && nparts <= 4 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0 &&
                     (nparts == 0 || (reinterpret_cast<uintptr_t>(parts) & 15) == 0);
     if (v4 && n <= 1024)
