@@ -347,3 +347,29 @@ def test_model_state_errors(ctx, c1):
         with pytest.raises(hw.HardwareException) as e:
             m.set_weight("model.layers.99.mlp.up_proj.weight", np.zeros(4, np.float32))
         assert e.value.code == hw.AR_HIP_ERR_NOT_FOUND
+
+
+def test_c3_persistent_per_head_norm_and_bias_match_multi_launch(ctx):
+    """The persistent kernel's per-head QK-norm (the partial sums of a head's eight QKV blocks) and
+    the q/k/v bias, on a C3-shape model with both: 24 prompt tokens fed one per step, then 16 greedy
+    steps, against the same steps as separate launches (tokens equal up to a near-tie, logits 1e-5)
+    and the first steps against the FP32 oracle."""
+    cfg = dataclasses.replace(C.C3_0_6B, layer_count=4, vocab_size=4096, shared_weights=False,
+                              qk_norm_mode=C.QK_NORM_PER_HEAD, qkv_bias=True, seq_len=64)
+    prompt = synthetic.prompt_ids(24, cfg.vocab_size, seed=5)
+    sd = synthetic.state_dict(cfg, seed=5)
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        assert am.persistent
+        fed_p, lg_p = gpu_generate(m, prompt, 16)
+        am.use_persistent(False)
+        fed_m, lg_m = gpu_generate(m, prompt, 16)
+        am.use_persistent(True)
+    stop = compare_tokens(fed_p[0], fed_m[0], lg_m[0], len(prompt))
+    assert stop == fed_m.shape[1], f"near-tie at step {stop}"
+    assert rel_err(lg_p[0], lg_m[0]) <= 1e-5
+    ref = oracle.OracleQwen3(cfg, sd, precision="fp32")
+    rf, rl = ref.generate(prompt, 16)
+    ref.close()
+    assert compare_tokens(fed_p[0], rf, rl, len(prompt)) == len(rf)
+    assert rel_err(lg_p[0], rl) <= LOGIT_TOL_F32
