@@ -598,25 +598,29 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         // O rows and gate/up rows of this block (held from their issue to the O and gate/up stages)
         wraw wo[NCo];
         wraw wg[RPWg][NCg];
-        auto issue_o_gu = [&](int wave, int lane) {
+        // issue_o_gu(wave, lane, i0, i1): the O rows (when i0 == 0) and gate/up rows i0 .. i1-1 of the wavefront
+        auto issue_o_gu = [&](int wave, int lane, int i0, int i1) {
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
+            if (i0 == 0) {
 #pragma unroll
-            for (int c = 0; c < NCo; c++)
-                wo[c] = WR::load(Ly.wo, (size_t)row * QD + col0 + c * CW + lane * WR::V);
+                for (int c = 0; c < NCo; c++)
+                    wo[c] = WR::load(Ly.wo, (size_t)row * QD + col0 + c * CW + lane * WR::V);
+            }
             // The blocks that are not busy with attention hold the gate/up rows back kGateUpDelay
             // after their QKV stage: issued at once they queue in HBM ahead of the attention's cache
             // rows and exchanges (measured at C3, ms per step: at once 0.711, after 1.5 / 2 / 2.5 /
             // 3 / 4 us 0.699 / 0.696 / 0.696 / 0.696 / 0.709, in their own stage 0.712; the down rows
             // issued here as well, after 4-5.5 us: 0.709-0.716).
-            if (b >= KV * nsplit)
+            if (b >= KV * nsplit && i0 == 0)
                 while (wall_clock64() < t_p1 + kGateUpDelay) __builtin_amdgcn_s_sleep(4);
             const bool up = wave >= kPW / 2;
             const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
             const void* W = up ? Ly.w3 : Ly.w1;
 #pragma unroll
             for (int i = 0; i < RPWg; i++)
+                if (i >= i0 && i < i1)
 #pragma unroll
-                for (int c = 0; c < NCg; c++) wg[i][c] = WR::load(W, (size_t)(r0 + i) * DIM + c * CW + lane * WR::V);
+                    for (int c = 0; c < NCg; c++) wg[i][c] = WR::load(W, (size_t)(r0 + i) * DIM + c * CW + lane * WR::V);
         };
 
         // ================= P2b: merge the splits of each query head ==================
@@ -624,10 +628,10 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         // merge, they arrive last of all and hold up every block's gate/up input (C3: 0.668 ->
         // 0.635 ms per step).  Where the rows and the merge's words do not fit in registers together
         // (bf16 at d 2048: 96 VGPRs of gate/up rows, 28 splits), they follow the merge.
-        constexpr bool kMergeIssuesEarly = RPWg * NCg <= 12;
+        constexpr int kMergeEarlyRows = RPWg * NCg <= 12 ? RPWg : RPWg / 3;
         if (b >= kPB - H) {  // one block per query head (never an attention block)
             STAGE_IDS();
-            if (kMergeIssuesEarly) issue_o_gu(wave, lane);
+            issue_o_gu(wave, lane, 0, kMergeEarlyRows);
             // thread t: dimension t % HD of splits (t / HD) * SPT .. + SPT - 1
             constexpr int SPT = SMAX * HD / kPT;
             static_assert(SMAX * HD % kPT == 0 && SPT >= 1, "split merge: threads per split");
@@ -677,7 +681,8 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // The gate/up rows (the largest stage, 24 MB at C3) are issued with the O rows, so they
             // stream while the attention chain runs instead of at the start of their own stage (the
             // merge blocks issued both before their merge).
-            if (b < kPB - H || !kMergeIssuesEarly) issue_o_gu(wave, lane);
+            if (b < kPB - H) issue_o_gu(wave, lane, 0, RPWg);
+            else if (kMergeEarlyRows < RPWg) issue_o_gu(wave, lane, kMergeEarlyRows, RPWg);
             constexpr int NA = QD / kPT;
             int idx[NA];
 #pragma unroll
@@ -891,6 +896,10 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
 template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
 int fits_t(int* blocks_per_cu) {
     auto kern = decode_persistent_kernel<TW, DIM, F, H, KV, HD, SMAX>;
+    // no private (scratch) memory: the dispatcher may hold back waves that need scratch beyond the
+    // runtime's scratch allocation, and every block of this kernel must be resident at once
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, (const void*)kern) != hipSuccess || fa.localSizeBytes != 0) return 0;
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kPadLds) != hipSuccess)
         return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (const void*)kern, kPT, kPadLds) != hipSuccess)
