@@ -636,24 +636,26 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             constexpr int SPT = SMAX * HD / kPT;
             static_assert(SMAX * HD % kPT == 0 && SPT >= 1, "split merge: threads per split");
             const int h = b - (kPB - H), kvh = h / G, gg = h - kvh * G;
+            // and thread t < 2 * SMAX: the maximum (even t) or the sum (odd t) of split t / 2
+            static_assert(2 * SMAX <= kPT, "split merge: one (max, sum) word per thread");
             const int i = tid % HD, s0 = (tid / HD) * SPT;
-            int idx[3 * SPT];
+            int idx[SPT + 1];
 #pragma unroll
             for (int k = 0; k < SPT; k++) {
                 const int s = s0 + k;
-                const int slot = OFF_PART + ((kvh * SMAX + s) * G + gg) * PART_STRIDE;
-                idx[3 * k] = s < nsplit ? slot + i : -1;
-                idx[3 * k + 1] = s < nsplit && i == 0 ? slot + HD : -1;
-                idx[3 * k + 2] = s < nsplit && i == 0 ? slot + HD + 1 : -1;
+                idx[k] = s < nsplit ? OFF_PART + ((kvh * SMAX + s) * G + gg) * PART_STRIDE + i : -1;
             }
-            float v[3 * SPT];
-            ll_wait<3 * SPT>(cur, idx, v, ep, dead, p.err);
+            const int sml = tid >> 1;
+            idx[SPT] = tid < 2 * SMAX && sml < nsplit
+                           ? OFF_PART + ((kvh * SMAX + sml) * G + gg) * PART_STRIDE + HD + (tid & 1)
+                           : -1;
+            float v[SPT + 1];
+            ll_wait<SPT + 1>(cur, idx, v, ep, dead, p.err);
 #pragma unroll
-            for (int k = 0; k < SPT; k++) {
-                mrg_o[s0 + k][i] = v[3 * k];
-                if (i == 0) {
-                    mrg_ml[s0 + k] = make_float2(s0 + k < nsplit ? v[3 * k + 1] : -INFINITY, v[3 * k + 2]);
-                }
+            for (int k = 0; k < SPT; k++) mrg_o[s0 + k][i] = v[k];
+            if (tid < 2 * SMAX) {
+                if (tid & 1) mrg_ml[sml].y = v[SPT];
+                else mrg_ml[sml].x = sml < nsplit ? v[SPT] : -INFINITY;
             }
             lds_barrier();
             if (tid < HD) {
