@@ -77,6 +77,15 @@ int ar_ops_init(ar_hip_ctx* ctx);
 int ar_ctx_alloc(ar_hip_ctx* ctx, size_t bytes, void** out);
 int ar_ctx_free(ar_hip_ctx* ctx, void* p);
 
+// Uncached device memory for cross-block exchange words: its loads and stores go past the XCD
+// L2s to memory, which shortens a device-scope exchange round (measured on the persistent decode
+// step).  Such memory is never returned to the driver while the process runs (device allocations
+// made after uncached memory was freed have held wrong values on these parts): a block given back
+// with ar_uncached_put joins a per-device free list and is handed out again by a later
+// ar_uncached_get of at most its size.  The caller clears what it gets; `device` must be current.
+int ar_uncached_get(int device, size_t bytes, void** out);
+void ar_uncached_put(void* p);
+
 // Per-device caches of launch facts (CU count, resident-grid size, function attributes set):
 // indexed by the device of the stream a launch goes to.
 constexpr int kMaxDevices = 64;

@@ -139,7 +139,7 @@ struct ar_qwen3 {
     bool pk_ok = false;          // shape, dtypes and device qualify; buffers below allocated
     bool pk_on = true;           // ar_hip_qwen3_use_persistent
     void* pk_layers = nullptr;   // device table of the layers' weight pointers
-    uint64_t* pk_ll = nullptr;   // exchange words
+    uint64_t* pk_ll = nullptr;   // exchange words (uncached memory: ar_uncached_get)
     int* pk_err = nullptr;       // timeout / position flag of the last launches
 
     int timed = AR_KT_NONE;
@@ -169,9 +169,13 @@ void release(ar_qwen3* m) {
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
                     m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->smp_rng, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16,
-                    m->pf_flag, m->pk_layers, m->pk_ll, m->pk_err};
+                    m->pf_flag, m->pk_layers, m->pk_err};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
+    if (m->pk_ll) {  // (uncached: back to the process-wide free list once no launch uses it)
+        hipStreamSynchronize(m->ctx->stream);
+        ar_uncached_put(m->pk_ll);
+    }
     delete m;
 }
 
@@ -686,7 +690,9 @@ static int setup_persistent(ar_qwen3* m) {
     if (!m->pk_ll) {
         const size_t words =
             decode_persistent_ll_words(c.weight_dtype, c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size);
-        AR_TRY(alloc_zero(m, words * 8, (void**)&m->pk_ll));
+        // exchange words in uncached memory: C3 0.630 -> 0.606 ms per step against cached memory
+        AR_TRY(ar_uncached_get(m->ctx->device, words * 8, (void**)&m->pk_ll));
+        AR_HIP_TRY(hipMemsetAsync(m->pk_ll, 0, words * 8, m->ctx->stream));
         AR_TRY(alloc_zero(m, 64, (void**)&m->pk_err));
         AR_TRY(alloc_zero(m, eb * c.layer_count, &m->pk_layers));
     }

@@ -8,6 +8,8 @@
 #include <cstdio>
 #include <atomic>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "ar_hip_internal.h"
 
@@ -177,6 +179,45 @@ int ar_ctx_free(ar_hip_ctx* ctx, void* p) {
     AR_HIP_TRY(hipStreamSynchronize(ctx->stream));
     AR_HIP_TRY(hipFree(p));
     return AR_HIP_OK;
+}
+
+namespace {
+struct UncachedBlock {
+    int device;
+    size_t bytes;
+    void* p;
+    bool used;
+};
+std::mutex g_uncached_mu;
+std::vector<UncachedBlock> g_uncached;  // every uncached block of the process, never freed
+}  // namespace
+
+int ar_uncached_get(int device, size_t bytes, void** out) {
+    AR_CHECK_ARG(out && bytes > 0, "uncached allocation: bad arguments");
+    std::lock_guard<std::mutex> lk(g_uncached_mu);
+    UncachedBlock* best = nullptr;
+    for (auto& b : g_uncached)
+        if (!b.used && b.device == device && b.bytes >= bytes && (!best || b.bytes < best->bytes)) best = &b;
+    if (!best) {
+        void* p = nullptr;
+        hipError_t e = hipExtMallocWithFlags(&p, bytes, hipDeviceMallocUncached);
+        if (e != hipSuccess) {
+            ar_set_error("uncached allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+            return AR_HIP_ERR_HIP;
+        }
+        g_uncached.push_back({device, bytes, p, false});
+        best = &g_uncached.back();
+    }
+    best->used = true;
+    *out = best->p;
+    return AR_HIP_OK;
+}
+
+void ar_uncached_put(void* p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(g_uncached_mu);
+    for (auto& b : g_uncached)
+        if (b.p == p) b.used = false;
 }
 
 extern "C" int ar_hip_alloc(ar_hip_ctx* ctx, size_t bytes, void** device_ptr) {

@@ -373,3 +373,50 @@ def test_c3_persistent_per_head_norm_and_bias_match_multi_launch(ctx):
     ref.close()
     assert compare_tokens(fed_p[0], rf, rl, len(prompt)) == len(rf)
     assert rel_err(lg_p[0], rl) <= LOGIT_TOL_F32
+
+
+def test_persistent_models_side_by_side_and_after_release(ctx):
+    """Two C3-shape models with the persistent step alive at once, their steps interleaved (each has
+    its own exchange words and epoch base), then a third created after the first is released (it
+    reuses the released model's uncached exchange words, cleared): every model's tokens and logits
+    equal its own run as separate launches (tokens up to a near-tie, logits 1e-5)."""
+    cfg = dataclasses.replace(C.C3_0_6B, layer_count=2, vocab_size=4096, shared_weights=False, seq_len=64)
+    prompts = [synthetic.prompt_ids(12, cfg.vocab_size, seed=s) for s in (31, 32, 33)]
+    sds = [synthetic.state_dict(cfg, seed=s) for s in (31, 32, 33)]
+
+    def reference(sd, prompt):
+        with Qwen3(cfg, sd, ctx) as m:
+            m.model.use_persistent(False)
+            return gpu_generate(m, prompt, 8)
+
+    refs = [reference(sd, p) for sd, p in zip(sds, prompts)]
+
+    def check(i, fed, lg):
+        fed_m, lg_m = refs[i]
+        stop = compare_tokens(fed[0], fed_m[0], lg_m[0], len(prompts[i]))
+        assert stop == fed_m.shape[1], f"model {i}: near-tie at step {stop}"
+        assert rel_err(lg[0], lg_m[0]) <= 1e-5, (i, rel_err(lg[0], lg_m[0]))
+
+    m0, m1 = Qwen3(cfg, sds[0], ctx), Qwen3(cfg, sds[1], ctx)
+    try:
+        assert m0.model.persistent and m1.model.persistent
+        out = {0: ([], []), 1: ([], [])}
+        for i, m in ((0, m0), (1, m1)):
+            m.model.reset()
+            m.model.set_prompt(prompts[i])
+        for _ in range(len(prompts[0]) + 8):  # one step of each model in turn
+            for i, m in ((0, m0), (1, m1)):
+                t, lg = m.model.next(return_logits=True)
+                out[i][0].append(t)
+                out[i][1].append(lg)
+        for i in (0, 1):
+            check(i, np.stack(out[i][0], axis=1), np.stack(out[i][1], axis=1))
+    finally:
+        m0.close()
+    try:
+        with Qwen3(cfg, sds[2], ctx) as m2:
+            assert m2.model.persistent
+            check(2, *gpu_generate(m2, prompts[2], 8))
+        check(1, *gpu_generate(m1, prompts[1], 8))
+    finally:
+        m1.close()
