@@ -476,6 +476,76 @@ def llama2_section(args):
             "hbm_frac": round(per_tok * tok_s / 1e9 / HBM_PEAK_GBS, 4), "checkpoint_load_s": round(load_s, 2)}
 
 
+CPU_RUNS, CPU_WARMUP, CPU_TOKENS = 3, 5, 20  # Qwen3BenchmarkTest.java:54-60 (runs, warm-up, timed tokens)
+
+
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(cfg, prompt, seed, gpu_generated):
+    """The reference-semantics CPU oracle timed on this host the way Qwen3BenchmarkTest times the
+    reference (engine/ml/src/test/java/org/almostrealism/ml/qwen3/Qwen3BenchmarkTest.java:54-183):
+    per precision, the C3 prompt is taken in by the oracle's batched prompt pass (untimed), then
+    CPU_RUNS runs of CPU_WARMUP untimed and CPU_TOKENS timed greedy decode steps, each on
+    max(2, nproc / 2) threads (the reference's JNI pool, KernelPreferences.java:68-71) and on all
+    nproc threads.  FP64 is the reference's default precision (Hardware.java:684); FP32 is its
+    AR_HARDWARE_PRECISION=FP32 mode and the GPU's arithmetic.  The greedy tokens of both are compared
+    with the GPU's generated tokens over the positions both produced."""
+    import numpy as np
+
+    import oracle
+    from common_amd import synthetic
+    nproc = os.cpu_count() or 1
+    half = max(2, nproc // 2)
+    runs, parity = {}, {}
+    for precision in ("fp64", "fp32"):
+        t0 = time.perf_counter()
+        ref = oracle.OracleQwen3(cfg, synthetic.iter_state_dict(cfg, seed=seed), precision=precision)
+        oracle.set_threads(nproc)
+        nxt, _ = ref.prefill(prompt, want_logits=False)
+        setup_s = time.perf_counter() - t0
+        generated = []
+        for threads in (half, nproc):
+            used = oracle.set_threads(threads)
+            if threads == half:
+                half_used = used
+            per_run = []
+            for _ in range(CPU_RUNS):
+                for _ in range(CPU_WARMUP):
+                    generated.append(nxt)
+                    nxt, _ = ref.step(nxt, want_logits=False)
+                tc = time.perf_counter()
+                for _ in range(CPU_TOKENS):
+                    generated.append(nxt)
+                    nxt, _ = ref.step(nxt, want_logits=False)
+                per_run.append(CPU_TOKENS / (time.perf_counter() - tc))
+            runs[f"{precision}_{used}t"] = {"precision": precision, "threads": used,
+                                            "tok_s_runs": [round(v, 3) for v in per_run],
+                                            "tok_s_mean": round(float(np.mean(per_run)), 3)}
+            log(f"[bench] cpu oracle {precision} on {used} threads: {runs[f'{precision}_{used}t']['tok_s_mean']} "
+                f"tok/s (runs {runs[f'{precision}_{used}t']['tok_s_runs']})")
+        ref.close()
+        k = min(len(generated), len(gpu_generated))
+        eq = int(np.sum(np.asarray(generated[:k]) == np.asarray(gpu_generated[:k])))
+        parity[precision] = {"generated_tokens_compared": k, "equal": eq, "all_equal": bool(eq == k),
+                             "setup_s": round(setup_s, 1)}
+    primary = runs[f"fp64_{half_used}t"]
+    return {"value": primary["tok_s_mean"], "unit": "tok/s", "cores": primary["threads"], "kind": "port",
+            "precision": "fp64", "cpu_model": cpu_model_name(), "nproc": nproc, "runs": runs,
+            "sample": f"C3 decode: prompt of {len(prompt)} tokens through the oracle's batched prompt pass (untimed), "
+                      f"then per precision and thread count {CPU_RUNS} runs x ({CPU_WARMUP} warm-up + {CPU_TOKENS} "
+                      f"timed greedy tokens), positions {len(prompt)}..{len(prompt) + 2 * CPU_RUNS * (CPU_WARMUP + CPU_TOKENS) - 1}; "
+                      f"value = FP64 (reference default) on max(2, nproc/2) = {primary['threads']} threads"}, parity
+
+
 def step_bytes_batch(cfg, pos, batch, kv_bytes=4):
     """Bytes one batched decode step must move at position `pos`: weights once, KV per sequence."""
     kv = cfg.layer_count * 2 * cfg.kv_dim * kv_bytes * (pos + 1)
@@ -489,7 +559,7 @@ def main():
     ap.add_argument("--steps", type=int, default=251)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--probe-steps", type=int, default=16)
-    ap.add_argument("--cpu-steps", type=int, default=160, help="oracle steps timed for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=1, help="time the CPU oracle baseline (0: skip)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 prefill/decode section")
@@ -506,8 +576,6 @@ def main():
     ap.add_argument("--prefill-probe", choices=("c3", "c4"),
                     help="only run that workload's prompt through the batched prefill (a warm call and "
                          "PREFILL_PROBE_RUNS more, no decode step) for rocprofv3 counter passes, and exit")
-    ap.add_argument("--prefetch", type=int, default=0,
-                    help="blocks of the Infinity-Cache weight prefetch branch (0 disables)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the path has no "
@@ -553,7 +621,6 @@ def main():
     log(f"[bench] weights generated + uploaded in {time.time() - t0:.1f}s on {info}")
     am = model.model
     am.use_graph(not args.no_graph)
-    am.use_prefetch(args.prefetch)
     am.reset()
     am.set_prompt(prompt)
 
@@ -728,30 +795,12 @@ def main():
     am.set_temperature(0.0)
     model.close()
 
-    # ---- CPU baseline: the oracle (reference semantics, fp32) on this host -------------
+    # ---- CPU baseline: the oracle (reference semantics) on this host, FP64 and FP32 ----------
     cpu = None
     parity = None
     if args.cpu_steps > 0:
-        import oracle
-        nproc = os.cpu_count() or 1
-        threads = oracle.set_threads(max(2, nproc // 2))
-        ref = oracle.OracleQwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed), precision="fp32")
-        n = min(args.cpu_steps, n_prompt + args.warmup + args.steps)
-        gpu_fed = np.concatenate([fed_prompt[0], warm[0], toks[0]])
-        tc = time.perf_counter()
-        fed, _ = ref.generate(prompt[:min(n, n_prompt)], max(0, n - n_prompt), want_logits=False)
-        cpu_s = time.perf_counter() - tc
-        ref.close()
-        steps_done = n
-        cpu = {"value": round(steps_done / cpu_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"first {steps_done} steps of the workload (prompt tokens 0..{min(n, n_prompt) - 1} fed one "
-                         f"per step as the reference does, then {max(0, n - n_prompt)} greedy tokens), oracle fp32, "
-                         f"{threads} OpenMP threads of {nproc} ({platform.processor() or platform.machine()})"}
-        if n > n_prompt:
-            match = int(np.sum(fed[:n] == gpu_fed[:n]))
-            parity = {"steps_compared": n, "tokens_equal": match, "all_equal": bool(match == n)}
-        log(f"[bench] cpu oracle: {cpu['value']} tok/s over {steps_done} steps ({cpu_s:.1f}s), parity {parity}")
-
+        gpu_generated = np.concatenate([warm[0], toks[0]]).tolist()
+        cpu, parity = cpu_baseline(cfg, prompt, args.seed, gpu_generated)
     out = {
         "metric": "decode tok/s (Qwen3-0.6B shape, b=1)",
         "value": round(tok_s, 2),
@@ -768,7 +817,7 @@ def main():
         "config": {"workload": "C3: Qwen3-0.6B shape fp32 (d1024, 28L, 16Q/8KV, hd128, F3072, V151936), "
                                "batch 1, prompt 128, greedy decode",
                    "decode_positions": f"{pos0}..{pos0 + args.steps - 1}", "graph": not args.no_graph,
-                   "prefetch_blocks": args.prefetch, "persistent_kernel": persistent},
+                   "persistent_kernel": persistent},
         "hbm": {"algorithmic_bytes_per_token": round(mean_bytes), "achieved_GBs": round(e2e_gbs, 1),
                 "frac_of_peak": round(e2e_gbs / HBM_PEAK_GBS, 4)},
         "sampled_c3": sampled,

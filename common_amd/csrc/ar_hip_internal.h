@@ -18,6 +18,8 @@
 // Every C-ABI entry point returns an AR_HIP_* code; the message for the calling thread
 // is kept here and returned by ar_hip_last_error().
 void ar_set_error(const char* fmt, ...);
+// A notice on stderr when AR_HIP_LOG is set (no error state).
+void ar_log(const char* fmt, ...);
 void ar_clear_error();
 
 #define AR_CHECK_ARG(cond, ...)                  \
@@ -391,6 +393,7 @@ struct DecodePersistentLaunch {
     int* state = nullptr;
     uint64_t* ll = nullptr;
     int* err = nullptr;        // 1: a cross-block wait timed out; 2: position outside the cache
+    unsigned wait_limit = 0;   // polls before a cross-block wait is abandoned (0: the kernel's default)
     float eps = 1e-6f;
     int per_head_norm = 0;
     // after the last layer: final RMSNorm, logits (stored when logits is non-null) and greedy keys
@@ -428,8 +431,6 @@ int launch_rope(float* x, int heads, int hd, int pos, double theta, int rows, in
 int launch_index_of_max(const float* x, int rows, int n, int* out, hipStream_t stream);
 int launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream);
 int launch_fill_i32(int* dst, int value, size_t n, hipStream_t stream);
-// Reads [p, p+bytes) (16-byte aligned) with `blocks` x 256 threads so it lands in the Infinity Cache.
-int launch_prefetch(const void* p, size_t bytes, unsigned* sink, int blocks, hipStream_t stream);
 
 // Token sampling (sample.hip): AR_SAMPLE_TOKEN = AutoregressiveModel.sampleToken(logits, V,
 // temperature, top_p, random), AR_SAMPLE_MODEL = the sample function of AutoregressiveModel.of.

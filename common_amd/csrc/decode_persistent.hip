@@ -36,7 +36,7 @@ constexpr int kPB = 256;           // blocks: one per CU
 constexpr int kPT = 512;           // threads per block
 constexpr int kPW = kPT / 64;      // wavefronts per block
 constexpr int kRowsPerSplit = 32;  // cache rows per split before another split is opened
-constexpr unsigned kSpinLimit = 1u << 18;  // polls before a wait is abandoned (~0.3 s)
+constexpr unsigned kSpinLimit = 1u << 18;  // default polls before a wait is abandoned (~0.3 s)
 constexpr int kPadLds = 64 * 1024;         // dynamic LDS that keeps a second block off each CU
 constexpr int kMaxLayers = 64;             // layer table held in LDS
 constexpr unsigned kGateUpDelay = 250;     // wall-clock ticks (10 ns): see the O stage
@@ -65,6 +65,7 @@ struct PParams {
     int* state;        // [0] position, [3] epoch base (advanced by L at the end of every launch)
     uint64_t* ll;      // exchange words, two parities
     int* err;          // set to 1 when a wait timed out
+    unsigned spin_limit;  // polls before a wait is abandoned
     float eps;
     int per_head;      // QK-norm: one RMS per head (else over the whole q / k vector)
     // after the last layer: final RMSNorm, logits and greedy-token keys
@@ -164,7 +165,7 @@ __device__ inline float ll_val(uint64_t w) { return __uint_as_float((unsigned)w)
 // Waits for N words at base[idx[j]] to carry epoch ep (or the block to be marked dead).
 template <int N>
 __device__ inline void ll_wait(const uint64_t* base, const int (&idx)[N], float (&out)[N], unsigned ep,
-                               int* dead, int* err) {
+                               int* dead, int* err, unsigned limit) {
     uint64_t w[N];
 #pragma unroll
     for (int j = 0; j < N; j++) w[j] = idx[j] >= 0 ? ll_get(base + idx[j]) : ((uint64_t)ep << 32);
@@ -174,7 +175,7 @@ __device__ inline void ll_wait(const uint64_t* base, const int (&idx)[N], float 
 #pragma unroll
         for (int j = 0; j < N; j++) ok &= ll_ok(w[j], ep);
         if (ok || dead_get(dead)) break;
-        if (++spins > kSpinLimit) {
+        if (++spins > limit) {
             dead_set(dead);
             __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 int idx[NX];
 #pragma unroll
                 for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XA + tid + j * kPT : -1;
-                ll_wait<NX>(prev, idx, xv, base + (unsigned)l, dead, p.err);
+                ll_wait<NX>(prev, idx, xv, base + (unsigned)l, dead, p.err, p.spin_limit);
             }
             float ss = 0.f;
 #pragma unroll
@@ -432,7 +433,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 idx[0] = OFF_SS + (tid - T_S);
             }
             float qv[2];
-            ll_wait<2>(cur, idx, qv, ep, dead, p.err);  // (words not waited for read as 0)
+            ll_wait<2>(cur, idx, qv, ep, dead, p.err, p.spin_limit);  // (words not waited for read as 0)
             if (p.per_head) {
                 if (tid >= T_S && tid - T_S < (G + 1) * RPH) ss_s[tid - T_S] = qv[0];
             } else {
@@ -652,7 +653,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                            ? OFF_PART + ((kvh * SMAX + sml) * G + gg) * PART_STRIDE + HD + (tid & 1)
                            : -1;
             float v[SPT + 1];
-            ll_wait<SPT + 1>(cur, idx, v, ep, dead, p.err);
+            ll_wait<SPT + 1>(cur, idx, v, ep, dead, p.err, p.spin_limit);
 #pragma unroll
             for (int k = 0; k < SPT; k++) mrg_o[s0 + k][i] = v[k];
             if (tid < 2 * SMAX) {
@@ -692,7 +693,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 #pragma unroll
             for (int j = 0; j < NA; j++) idx[j] = OFF_A + tid + j * kPT;
             float av[NA];
-            ll_wait<NA>(cur, idx, av, ep, dead, p.err);
+            ll_wait<NA>(cur, idx, av, ep, dead, p.err, p.spin_limit);
 #pragma unroll
             for (int j = 0; j < NA; j++) xin[tid + j * kPT] = av[j];
             lds_barrier();
@@ -724,7 +725,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 #pragma unroll
             for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XM + tid + j * kPT : -1;
             float xv[NX];
-            ll_wait<NX>(cur, idx, xv, ep, dead, p.err);
+            ll_wait<NX>(cur, idx, xv, ep, dead, p.err, p.spin_limit);
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < NX; j++) {
@@ -767,7 +768,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 #pragma unroll
             for (int j = 0; j < NH; j++) idx[j] = tid + j * kPT < F ? OFF_H + tid + j * kPT : -1;
             float hv[NH];
-            ll_wait<NH>(cur, idx, hv, ep, dead, p.err);
+            ll_wait<NH>(cur, idx, hv, ep, dead, p.err, p.spin_limit);
 #pragma unroll
             for (int j = 0; j < NH; j++)
                 if (tid + j * kPT < F) xin[tid + j * kPT] = hv[j];
@@ -820,7 +821,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 #pragma unroll
         for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XA + tid + j * kPT : -1;
         float xv[NX];
-        ll_wait<NX>(p.ll + (size_t)((p.L - 1) & 1) * PAR_WORDS, idx, xv, base + (unsigned)p.L, dead, p.err);
+        ll_wait<NX>(p.ll + (size_t)((p.L - 1) & 1) * PAR_WORDS, idx, xv, base + (unsigned)p.L, dead, p.err, p.spin_limit);
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < NX; j++) {
@@ -886,6 +887,7 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     p.L = a.layer_count;
     p.x = a.x; p.kcache = a.kcache; p.vcache = a.vcache; p.S = a.max_seq; p.rope_tab = a.rope_tab;
     p.state = a.state; p.ll = a.ll; p.err = a.err; p.eps = a.eps; p.per_head = a.per_head_norm;
+    p.spin_limit = a.wait_limit ? a.wait_limit : kSpinLimit;
     p.final_norm = a.final_norm; p.lm_head = a.lm_head; p.vocab = a.vocab; p.logits = a.logits; p.keys = a.keys;
     auto kern = decode_persistent_kernel<TW, DIM, F, H, KV, HD, SMAX>;  // (its LDS attribute is set by fits_t)
     // A plain launch (a cooperative one measured ~20 us longer per step): every block must be resident

@@ -150,28 +150,6 @@ __global__ void fill_i32_kernel(int* dst, int value, size_t n) {
         dst[i] = value;
 }
 
-// Streams [p, p + n16*16) through the memory hierarchy so a later kernel finds it in the
-// Infinity Cache.  The loaded words are folded into an XOR that is stored only when it equals a
-// value no weight tensor produces in practice, which keeps the loads from being removed.
-__global__ __launch_bounds__(256) void prefetch_kernel(const uint4* __restrict__ p, size_t n16, unsigned sentinel,
-                                                       unsigned* sink) {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    unsigned acc = 0;
-    for (; i + 7 * stride < n16; i += 8 * stride) {
-        uint4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = p[i + u * stride];
-#pragma unroll
-        for (int u = 0; u < 8; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-    }
-    for (; i < n16; i += stride) {
-        const uint4 v = p[i];
-        acc ^= v.x ^ v.y ^ v.z ^ v.w;
-    }
-    if (acc == sentinel) sink[0] = acc;
-}
-
 int grid_for(size_t n, int threads, int cap = 4096) {
     size_t g = (n + threads - 1) / threads;
     if (g < 1) g = 1;
@@ -223,15 +201,6 @@ int launch_index_of_max(const float* x, int rows, int n, int* out, hipStream_t s
 int launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream) {
     if (!n) return AR_HIP_OK;
     hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, src, dst, n);
-    AR_LAUNCH_CHECK();
-    return AR_HIP_OK;
-}
-
-int launch_prefetch(const void* p, size_t bytes, unsigned* sink, int blocks, hipStream_t stream) {
-    AR_CHECK_ARG(p && sink && (reinterpret_cast<uintptr_t>(p) & 15) == 0, "prefetch: bad arguments");
-    if (bytes < 16) return AR_HIP_OK;
-    hipLaunchKernelGGL(prefetch_kernel, dim3(blocks), dim3(256), 0, stream, (const uint4*)p, bytes / 16,
-                       0x9E3779B9u, sink);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -100,16 +100,8 @@ struct ar_qwen3 {
 
     bool use_graph = true;
     hipGraphExec_t graph[2] = {nullptr, nullptr};  // [store logits]
-
-    // Infinity-Cache prefetch branch: a second stream streams layer l+1's weights while layer l
-    // computes (forked from the compute stream by an event at the start of each layer, joined at
-    // the end of the step).  0 blocks disables it.
-    int prefetch_blocks = 0;
-    hipStream_t pstream = nullptr;
-    std::vector<hipEvent_t> fork_ev;   // one per layer + 1
-    hipEvent_t join_ev = nullptr;
-    unsigned* sink = nullptr;
-    std::vector<std::pair<size_t, size_t>> layer_bytes;  // [offset, end) of each layer in the arena
+    // set by the kernel-loop probe, which overwrites the step state: steps are refused until reset()
+    bool needs_reset = false;
 
     // prefill buffers, sized for pf_rows = batch x prompt rows on first use
     size_t pf_rows = 0;
@@ -140,7 +132,12 @@ struct ar_qwen3 {
     bool pk_on = true;           // ar_hip_qwen3_use_persistent
     void* pk_layers = nullptr;   // device table of the layers' weight pointers
     uint64_t* pk_ll = nullptr;   // exchange words (uncached memory: ar_uncached_get)
+    size_t pk_ll_words = 0;
     int* pk_err = nullptr;       // timeout / position flag of the last launches
+    unsigned pk_wait_limit = 0;  // polls per cross-block wait before it is abandoned (0: kernel default)
+    bool pk_suspended = false;   // steps being recomputed as separate launches after a timed-out step
+    int pk_recomputed = 0;       // steps recomputed so (ar_hip_qwen3_persistent_recomputed)
+    unsigned long long* smp_rng_saved = nullptr;  // [B] generator states before the last persistent call
 
     int timed = AR_KT_NONE;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
@@ -163,11 +160,9 @@ void release(ar_qwen3* m) {
         hipEventDestroy(e.first);
         hipEventDestroy(e.second);
     }
-    for (auto& e : m->fork_ev) hipEventDestroy(e);
-    if (m->join_ev) hipEventDestroy(m->join_ev);
-    if (m->pstream) hipStreamDestroy(m->pstream);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->smp_rng, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging, m->sink,
+                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->smp_rng,
+                    m->smp_rng_saved, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16,
                     m->pf_flag, m->pk_layers, m->pk_err};
     for (void* b : bufs)
@@ -305,9 +300,9 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
 }
 
 // The persistent kernel runs the layers and the logits of the step unless it is switched off, a kernel
-// class of the multi-launch step is being timed, or the prefetch branch (multi-launch only) is on.
+// class of the multi-launch step is being timed, or a timed-out step is being recomputed.
 bool persistent_active(const ar_qwen3* m) {
-    return m->pk_ok && m->pk_on && m->prefetch_blocks == 0 && (m->timed == AR_KT_NONE || m->timed == AR_KT_LAYERS);
+    return m->pk_ok && m->pk_on && !m->pk_suspended && (m->timed == AR_KT_NONE || m->timed == AR_KT_LAYERS);
 }
 
 int enqueue_step(ar_qwen3* m, bool store_logits) {
@@ -354,7 +349,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         d.hidden_dim = c.hidden_dim;
         d.heads = c.head_count; d.kv_heads = c.kv_head_count; d.head_dim = c.head_size; d.x = m->x;
         d.kcache = (float*)m->kcache; d.vcache = (float*)m->vcache; d.max_seq = m->S; d.rope_tab = m->rope_tab;
-        d.state = m->state; d.ll = m->pk_ll; d.err = m->pk_err; d.eps = (float)c.epsilon;
+        d.state = m->state; d.ll = m->pk_ll; d.err = m->pk_err; d.wait_limit = m->pk_wait_limit;
+        d.eps = (float)c.epsilon;
         d.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
         const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
         d.final_norm = m->final_norm; d.lm_head = m->lm_head; d.vocab = c.vocab_size;
@@ -372,27 +368,14 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         if (sampling) AR_TRY(enqueue_sample(m));
         return AR_HIP_OK;
     }
-    const bool pf = m->prefetch_blocks > 0;
-    auto prefetch_layer = [&](int l, int ev) -> int {
-        AR_HIP_TRY(hipEventRecord(m->fork_ev[ev], st));
-        AR_HIP_TRY(hipStreamWaitEvent(m->pstream, m->fork_ev[ev], 0));
-        const auto& r = m->layer_bytes[l];
-        return launch_prefetch(m->arena + r.first, r.second - r.first, m->sink, m->prefetch_blocks, m->pstream);
-    };
-    if (pf) AR_TRY(prefetch_layer(0, 0));
     const StepPlanes pl = step_planes(m);
     AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys, m->state,
                              B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, st));
     for (int l = 0; l < c.layer_count; l++) {
-        if (pf && l + 1 < c.layer_count) AR_TRY(prefetch_layer(l + 1, l + 1));
         for (int which : {AR_KT_QKV, AR_KT_ATTENTION, AR_KT_O, AR_KT_GATE_UP, AR_KT_DOWN}) AR_TRY(timed_class(which, l));
     }
     AR_TRY(timed_class(AR_KT_LOGITS, 0));
     if (!sample_is_greedy(m->smp_mode, m->smp_temperature)) AR_TRY(enqueue_sample(m));
-    if (pf) {  // join the prefetch branch back into the compute stream
-        AR_HIP_TRY(hipEventRecord(m->join_ev, m->pstream));
-        AR_HIP_TRY(hipStreamWaitEvent(st, m->join_ev, 0));
-    }
     return AR_HIP_OK;
 }
 
@@ -511,7 +494,6 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
         o[7] = place(p + "self_attn.q_norm.weight", m->q_dim, false, false);
         o[8] = place(p + "self_attn.k_norm.weight", m->kv_dim, false, false);
         o[9] = c.qkv_bias ? place(p + "self_attn.qkv_bias", m->qkv_dim, false) : (size_t)-1;
-        m->layer_bytes.push_back({o[0], off});
     }
     m->arena_bytes = off;
     int rc = ar_ctx_alloc(ctx, m->arena_bytes, (void**)&m->arena);
@@ -582,6 +564,7 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     }
     ALLOC(am_keys, B * kArgmaxSlots * 8);
     ALLOC(smp_rng, B * 8);
+    ALLOC(smp_rng_saved, B * 8);
     {
         // every sequence starts with new Random(0)
         std::vector<unsigned long long> st0(B, 0x5DEECE66DULL & ((1ULL << 48) - 1));
@@ -597,22 +580,7 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
     ALLOC(tokens, B * (m->S + 1) * 4);
     ALLOC(state, 64);
     ALLOC(staging, m->staging_floats * 4);
-    ALLOC(sink, 64);
 #undef ALLOC
-    {
-        hipError_t e = hipStreamCreateWithFlags(&m->pstream, hipStreamNonBlocking);
-        for (int i = 0; e == hipSuccess && i <= c.layer_count; i++) {
-            hipEvent_t ev;
-            e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
-            if (e == hipSuccess) m->fork_ev.push_back(ev);
-        }
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&m->join_ev, hipEventDisableTiming);
-        if (e != hipSuccess) {
-            release(m);
-            ar_set_error("prefetch stream/event creation failed: %s", hipGetErrorString(e));
-            return AR_HIP_ERR_HIP;
-        }
-    }
     {
         // RoPE (cos, sin) for every cache position, in double as computeRopeFreqs defines them
         // (engine/ml/.../RotationFeatures.java:189-208): invf[f] = exp(f * -2 ln(theta) / hd).
@@ -692,6 +660,7 @@ static int setup_persistent(ar_qwen3* m) {
             decode_persistent_ll_words(c.weight_dtype, c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size);
         // exchange words in uncached memory: C3 0.630 -> 0.606 ms per step against cached memory
         AR_TRY(ar_uncached_get(m->ctx->device, words * 8, (void**)&m->pk_ll));
+        m->pk_ll_words = words;
         AR_HIP_TRY(hipMemsetAsync(m->pk_ll, 0, words * 8, m->ctx->stream));
         AR_TRY(alloc_zero(m, 64, (void**)&m->pk_err));
         AR_TRY(alloc_zero(m, eb * c.layer_count, &m->pk_layers));
@@ -708,16 +677,75 @@ static int setup_persistent(ar_qwen3* m) {
     return AR_HIP_OK;
 }
 
-// After a synchronisation: reports (and clears) the persistent kernel's error flag.
-static int check_persistent(ar_qwen3* m) {
+// After a synchronisation: the persistent kernel's error flag of the launches since the last check
+// (0 none, 1 a cross-block wait timed out, 2 position outside the cache), cleared.
+static int persistent_status(ar_qwen3* m, int* status) {
+    *status = 0;
     if (!m->pk_err) return AR_HIP_OK;
-    int e = 0;
-    AR_HIP_TRY(hipMemcpy(&e, m->pk_err, sizeof(int), hipMemcpyDeviceToHost));
-    if (!e) return AR_HIP_OK;
-    AR_HIP_TRY(hipMemset(m->pk_err, 0, sizeof(int)));
-    ar_set_error(e == 1 ? "persistent decode step: a cross-block wait timed out (the step's results are invalid)"
-                        : "persistent decode step: position outside the KV cache");
-    return AR_HIP_ERR_HIP;
+    AR_HIP_TRY(hipMemcpy(status, m->pk_err, sizeof(int), hipMemcpyDeviceToHost));
+    if (*status) AR_HIP_TRY(hipMemset(m->pk_err, 0, sizeof(int)));
+    return AR_HIP_OK;
+}
+
+// A persistent launch needs every block resident at once; when another kernel or process holds CUs,
+// the blocks that did run abandon their waits after the wait limit and the launch drains with invalid
+// results.  The steps [start, start + n) of the call are then recomputed as separate launches before
+// the call returns, and the model stays on separate launches until use_persistent(1):
+//  * the exchange words are cleared: a block that started after block 0 had published the next
+//    launch's epoch base wrote words tagged with that launch's epochs;
+//  * the generators of a sampling model are restored to their state before the call (the sampler ran
+//    on the invalid logits);
+//  * the loop state returns to position start.  The token fed at start was stored by the call's first
+//    step-begin, from the keys of the last valid step, so the recompute reads it as a prompt token (the
+//    prompt length seen by the step-begin is max(prompt_len, start + 1) during the recompute; every
+//    later step decides prompt / generated exactly as before), and the prompt length is restored after.
+static int recompute_timed_out(ar_qwen3* m, int start, int n, bool store_logits) {
+    hipStream_t st = m->ctx->stream;
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    AR_HIP_TRY(hipMemsetAsync(m->pk_ll, 0, m->pk_ll_words * 8, st));
+    if (!sample_is_greedy(m->smp_mode, m->smp_temperature))
+        AR_HIP_TRY(hipMemcpyAsync(m->smp_rng, m->smp_rng_saved, (size_t)m->B * 8, hipMemcpyDeviceToDevice, st));
+    const int loop[3] = {start, std::max(m->prompt_len, start + 1), start};
+    AR_HIP_TRY(hipMemcpyAsync(m->state, loop, sizeof(loop), hipMemcpyHostToDevice, st));
+    m->pk_suspended = true;
+    int rc = AR_HIP_OK;
+    for (int i = 0; i < n && rc == AR_HIP_OK; i++) rc = run_step(m, store_logits);
+    m->pk_suspended = false;
+    AR_TRY(rc);
+    AR_HIP_TRY(hipMemcpyAsync(m->state + 1, &m->prompt_len, sizeof(int), hipMemcpyHostToDevice, st));
+    AR_HIP_TRY(hipStreamSynchronize(st));
+    m->pk_on = false;
+    m->pk_recomputed += n;
+    ar_log("persistent decode step timed out (blocks not resident together); %d step(s) from position %d "
+           "recomputed as separate launches, the model now runs separate launches", n, start);
+    return AR_HIP_OK;
+}
+
+// Before a call that enqueues persistent steps of a sampling model: the generators' state, so a
+// recompute draws what the steps would have drawn.
+static int save_generators(ar_qwen3* m) {
+    if (persistent_active(m) && !sample_is_greedy(m->smp_mode, m->smp_temperature))
+        AR_HIP_TRY(hipMemcpyAsync(m->smp_rng_saved, m->smp_rng, (size_t)m->B * 8, hipMemcpyDeviceToDevice,
+                                  m->ctx->stream));
+    return AR_HIP_OK;
+}
+
+// After the synchronisation that ends a call of n steps from position start: a timed-out persistent
+// step is recomputed (returns 1 in *redone, the outputs must be copied again), a position outside the
+// cache (the host never steps there) is an error.
+static int finish_persistent(ar_qwen3* m, int start, int n, bool store_logits, int* redone) {
+    *redone = 0;
+    int status = 0;
+    AR_TRY(persistent_status(m, &status));
+    if (status == 2) {
+        ar_set_error("persistent decode step: position outside the KV cache");
+        return AR_HIP_ERR_HIP;
+    }
+    if (status == 1) {
+        AR_TRY(recompute_timed_out(m, start, n, store_logits));
+        *redone = 1;
+    }
+    return AR_HIP_OK;
 }
 
 extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
@@ -747,6 +775,7 @@ extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
 extern "C" int ar_hip_qwen3_reset(ar_qwen3* m) {
     AR_CHECK_ARG(m, "null model");
     m->host_pos = 0;
+    m->needs_reset = false;
     int st[3] = {0, m->prompt_len, 0};
     AR_HIP_TRY(hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, m->ctx->stream));
     AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
@@ -782,6 +811,10 @@ static int check_ready(ar_qwen3* m, int steps) {
         ar_set_error("model not finalized (call ar_hip_qwen3_finalize after setting weights)");
         return AR_HIP_ERR_STATE;
     }
+    if (m->needs_reset) {
+        ar_set_error("the kernel-loop probe overwrote the step state: reset() before the next step");
+        return AR_HIP_ERR_STATE;
+    }
     if (m->prompt_len < 1) {
         ar_set_error("no prompt: set at least one prompt token before stepping");
         return AR_HIP_ERR_STATE;
@@ -801,16 +834,21 @@ static int check_ready(ar_qwen3* m, int steps) {
 extern "C" int ar_hip_qwen3_next(ar_qwen3* m, int32_t* tokens_out, float* logits_out) {
     AR_TRY(check_ready(m, 1));
     hipStream_t st = m->ctx->stream;
+    AR_TRY(save_generators(m));
     AR_TRY(run_step(m, logits_out != nullptr));
-    if (tokens_out)
-        for (int b = 0; b < m->B; b++)
-            AR_HIP_TRY(hipMemcpyAsync(tokens_out + b, m->tokens + (size_t)b * (m->S + 1) + m->host_pos, 4,
+    for (int pass = 0; pass < 2; pass++) {
+        if (tokens_out)
+            for (int b = 0; b < m->B; b++)
+                AR_HIP_TRY(hipMemcpyAsync(tokens_out + b, m->tokens + (size_t)b * (m->S + 1) + m->host_pos, 4,
+                                          hipMemcpyDeviceToHost, st));
+        if (logits_out)
+            AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)m->B * m->cfg.vocab_size * 4,
                                       hipMemcpyDeviceToHost, st));
-    if (logits_out)
-        AR_HIP_TRY(hipMemcpyAsync(logits_out, m->logits, (size_t)m->B * m->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
-                                  st));
-    AR_HIP_TRY(hipStreamSynchronize(st));
-    AR_TRY(check_persistent(m));
+        AR_HIP_TRY(hipStreamSynchronize(st));
+        int redone = 0;
+        if (pass == 0) AR_TRY(finish_persistent(m, m->host_pos, 1, logits_out != nullptr, &redone));
+        if (!redone) break;
+    }
     m->host_pos++;
     return AR_HIP_OK;
 }
@@ -820,13 +858,18 @@ extern "C" int ar_hip_qwen3_run(ar_qwen3* m, int steps, int32_t* tokens_out) {
     AR_TRY(check_ready(m, steps));
     hipStream_t st = m->ctx->stream;
     const int start = m->host_pos;
+    AR_TRY(save_generators(m));
     for (int i = 0; i < steps; i++) AR_TRY(run_step(m, false));
-    if (tokens_out && steps > 0)
-        for (int b = 0; b < m->B; b++)
-            AR_HIP_TRY(hipMemcpyAsync(tokens_out + (size_t)b * steps, m->tokens + (size_t)b * (m->S + 1) + start,
-                                      (size_t)steps * 4, hipMemcpyDeviceToHost, st));
-    AR_HIP_TRY(hipStreamSynchronize(st));
-    AR_TRY(check_persistent(m));
+    for (int pass = 0; pass < 2; pass++) {
+        if (tokens_out && steps > 0)
+            for (int b = 0; b < m->B; b++)
+                AR_HIP_TRY(hipMemcpyAsync(tokens_out + (size_t)b * steps, m->tokens + (size_t)b * (m->S + 1) + start,
+                                          (size_t)steps * 4, hipMemcpyDeviceToHost, st));
+        AR_HIP_TRY(hipStreamSynchronize(st));
+        int redone = 0;
+        if (pass == 0) AR_TRY(finish_persistent(m, start, steps, false, &redone));
+        if (!redone) break;
+    }
     m->host_pos += steps;
     return AR_HIP_OK;
 }
@@ -885,6 +928,7 @@ extern "C" int ar_hip_qwen3_kernel_loop(ar_qwen3* m, int which, int reps, double
     AR_CHECK_ARG(reps >= 1 && reps <= 4096, "reps %d outside 1..4096", reps);
     hipStream_t st = m->ctx->stream;
     AR_HIP_TRY(hipStreamSynchronize(st));
+    m->needs_reset = true;  // the launches overwrite the residual stream and the greedy keys
     const StepPlanes pl = step_planes(m);
     if (!m->use_graph) {  // plain launches, back to back between the two events
         hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -995,12 +1039,16 @@ extern "C" int ar_hip_qwen3_persistent(ar_qwen3* m, int* active) {
     return AR_HIP_OK;
 }
 
-extern "C" int ar_hip_qwen3_use_prefetch(ar_qwen3* m, int blocks) {
+extern "C" int ar_hip_qwen3_persistent_wait_limit(ar_qwen3* m, unsigned polls) {
     AR_CHECK_ARG(m, "null model");
-    AR_CHECK_ARG(blocks >= 0 && blocks <= 4096, "prefetch blocks %d outside 0..4096", blocks);
     AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-    AR_TRY(invalidate_graphs(m));
-    m->prefetch_blocks = blocks;
+    m->pk_wait_limit = polls;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_persistent_recomputed(ar_qwen3* m, int* steps) {
+    AR_CHECK_ARG(m && steps, "null argument");
+    *steps = m->pk_recomputed;
     return AR_HIP_OK;
 }
 

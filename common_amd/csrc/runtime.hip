@@ -38,6 +38,16 @@ void ar_set_error(const char* fmt, ...) {
     if (log_errors()) fprintf(stderr, "[ar_hip] %s\n", g_last_error);
 }
 
+void ar_log(const char* fmt, ...) {
+    if (!log_errors()) return;
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "[ar_hip] %s\n", buf);
+}
+
 void ar_clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char* ar_hip_last_error(void) { return g_last_error; }

@@ -89,9 +89,10 @@ _SIGS = {
     "ar_hip_qwen3_kernel_time": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), _c_int_p]),
     "ar_hip_qwen3_kernel_loop": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "ar_hip_qwen3_use_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
-    "ar_hip_qwen3_use_prefetch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_use_persistent": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_persistent": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
+    "ar_hip_qwen3_persistent_recomputed": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
+    "ar_hip_qwen3_persistent_wait_limit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint]),
     "ar_hip_qwen3_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_qwen3_prefill_by_steps": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
     "ar_hip_gemm_bf16": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4),

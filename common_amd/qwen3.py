@@ -107,14 +107,27 @@ class AutoregressiveModel:
     def use_graph(self, enable: bool):
         hw.check(hw.lib().ar_hip_qwen3_use_graph(self.handle, int(enable)))
 
-    def use_prefetch(self, blocks: int):
-        """Infinity-Cache prefetch of the next layer's weights on a second stream (0 disables)."""
-        hw.check(hw.lib().ar_hip_qwen3_use_prefetch(self.handle, int(blocks)))
-
     def use_persistent(self, enable: bool):
         """Run the layers of each decode step as one persistent launch when the model qualifies
-        (batch 1, fp32 weights and cache; default on) or as separate launches."""
+        (default on) or as separate launches.  It qualifies at batch 1 with an fp32 KV cache on the
+        two instantiated shapes: d1024/F3072, 16/8 heads of 128, fp32 weights (Qwen3-0.6B) and
+        d2048/F6144, 16/8 heads of 128, bf16 weights (Qwen3-1.7B).  A call whose persistent launch
+        timed out (blocks not resident together) is recomputed as separate launches and switches
+        the model to them until this is called with True again."""
         hw.check(hw.lib().ar_hip_qwen3_use_persistent(self.handle, int(enable)))
+
+    @property
+    def persistent_recomputed(self) -> int:
+        """Steps recomputed as separate launches after a timed-out persistent launch."""
+        n = ctypes.c_int()
+        hw.check(hw.lib().ar_hip_qwen3_persistent_recomputed(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def persistent_wait_limit(self, polls: int):
+        """Polls of one cross-block wait of the persistent kernel before it is abandoned (0: the
+        default).  A test knob: a tiny limit makes the waits time out while every block still runs
+        to its end."""
+        hw.check(hw.lib().ar_hip_qwen3_persistent_wait_limit(self.handle, int(polls)))
 
     @property
     def persistent(self) -> bool:

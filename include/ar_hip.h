@@ -278,23 +278,31 @@ int ar_hip_qwen3_kernel_time(ar_qwen3 *m, double *ms, int *launches);
 int ar_hip_qwen3_kernel_loop(ar_qwen3 *m, int which, int reps, double *us_per_launch);
 /* Use a captured HIP graph per decode step (1, default) or plain launches (0). */
 int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
-/* Persistent decode step.  For batch 1 with fp32 weights and an fp32 KV cache (on a device that can
- * hold one 512-thread block per CU on 256 CUs at once), the layers and the logits of each decode step
- * run as one launch whose stages exchange data through device-scope words tagged with an epoch,
- * instead of five launches per layer and one for the logits; the step-begin kernel stays separate,
- * and the two launches are enqueued directly (a graph replay of them measured slower).  No counterpart in the reference
- * (its backend runs the compiled operation list); a throughput option only: results match the
- * multi-launch step within float rounding.  enable 1 (default) or 0; ar_hip_qwen3_persistent reports
- * whether the next steps use it.  A cross-block wait that times out (possible only if another
- * kernel occupied CUs during the step) makes the next ar_hip_qwen3_next / run fail with
- * AR_HIP_ERR_HIP. */
+/* Persistent decode step.  For batch 1 with an fp32 KV cache, on the instantiated shapes
+ *   dim 1024 / FFN 3072 / 16 Q, 8 KV heads / head size 128 with fp32 weights (Qwen3-0.6B), and
+ *   dim 2048 / FFN 6144 / 16 Q, 8 KV heads / head size 128 with bf16 weights (Qwen3-1.7B),
+ * on a device that holds one 512-thread block per CU on 256 CUs at once, the layers and the logits of
+ * each decode step run as one launch whose stages exchange data through device-scope words tagged
+ * with an epoch, instead of five launches per layer and one for the logits; the step-begin kernel
+ * stays separate, and the two launches are enqueued directly (a graph replay of them measured
+ * slower).  No counterpart in the reference (its backend runs the compiled operation list); a
+ * throughput option only: results match the multi-launch step within float rounding.  enable 1
+ * (default) or 0; ar_hip_qwen3_persistent reports whether the next steps use it.
+ * The launch needs every block resident at once.  If another kernel or process holds CUs, the
+ * blocks that run abandon their waits after a bounded number of polls (about 0.3 s) and the launch
+ * drains with invalid results; ar_hip_qwen3_next / run then recompute the steps of that call as
+ * separate launches before returning (same tokens, logits and sampler draws as an undisturbed call)
+ * and switch the model to separate launches (ar_hip_qwen3_persistent reports 0) until
+ * ar_hip_qwen3_use_persistent(m, 1). */
 int ar_hip_qwen3_use_persistent(ar_qwen3 *m, int enable);
 int ar_hip_qwen3_persistent(ar_qwen3 *m, int *active);
-/* Infinity-Cache prefetch: a second stream reads layer l+1's weights while layer l computes, with
- * `blocks` x 256 threads (default 0 = off: on MI355X the extra
- * cross-stream dependencies cost more than the cache hits save).  No counterpart in the reference (its CPU
- * backend has no memory hierarchy to manage); a throughput knob only, results are unchanged. */
-int ar_hip_qwen3_use_prefetch(ar_qwen3 *m, int blocks);
+/* Steps recomputed as separate launches after a timed-out persistent launch, over the model's life. */
+int ar_hip_qwen3_persistent_recomputed(ar_qwen3 *m, int *steps);
+/* Polls of one cross-block wait of the persistent kernel before it is abandoned (0: the default,
+ * 2^18).  A test and diagnostic knob: a small limit makes the waits time out while every block of the
+ * launch still runs to its end, which exercises the recompute above without any other load on the
+ * device. */
+int ar_hip_qwen3_persistent_wait_limit(ar_qwen3 *m, unsigned polls);
 
 #ifdef __cplusplus
 }

@@ -285,6 +285,110 @@ def test_c3_persistent_step_matches_multi_launch(ctx):
     assert rel_err(lg_p[0], lg_m[0]) <= 1e-5
 
 
+def persistent_split_plan(pos, rows_per_split=32, max_splits=8):
+    """(splits per KV head, longest split) of the C3 persistent kernel's attention at position pos:
+    ceil((pos + 1) / 32) splits, at most 8, of ceil((pos + 1) / splits) rows."""
+    n = pos + 1
+    s = min(max(-(-n // rows_per_split), 1), max_splits)
+    return s, -(-n // s)
+
+
+def test_c3_full_workload_persistent_vs_oracle(ctx):
+    """BASELINE C3 end to end on the default decode step (the persistent kernel): the 128-token
+    prompt fed one token per step as AutoregressiveModel feeds it, then all 256 greedy steps
+    (positions 0..383), against the FP32 oracle: tokens bit-exact (up to a near-tie of the oracle),
+    logits within 1e-4 (max|gpu-ref| / max|ref|) at every one of the 384 steps, and the argmax of every
+    step whose oracle top-2 margin is at least 1e-5.  At C3 the kernel cuts each KV head's context into
+    1..8 splits of up to 48 rows: the run covers every split count and split length."""
+    cfg = C.C3_0_6B
+    prompt = synthetic.prompt_ids(C.C3_PROMPT, cfg.vocab_size, seed=0)
+    sd = synthetic.state_dict(cfg, seed=0)
+    with Qwen3(cfg, sd, ctx) as m:
+        assert m.model.persistent
+        fed, logits = gpu_generate(m, prompt, C.C3_DECODE)
+    ref = oracle.OracleQwen3(cfg, sd, precision="fp32")
+    del sd
+    rf, rl = ref.generate(prompt, C.C3_DECODE)
+    ref.close()
+    steps = len(prompt) + C.C3_DECODE
+    assert fed.shape[1] == steps == cfg.seq_len
+    assert compare_tokens(fed[0], rf, rl, len(prompt)) == steps
+    per_step = np.abs(logits[0] - rl).max(axis=1) / np.abs(rl).max(axis=1)
+    worst = int(per_step.argmax())
+    assert per_step[worst] <= LOGIT_TOL_F32, (worst, per_step[worst])
+    n, distinct, margin = argmax_decisions(logits[0], rl)
+    plans = [persistent_split_plan(p) for p in range(steps)]
+    counts = sorted({s for s, _ in plans})
+    longest = max(t for _, t in plans)
+    print(f"C3 full workload: {steps} steps, tokens equal, worst step logit err {per_step[worst]:.2e} at "
+          f"{worst}; {n} argmax decisions over {distinct} distinct tokens (min margin {margin:.1e}); "
+          f"split counts {counts}, longest split {longest} rows; "
+          f"{len(set(rf[len(prompt):].tolist()))} distinct generated tokens", flush=True)
+    assert counts == list(range(1, 9)) and longest == 48, (counts, longest)
+    assert n >= steps - 8 and distinct >= 16, (n, distinct)
+
+
+def test_persistent_timeout_recomputed_as_separate_launches(ctx):
+    """A persistent launch whose cross-block waits time out, forced from the host with a wait limit
+    of one poll (every block still runs to its end), is recomputed as separate launches before next()
+    / run() return: tokens and logits equal an undisturbed run's, the model reports separate launches
+    afterwards, and once re-enabled at the normal limit the persistent steps continue from the
+    recomputed state (the exchange words were cleared) and still match.  With the sampler on, the
+    recomputed call draws exactly what an undisturbed call draws (the generators are restored)."""
+    cfg = dataclasses.replace(C.C3_0_6B, layer_count=2, vocab_size=4096, shared_weights=False, seq_len=64)
+    prompt = synthetic.prompt_ids(12, cfg.vocab_size, seed=41)
+    sd = synthetic.state_dict(cfg, seed=41)
+    n_dec = 12
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        assert am.persistent
+        am.use_persistent(False)
+        ref_fed, ref_lg = gpu_generate(m, prompt, n_dec)
+        am.use_persistent(True)
+        # next(): a prompt step and a generated step time out
+        am.reset()
+        am.set_prompt(prompt)
+        fed, lgs = [], []
+        for s in range(len(prompt) + n_dec):
+            forced = s in (5, len(prompt) + 3)
+            if forced:
+                am.persistent_wait_limit(1)
+            t, lg = am.next(return_logits=True)
+            if forced:
+                assert not am.persistent
+                am.persistent_wait_limit(0)
+                am.use_persistent(True)
+            fed.append(t)
+            lgs.append(lg)
+        assert am.persistent_recomputed == 2
+        fed, lgs = np.stack(fed, axis=1), np.stack(lgs, axis=1)
+        stop = compare_tokens(fed[0], ref_fed[0], ref_lg[0], len(prompt))
+        assert stop == ref_fed.shape[1], f"near-tie at step {stop}"
+        assert rel_err(lgs[0], ref_lg[0]) <= 1e-5
+        # run(): every step of the call times out and is recomputed
+        am.reset()
+        am.set_prompt(prompt)
+        am.persistent_wait_limit(1)
+        toks = am.run(len(prompt) + n_dec)
+        assert not am.persistent and am.persistent_recomputed == 2 + len(prompt) + n_dec
+        np.testing.assert_array_equal(toks, ref_fed)
+        # sampling: the recomputed steps draw what an undisturbed run draws
+        am.persistent_wait_limit(0)
+        sampled = {}
+        for persistent in (False, True):
+            am.use_persistent(persistent)
+            am.reset()
+            am.set_prompt(prompt)
+            am.set_sampling(hw.SAMPLE_TOKEN, 0.8, 0.9, seeds=[7])
+            if persistent:
+                am.persistent_wait_limit(1)
+            sampled[persistent] = am.run(len(prompt) + n_dec)
+            am.persistent_wait_limit(0)
+        am.set_temperature(0.0)
+        np.testing.assert_array_equal(sampled[True], sampled[False])
+        assert len(set(sampled[False][0, len(prompt):].tolist())) >= 3
+
+
 @pytest.mark.parametrize("seq_len", [3000, 4500])
 def test_long_context_split_attention(ctx, seq_len):
     """Caches long enough that the decode step cuts the context into up to 128 splits of up to 24 /
@@ -322,6 +426,11 @@ def test_kernel_loop_probe(ctx, c1):
             am.kernel_loop(q.KT_ATTENTION, 4)
         with pytest.raises(hw.HardwareException):
             am.kernel_loop(q.KT_QKV, 0)
+        # the probe overwrote the step state: no step before reset()
+        am.set_prompt(prompt)
+        with pytest.raises(hw.HardwareException) as e:
+            am.next()
+        assert e.value.code == hw.AR_HIP_ERR_STATE
         am.reset()
         am.set_prompt(prompt)
         assert np.array_equal(am.run(len(prompt) + 8), before)

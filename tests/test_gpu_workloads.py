@@ -158,3 +158,32 @@ def test_c4_workload_batch1_persistent_vs_oracle_and_multi_launch(ctx):
     assert np.array_equal(toks, toks_m)
     assert rel_err(lgs[0], lgs_m[0]) <= 1e-5, rel_err(lgs[0], lgs_m[0])
     assert rel_err(sl[0], sl_m[0]) <= 1e-5, rel_err(sl[0], sl_m[0])
+
+
+def test_c4_full_depth_prefill_and_persistent_decode_vs_oracle(ctx):
+    """BASELINE C4 at full depth: the Qwen3-1.7B shape with all 28 layers and the tied
+    151,936-word head, bf16 weights, a 2048-token prompt through the batched prefill (fp16 MFMA GEMMs
+    and flash attention), then 16 greedy steps on the persistent decode kernel, against the FP32
+    oracle's batched prompt pass and decode steps on the same bf16-rounded weights: logits within
+    2e-2 of the oracle at the last prompt row and at every step, and all 16 greedy decisions equal."""
+    T, steps = C.C4_PROMPT, 16
+    cfg = dataclasses.replace(C.C4_1_7B, seq_len=T + steps + 8, max_batch=1)
+    assert cfg.layer_count == 28 and cfg.shared_weights and cfg.vocab_size == 151936
+    sd = synthetic.state_dict(cfg, seed=41)
+    prompt = synthetic.prompt_ids(T, cfg.vocab_size, seed=42)
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        assert am.persistent, "the bf16 C4 shape should run the persistent decode kernel"
+        am.reset()
+        am.set_prompt(prompt)
+        lp = am.prefill(return_logits=True)
+        assert am.prefill_by_steps() == 0, "the C4 prompt must take the batched path"
+        out = [am.next(return_logits=True) for _ in range(steps)]
+        assert am.persistent and am.persistent_recomputed == 0
+    toks = np.stack([t for t, _ in out], axis=1)
+    lgs = np.stack([lg for _, lg in out], axis=1)
+    fed, rl = _oracle_stream(cfg, sd, prompt, steps)
+    del sd
+    assert len(set(fed.tolist())) >= 3, f"degenerate reference stream {fed.tolist()}"
+    compared = _check_against("C4 full depth vs oracle", lp[0], toks[0], lgs[0], fed, rl)
+    assert len(compared) == steps, compared
