@@ -337,6 +337,104 @@ def prefill_probe(args):
                                         "by_steps": by_steps}}), flush=True)
 
 
+TRACE_MARKS = ["layer start", "QKV input (thread 0)", "QKV stored", "attention input (thread 0)", "attention stored",
+               "merge input (thread 0)", "merge stored", "O input (thread 0)", "O stored", "gate/up input (thread 0)",
+               "gate/up stored", "down input (thread 0)", "down stored", "final input", "logits end",
+               "QKV all inputs", "attention all inputs", "attention q/k normalised", "attention rows scored (wave 0)",
+               "attention waves merged", "merge all inputs", "O all inputs", "gate/up all inputs", "down all inputs"]
+TRACE_STEPS = 24
+
+
+def stage_trace(args):
+    """Per-stage timeline of the persistent decode kernel at C3 (or C4 with --stage-trace c4): needs the
+    diagnostic build (python -m common_amd.build --trace, loaded with AR_HIP_LIB=common_amd/lib/trace/
+    libar_hip.so), whose kernel records the wall clock (10 ns ticks, common to all CUs) at every stage
+    boundary of every layer in thread 0 of every block.  The prompt is prefilled, TRACE_STEPS decode
+    steps are traced one by one; per layer (layers 1..L-2), times are taken from the median block's
+    layer start: the median over the blocks that run a stage of its input / stored marks, the slowest
+    producer's store, and the exchange latency = consumers' median input - slowest producer's store.
+    Printed as one JSON line; medians over layers and steps."""
+    import ctypes
+    import dataclasses
+
+    import numpy as np
+
+    from common_amd import config as C
+    from common_amd import hardware as hw
+    from common_amd import synthetic
+    from common_amd.qwen3 import Qwen3
+
+    L_lib = hw.lib()
+    if not hasattr(L_lib, "ar_hip_pk_trace_read"):
+        raise SystemExit("stage trace: load the trace build (AR_HIP_LIB=common_amd/lib/trace/libar_hip.so)")
+    if args.stage_trace == "c4":
+        cfg, T = C.C4_1_7B, C.C4_PROMPT
+    else:
+        cfg, T = C.C3_0_6B, C.C3_PROMPT
+    cfg = dataclasses.replace(cfg, seq_len=max(cfg.seq_len, T + 8 + TRACE_STEPS))
+    prompt = synthetic.prompt_ids(T, cfg.vocab_size, seed=args.seed)
+    buf = np.zeros((64, 256, 24), np.uint64)
+    L_lib.ar_hip_pk_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    G = cfg.head_count // cfg.kv_head_count
+    rows = {k: [] for k in ("input", "stored", "slowest_store", "exchange", "att", "mrg", "free")}
+    per_layer_us = []
+    with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed)) as model:
+        am = model.model
+        assert am.persistent, "the stage trace needs the persistent decode kernel"
+        am.reset()
+        am.set_prompt(prompt)
+        am.prefill()
+        am.run(5)
+        smax = 8 if cfg.dim == 1024 else 28
+        for step in range(TRACE_STEPS):
+            pos = T + 5 + step
+            am.run(1)
+            hw.check(L_lib.ar_hip_pk_trace_read(buf.ctypes.data, buf.nbytes))
+            nsplit = min(max(-(-(pos + 1) // 32), 1), smax)
+            att = np.arange(cfg.kv_head_count * nsplit)
+            mrg = np.arange(256 - cfg.head_count, 256)
+            if nsplit > 1:  # the split merge may run in dedicated blocks or in the attention blocks
+                lt = buf[2].astype(np.int64)
+                t_ref = np.median(lt[:, 0])
+                alt = np.arange(min(cfg.head_count, cfg.kv_head_count * nsplit))
+                if np.median(np.abs(lt[alt, 5] - t_ref)) < np.median(np.abs(lt[mrg, 5] - t_ref)):
+                    mrg = alt
+            allb = np.arange(256)
+            who = {1: allb, 2: allb, 3: att, 4: att, 5: mrg, 6: mrg, 7: allb, 8: allb, 9: allb, 10: allb, 11: allb,
+                   12: allb, 15: allb, 16: att, 17: att, 18: att, 19: att, 20: mrg, 21: allb, 22: allb, 23: allb}
+            # each stage's input: (consumer all-inputs mark, producer stored mark, producer blocks, layer offset)
+            feeds = {"QKV": (15, 12, allb, -1), "attention": (16, 2, allb, 0), "merge": (20, 4, att, 0),
+                     "O": (21, 6, mrg, 0), "gate/up": (22, 8, allb, 0), "down": (23, 10, allb, 0)}
+            for l in range(1, cfg.layer_count - 1):
+                t = buf[l].astype(np.int64)
+                t0 = np.median(t[:, 0])
+                per_layer_us.append((np.median(buf[l + 1][:, 0].astype(np.int64)) - t0) * 0.01)
+                inp = {k: (np.median(t[who[k], k]) - t0) * 0.01 for k in who}
+                rows["input"].append([inp.get(k, np.nan) for k in range(24)])
+                ex = []
+                for name, (ci, ps, pb, dl) in feeds.items():
+                    prod = buf[l + dl].astype(np.int64)[pb, ps]
+                    cons = t[who[ci], ci]
+                    ex.append((np.median(cons) - prod.max()) * 0.01)
+                rows["exchange"].append(ex)
+                rows["slowest_store"].append([(t[who[k], k].max() - t0) * 0.01 if k in who else np.nan
+                                              for k in range(24)])
+                free = np.setdiff1d(allb, np.concatenate([att, mrg]))
+                for g, bl in (("att", att), ("mrg", mrg), ("free", free)):
+                    rows[g].append([(np.median(t[bl, k]) - t0) * 0.01 if who.get(k) is allb else np.nan
+                                    for k in range(24)])
+    med = lambda a: [round(float(v), 2) for v in np.nanmedian(np.array(a, np.float64), axis=0)]
+    out = {"stage_trace": {"workload": args.stage_trace, "steps": TRACE_STEPS, "positions": f"{T + 5}..{T + 4 + TRACE_STEPS}",
+                           "layer_us_median": round(float(np.median(per_layer_us)), 2),
+                           "median_block_us": dict(zip(TRACE_MARKS, med(rows["input"]))),
+                           "slowest_block_us": dict(zip(TRACE_MARKS, med(rows["slowest_store"]))),
+                           "by_role_median_us": {g: dict(zip(TRACE_MARKS, med(rows[g])))
+                                                 for g in ("att", "mrg", "free")},
+                           "exchange_us": dict(zip(["QKV", "attention", "merge", "O", "gate/up", "down"],
+                                                   med(rows["exchange"])))}}
+    print(json.dumps(out), flush=True)
+
+
 # kernel-name prefixes of the C3 decode classes in a rocprofv3 trace (batch 1, fp32 weights)
 C3_CLASS_KERNELS = {
     "decode_persistent": "decode_persistent_kernel",
@@ -573,6 +671,8 @@ def main():
                     help="only run the workload of the rocprofv3 FETCH_SIZE / WRITE_SIZE passes and exit")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise the two counter passes' CSV output directories per decode class and exit")
+    ap.add_argument("--stage-trace", choices=("c3", "c4"),
+                    help="per-stage timeline of the persistent decode kernel (needs the trace build) and exit")
     ap.add_argument("--prefill-probe", choices=("c3", "c4"),
                     help="only run that workload's prompt through the batched prefill (a warm call and "
                          "PREFILL_PROBE_RUNS more, no decode step) for rocprofv3 counter passes, and exit")
@@ -589,6 +689,9 @@ def main():
         return
     if args.prefill_probe:
         prefill_probe(args)
+        return
+    if args.stage_trace:
+        stage_trace(args)
         return
     sections = {x.strip() for x in args.sections.split(",") if x.strip()}
     if "c3" not in sections:  # profiling aid: only the named extra sections, one JSON line of them

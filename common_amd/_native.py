@@ -9,7 +9,8 @@ import ctypes
 import os
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
-HIP_LIB = os.path.join(LIB_DIR, "libar_hip.so")
+# AR_HIP_LIB names another build of the backend library (the stage-trace build, lib/trace/libar_hip.so)
+HIP_LIB = os.environ.get("AR_HIP_LIB") or os.path.join(LIB_DIR, "libar_hip.so")
 SYNTH_LIB = os.path.join(LIB_DIR, "libar_synth.so")
 
 _cache = {}

@@ -44,18 +44,24 @@ def build_synth():
     return out
 
 
-def build_hip(jobs: int = 8):
+def build_hip(jobs: int = 8, trace: bool = False):
+    """libar_hip.so; trace=True builds the diagnostic variant with the persistent decode kernel's stage
+    timeline (-DAR_PK_TRACE) into lib/trace/ (load it with AR_HIP_LIB=<that path>)."""
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    os.makedirs(OBJ, exist_ok=True)
+    obj_dir = os.path.join(OBJ, "trace") if trace else OBJ
+    lib_dir = os.path.join(LIB, "trace") if trace else LIB
+    os.makedirs(obj_dir, exist_ok=True)
+    os.makedirs(lib_dir, exist_ok=True)
+    extra = ["-DAR_PK_TRACE"] if trace else []
 
     def compile_one(src):
-        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-I", os.path.join(HERE, "..", "include"), "-c", src, "-o", obj])
+        obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+        _run([HIPCC, *HIP_FLAGS, *extra, "-I", os.path.join(HERE, "..", "include"), "-c", src, "-o", obj])
         return obj
 
     def compile_host(src):
         # host-only C++ (no device code): the host compiler, as its own objects in the library
-        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+        obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
         _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(HERE, "..", "include"), "-c", src,
               "-o", obj])
         return obj
@@ -63,7 +69,7 @@ def build_hip(jobs: int = 8):
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, srcs))
         objs += list(ex.map(compile_host, sorted(glob.glob(os.path.join(CSRC, "*.cpp")))))
-    out = os.path.join(LIB, "libar_hip.so")
+    out = os.path.join(lib_dir, "libar_hip.so")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", *objs])
     os.replace(out + ".tmp", out)
     return out
@@ -78,5 +84,10 @@ def build(jobs: int = 8):
 
 
 if __name__ == "__main__":
-    for p in build(int(sys.argv[1]) if len(sys.argv) > 1 else 8):
-        print("built", p)
+    args = [a for a in sys.argv[1:] if a != "--trace"]
+    jobs = int(args[0]) if args else 8
+    if "--trace" in sys.argv[1:]:
+        print("built", build_hip(jobs, trace=True))
+    else:
+        for p in build(jobs):
+            print("built", p)

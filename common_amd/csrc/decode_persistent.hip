@@ -30,6 +30,27 @@
 #include "ar_hip_internal.h"
 #include "gemv_impl.h"
 
+// Stage timeline (diagnostic build only, -DAR_PK_TRACE): thread 0 of every block records the wall
+// clock (100 MHz, common to all CUs) at each stage boundary of every layer; ar_hip_pk_trace_read
+// copies the table out.  The default build compiles the marks away.
+#ifdef AR_PK_TRACE
+constexpr int kTraceLayers = 64, kTraceMarks = 24;
+__device__ unsigned long long g_pk_trace[kTraceLayers][256][kTraceMarks];
+#define PK_MARK(l, k)                                                                              \
+    do {                                                                                           \
+        if (threadIdx.x == 0 && (l) < kTraceLayers) g_pk_trace[(l)][blockIdx.x][(k)] = wall_clock64(); \
+    } while (0)
+extern "C" int ar_hip_pk_trace_read(void* dst, size_t bytes) {
+    if (bytes < sizeof(g_pk_trace)) return AR_HIP_ERR_INVALID;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_pk_trace), sizeof(g_pk_trace)) == hipSuccess ? AR_HIP_OK
+                                                                                                : AR_HIP_ERR_HIP;
+}
+#else
+#define PK_MARK(l, k) \
+    do {              \
+    } while (0)
+#endif
+
 namespace {
 
 constexpr int kPB = 256;           // blocks: one per CU
@@ -39,7 +60,9 @@ constexpr int kRowsPerSplit = 32;  // cache rows per split before another split 
 constexpr unsigned kSpinLimit = 1u << 18;  // default polls before a wait is abandoned (~0.3 s)
 constexpr int kPadLds = 64 * 1024;         // dynamic LDS that keeps a second block off each CU
 constexpr int kMaxLayers = 64;             // layer table held in LDS
-constexpr unsigned kGateUpDelay = 250;     // wall-clock ticks (10 ns): see the O stage
+// gate/up hold-back of the blocks without attention, wall-clock ticks (10 ns): see the O stage
+template <typename TW>
+constexpr unsigned kGateUpDelay = sizeof(TW) == 4 ? 150 : 250;
 
 struct PLayer {
     const void* wqkv;  // projection weights in the model's weight type (fp32 or bf16)
@@ -288,8 +311,13 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         reinterpret_cast<uint64_t*>(lay_s)[i] = reinterpret_cast<const uint64_t*>(p.layers)[i];
     __syncthreads();
 
-    // QKV rows: layer 0's before the loop, layer l+1's at the start of layer l's gate/up stage (whose
-    // own rows are in by then; issued in the QKV stage itself: 0.697 vs 0.689 ms per C3 step)
+    // QKV rows: layer 0's before the loop, layer l+1's after layer l's down stores (fp32 weights) or at
+    // the start of layer l's gate/up stage (bf16 weights, whose register budget has no room for them
+    // there).  A wavefront's memory operations leave a CU in issue order, so rows issued at the
+    // gate/up stage's start sit ahead of that stage's input poll and its stores (each waited ~1.5 us
+    // longer, stage timeline); issued after the down stores they only delay the next QKV stage's dot
+    // products: C3 0.593 -> 0.584 ms per step.
+    constexpr bool kQkvAfterDown = sizeof(TW) == 4;
     wraw wq[RPWq][NCq];
     auto load_wq = [&](const void* W, int wave, int lane) {
         const int r0 = b * RQ + wave * RPWq;
@@ -309,6 +337,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         const uint64_t* prev = p.ll + (size_t)((l + 1) & 1) * PAR_WORDS;
 
         // ================= P1: QKV =================================================
+        PK_MARK(l, 0);
         lds_barrier();  // the previous layer's readers of xin / xr are done
         {
         STAGE_IDS();
@@ -328,6 +357,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XA + tid + j * kPT : -1;
                 ll_wait<NX>(prev, idx, xv, base + (unsigned)l, dead, p.err, p.spin_limit);
             }
+            PK_MARK(l, 1);
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < NX; j++) {
@@ -339,6 +369,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 }
             }
             const float tot = block_sum(ss, red, lane, wave);  // (its barrier also publishes xr / xin)
+            PK_MARK(l, 15);
             const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
             float ssq = 0.f;
 #pragma unroll
@@ -369,31 +400,42 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         }
         }
 
+        PK_MARK(l, 2);
         const unsigned long long t_p1 = wall_clock64();  // (100 MHz)
         // ================= P2: attention (blocks of (KV head, split)) ==============
+        // The split's cache rows are dealt round-robin to the wavefronts; a lane holds HD / 64
+        // dimensions of a row, so each score is one full-wavefront sum (DPP into lane 63, read back as
+        // a uniform value) and every wavefront runs its own online softmax over its rows; the eight
+        // wavefront states merge through LDS.  (Rows in 16-lane groups, four groups per wavefront,
+        // needed two lane-swap merges of the 2 x 8 accumulators per lane: 2.75 -> 2.2 us from the
+        // attention inputs to the partials' stores, C3 0.596 -> 0.588 ms per step.)
         if (b < KV * nsplit) {
             STAGE_IDS();
-            constexpr int EPL = HD / 16, NGR = kPT / 16, RU = 2;
+            constexpr int DPL = HD / 64;                  // cache dimensions per lane
+            constexpr int RW = SMAX <= 8 ? 6 : 10;        // cache rows per wavefront per chunk
+            static_assert(DPL == 1 || DPL == 2, "head size 64 or 128");
             const int g = b / nsplit, s = b - g * nsplit;
             const int t0 = s * tile, t1 = min(t0 + tile, n);
-            const int grp = tid >> 4, gl = tid & 15;
             const size_t head_base = ((size_t)l * KV + g) * (size_t)p.S * HD;
             float* kc = p.kcache + head_base;
             float* vc = p.vcache + head_base;
-            auto dim_of = [&](int e) { return 16 * (e & ~3) + gl * 4 + (e & 3); };
-            float kr[RU][EPL], vr[RU][EPL];
-            auto load_rows = [&](float (&dst)[RU][EPL], const float* src, int c) {
+            // row j of chunk c of this wavefront (uniform over the wavefront)
+            auto row_of = [&](int c, int j) { return t0 + c * (kPW * RW) + wave + kPW * j; };
+            float kr[RW][DPL], vr[RW][DPL];
+            auto load_rows = [&](float (&dst)[RW][DPL], const float* src, int c) {
 #pragma unroll
-                for (int j = 0; j < RU; j++) {
-                    const int t = min(t0 + grp + NGR * (c * RU + j), t1 - 1);
-#pragma unroll
-                    for (int e = 0; e < EPL; e += 4) {
-                        const float4 v = *reinterpret_cast<const float4*>(src + (size_t)t * HD + 16 * e + gl * 4);
-                        dst[j][e] = v.x; dst[j][e + 1] = v.y; dst[j][e + 2] = v.z; dst[j][e + 3] = v.w;
+                for (int j = 0; j < RW; j++) {
+                    const float* r = src + (size_t)min(row_of(c, j), t1 - 1) * HD + lane * DPL;
+                    if constexpr (DPL == 2) {
+                        const float2 v = *reinterpret_cast<const float2*>(r);
+                        dst[j][0] = v.x;
+                        dst[j][1] = v.y;
+                    } else {
+                        dst[j][0] = r[0];
                     }
                 }
             };
-            const int nch = t1 > t0 ? (t1 - t0 + NGR * RU - 1) / (NGR * RU) : 0;
+            const int nch = t1 > t0 ? (t1 - t0 + kPW * RW - 1) / (kPW * RW) : 0;
             if (nch > 0) {  // cache rows before pos are final: issued before the wait for q / k / v
                 load_rows(kr, kc, 0);
                 load_rows(vr, vc, 0);
@@ -434,6 +476,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
             float qv[2];
             ll_wait<2>(cur, idx, qv, ep, dead, p.err, p.spin_limit);  // (words not waited for read as 0)
+            PK_MARK(l, 3);
             if (p.per_head) {
                 if (tid >= T_S && tid - T_S < (G + 1) * RPH) ss_s[tid - T_S] = qv[0];
             } else {
@@ -445,6 +488,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
             if (tid >= T_V && tid < T_S) v_new[tid - T_V] = qv[0];
             lds_barrier();
+            PK_MARK(l, 16);
             const bool has_pos = pos >= t0 && pos < t1;
             // normalised, rotated q (G heads) and k from the pair this thread holds; the block holding
             // pos writes the cache rows
@@ -480,49 +524,43 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 vc[(size_t)pos * HD + (tid - T_V)] = qv[0];
             }
             lds_barrier();
+            PK_MARK(l, 17);
 
             const float c2 = 1.4426950408889634f / sqrtf((float)HD);
-            float qf[G][EPL];
+            float qf[G][DPL];
 #pragma unroll
             for (int gg = 0; gg < G; gg++)
 #pragma unroll
-                for (int e = 0; e < EPL; e += 4) {
-                    const float4 t = *reinterpret_cast<const float4*>(&q_s[gg][dim_of(e)]);
-                    qf[gg][e] = t.x * c2; qf[gg][e + 1] = t.y * c2; qf[gg][e + 2] = t.z * c2; qf[gg][e + 3] = t.w * c2;
-                }
-            float m[G], lsum[G], acc[G][EPL];
+                for (int e = 0; e < DPL; e++) qf[gg][e] = q_s[gg][lane * DPL + e] * c2;
+            float m[G], lsum[G], acc[G][DPL];
 #pragma unroll
             for (int gg = 0; gg < G; gg++) {
                 m[gg] = -INFINITY;
                 lsum[gg] = 0.f;
 #pragma unroll
-                for (int e = 0; e < EPL; e++) acc[gg][e] = 0.f;
+                for (int e = 0; e < DPL; e++) acc[gg][e] = 0.f;
             }
             for (int c = 0; c < nch; c++) {
                 if (has_pos) {
 #pragma unroll
-                    for (int j = 0; j < RU; j++)
-                        if (min(t0 + grp + NGR * (c * RU + j), t1 - 1) == pos)
+                    for (int j = 0; j < RW; j++)
+                        if (min(row_of(c, j), t1 - 1) == pos)
 #pragma unroll
-                            for (int e = 0; e < EPL; e++) {
-                                kr[j][e] = k_new[dim_of(e)];
-                                vr[j][e] = v_new[dim_of(e)];
+                            for (int e = 0; e < DPL; e++) {
+                                kr[j][e] = k_new[lane * DPL + e];
+                                vr[j][e] = v_new[lane * DPL + e];
                             }
                 }
-                float sc[G][RU];
+                float sc[G][RW];  // (uniform over the wavefront)
 #pragma unroll
-                for (int j = 0; j < RU; j++) {
-                    const bool valid = t0 + grp + NGR * (c * RU + j) < t1;
+                for (int j = 0; j < RW; j++) {
+                    const bool valid = row_of(c, j) < t1;
 #pragma unroll
                     for (int gg = 0; gg < G; gg++) {
                         float d = 0.f;
 #pragma unroll
-                        for (int e = 0; e < EPL; e++) d = fmaf(qf[gg][e], kr[j][e], d);
-                        // sum over the 16 lanes of the row group (quad swaps, half-row and row mirrors)
-                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0xB1, 0xF, 0xF, true));
-                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x4E, 0xF, 0xF, true));
-                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x141, 0xF, 0xF, true));
-                        d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x140, 0xF, 0xF, true));
+                        for (int e = 0; e < DPL; e++) d = fmaf(qf[gg][e], kr[j][e], d);
+                        d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gemv::dpp_sum_lane63(d)), 63));
                         sc[gg][j] = valid ? d : -INFINITY;
                     }
                 }
@@ -531,52 +569,37 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 for (int gg = 0; gg < G; gg++) {
                     float mc = sc[gg][0];
 #pragma unroll
-                    for (int j = 1; j < RU; j++) mc = fmaxf(mc, sc[gg][j]);
+                    for (int j = 1; j < RW; j++) mc = fmaxf(mc, sc[gg][j]);
                     const float mn = fmaxf(m[gg], mc);
                     if (mn == -INFINITY) continue;
                     const float alpha = (m[gg] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[gg] - mn);
                     lsum[gg] *= alpha;
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) acc[gg][e] *= alpha;
+                    for (int e = 0; e < DPL; e++) acc[gg][e] *= alpha;
 #pragma unroll
-                    for (int j = 0; j < RU; j++) {
+                    for (int j = 0; j < RW; j++) {
                         const float pj = __builtin_amdgcn_exp2f(sc[gg][j] - mn);
                         lsum[gg] += pj;
 #pragma unroll
-                        for (int e = 0; e < EPL; e++) acc[gg][e] = fmaf(pj, vr[j][e], acc[gg][e]);
+                        for (int e = 0; e < DPL; e++) acc[gg][e] = fmaf(pj, vr[j][e], acc[gg][e]);
                     }
                     m[gg] = mn;
                 }
                 if (c + 1 < nch) load_rows(vr, vc, c + 1);
             }
-            // merge the row groups: the four of a wavefront by lane swaps, the wavefronts via LDS
-            auto merge_with = [&](auto partner) {
+            PK_MARK(l, 18);
+            // the wavefronts' states through LDS
 #pragma unroll
-                for (int gg = 0; gg < G; gg++) {
-                    const float mo = partner(m[gg]), lo = partner(lsum[gg]);
-                    const float mn = fmaxf(m[gg], mo);
-                    const float a = (m[gg] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[gg] - mn);
-                    const float bo = (mo == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mo - mn);
-                    lsum[gg] = lsum[gg] * a + lo * bo;
+            for (int gg = 0; gg < G; gg++) {
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) acc[gg][e] = acc[gg][e] * a + partner(acc[gg][e]) * bo;
-                    m[gg] = mn;
-                }
-            };
-            merge_with([&](float v) { return xor16(v, lane); });
-            merge_with([&](float v) { return xor32(v, lane); });
-            if (lane < 16) {
-#pragma unroll
-                for (int gg = 0; gg < G; gg++) {
-#pragma unroll
-                    for (int e = 0; e < EPL; e++) red_acc[wave][gg][dim_of(e)] = acc[gg][e];
-                    if (lane == 0) {
-                        red_m[wave][gg] = m[gg];
-                        red_l[wave][gg] = lsum[gg];
-                    }
+                for (int e = 0; e < DPL; e++) red_acc[wave][gg][lane * DPL + e] = acc[gg][e];
+                if (lane == 0) {
+                    red_m[wave][gg] = m[gg];
+                    red_l[wave][gg] = lsum[gg];
                 }
             }
             lds_barrier();
+            PK_MARK(l, 19);
             for (int idx = tid; idx < G * HD; idx += kPT) {
                 const int gg = idx / HD, i = idx - gg * HD;
                 float M = -INFINITY;
@@ -596,6 +619,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                     ll_put(slot + HD + 1, ep, Ls);
                 }
             }
+            PK_MARK(l, 4);
         }
 
         // O rows and gate/up rows of this block (held from their issue to the O and gate/up stages)
@@ -611,11 +635,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
             // The blocks that are not busy with attention hold the gate/up rows back kGateUpDelay
             // after their QKV stage: issued at once they queue in HBM ahead of the attention's cache
-            // rows and exchanges (measured at C3, ms per step: at once 0.711, after 1.5 / 2 / 2.5 /
-            // 3 / 4 us 0.699 / 0.696 / 0.696 / 0.696 / 0.709, in their own stage 0.712; the down rows
-            // issued here as well, after 4-5.5 us: 0.709-0.716).
+            // rows and exchanges.  Measured at C3 (ms per step) with the current schedule: at once
+            // 0.569, after 0.5 / 1 / 1.5 / 2 / 2.5 us 0.571 / 0.569 / 0.560 / 0.564 / 0.576; the down
+            // rows issued here as well (blocks without attention or merge): 0.580 vs 0.576.
             if (b >= KV * nsplit && i0 == 0)
-                while (wall_clock64() < t_p1 + kGateUpDelay) __builtin_amdgcn_s_sleep(4);
+                while (wall_clock64() < t_p1 + kGateUpDelay<TW>) __builtin_amdgcn_s_sleep(4);
             const bool up = wave >= kPW / 2;
             const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
             const void* W = up ? Ly.w3 : Ly.w1;
@@ -654,6 +678,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                            : -1;
             float v[SPT + 1];
             ll_wait<SPT + 1>(cur, idx, v, ep, dead, p.err, p.spin_limit);
+            PK_MARK(l, 5);
 #pragma unroll
             for (int k = 0; k < SPT; k++) mrg_o[s0 + k][i] = v[k];
             if (tid < 2 * SMAX) {
@@ -661,6 +686,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 else mrg_ml[sml].x = sml < nsplit ? v[SPT] : -INFINITY;
             }
             lds_barrier();
+            PK_MARK(l, 20);
             if (tid < HD) {
                 float M = -INFINITY;
 #pragma unroll
@@ -676,6 +702,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                     }
                 ll_put(cur + OFF_A + h * HD + tid, ep, o / Ls);
             }
+            PK_MARK(l, 6);
         }
 
         // ================= P3: O projection + residual ==============================
@@ -694,9 +721,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             for (int j = 0; j < NA; j++) idx[j] = OFF_A + tid + j * kPT;
             float av[NA];
             ll_wait<NA>(cur, idx, av, ep, dead, p.err, p.spin_limit);
+            PK_MARK(l, 7);
 #pragma unroll
             for (int j = 0; j < NA; j++) xin[tid + j * kPT] = av[j];
             lds_barrier();
+            PK_MARK(l, 21);
             float a = 0.f;
 #pragma unroll
             for (int c = 0; c < NCo; c++) a = WR::dot(wo[c], &xin[col0 + c * CW + lane * WR::V], a);
@@ -710,13 +739,14 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 const int r = b * RO + tid;
                 ll_put(cur + OFF_XM + r, ep, xr[r] + sum);
             }
+            PK_MARK(l, 8);
         }
 
         // ================= P4: gate/up + SwiGLU =====================================
         lds_barrier();  // xin / rows_s readers (P3) are done
         {
             STAGE_IDS();
-            if (l + 1 < p.L) load_wq(lay_s[l + 1].wqkv, wave, lane);
+            if (!kQkvAfterDown && l + 1 < p.L) load_wq(lay_s[l + 1].wqkv, wave, lane);
             constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
             float gv[NX];
 #pragma unroll
@@ -726,6 +756,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XM + tid + j * kPT : -1;
             float xv[NX];
             ll_wait<NX>(cur, idx, xv, ep, dead, p.err, p.spin_limit);
+            PK_MARK(l, 9);
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < NX; j++) {
@@ -737,6 +768,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 }
             }
             const float tot = block_sum(ss, red, lane, wave);
+            PK_MARK(l, 22);
             const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
 #pragma unroll
             for (int i = 0; i < RPWg; i++) {
@@ -752,6 +784,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 const float sg = 1.0f / (expf(-gt) + 1.0f);
                 ll_put(cur + OFF_H + b * RG + tid, ep, u * (gt * sg));
             }
+            PK_MARK(l, 10);
         }
 
         // ================= P5: down + residual ======================================
@@ -769,10 +802,12 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             for (int j = 0; j < NH; j++) idx[j] = tid + j * kPT < F ? OFF_H + tid + j * kPT : -1;
             float hv[NH];
             ll_wait<NH>(cur, idx, hv, ep, dead, p.err, p.spin_limit);
+            PK_MARK(l, 11);
 #pragma unroll
             for (int j = 0; j < NH; j++)
                 if (tid + j * kPT < F) xin[tid + j * kPT] = hv[j];
             lds_barrier();
+            PK_MARK(l, 23);
             float a = 0.f;
 #pragma unroll
             for (int c = 0; c < NCd; c++) a = WR::dot(wd[c], &xin[col0 + c * CW + lane * WR::V], a);
@@ -788,6 +823,8 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 ll_put(cur + OFF_XA + r, ep, xn);
                 if (l + 1 == p.L) p.x[r] = xn;
             }
+            PK_MARK(l, 12);
+            if (kQkvAfterDown && l + 1 < p.L) load_wq(lay_s[l + 1].wqkv, wave, lane);
         }
     }
 
@@ -822,6 +859,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         for (int j = 0; j < NX; j++) idx[j] = tid + j * kPT < DIM ? OFF_XA + tid + j * kPT : -1;
         float xv[NX];
         ll_wait<NX>(p.ll + (size_t)((p.L - 1) & 1) * PAR_WORDS, idx, xv, base + (unsigned)p.L, dead, p.err, p.spin_limit);
+        PK_MARK(p.L - 1, 13);
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < NX; j++) {
@@ -867,6 +905,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         }
         if (lane == 63 && best) atomicMax(p.keys + ((b * kPW + wave) & (kArgmaxSlots - 1)), best);
     }
+    PK_MARK(p.L - 1, 14);
 
     // every block read the epoch base before block 0 could get here (block 0's last stage waited
     // for every block's last output), so the next launch's base can be published now
