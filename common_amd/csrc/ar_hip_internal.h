@@ -20,6 +20,10 @@
 void ar_set_error(const char* fmt, ...);
 // A notice on stderr when AR_HIP_LOG is set (no error state).
 void ar_log(const char* fmt, ...);
+// Debug pointer check (AR_HIP_CHECK_PTRS=1): [p, p + bytes) must lie inside the device allocation
+// holding p; null p or zero bytes pass.  A no-op returning AR_HIP_OK when the flag is off.
+bool ar_check_ptrs_enabled();
+int ar_check_range(const void* p, size_t bytes, const char* kernel, const char* what);
 void ar_clear_error();
 
 #define AR_CHECK_ARG(cond, ...)                  \

@@ -757,6 +757,32 @@ int launch_attention_decode(const AttnLaunch& a, hipStream_t stream) {
     AR_CHECK_ARG(a.batch >= 1 && a.batch <= 65535, "attention: bad batch %d", a.batch);
     AR_CHECK_ARG((reinterpret_cast<uintptr_t>(a.kcache) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.vcache) & 15) == 0,
                  "attention: caches must be 16-byte aligned");
+    if (ar_check_ptrs_enabled()) {  // extents of the attention and combine kernels
+        const char* k = "attention";
+        const size_t hd = a.head_dim, qd = (size_t)a.heads * hd, kvd = (size_t)a.kv_heads * hd, B1 = a.batch - 1;
+        const size_t elem = a.kv16 ? 2 : 4, cache = (size_t)a.batch * kvd * a.max_seq * elem;
+        if (a.qkv) {
+            AR_TRY(ar_check_range(a.qkv, (B1 * a.qkv_stride + qd + 2 * kvd) * 4, k, "q/k/v rows"));
+        } else {
+            AR_TRY(ar_check_range(a.q, (B1 * a.qkv_stride + qd) * 4, k, "q rows"));
+            AR_TRY(ar_check_range(a.k, (B1 * a.qkv_stride + kvd) * 4, k, "k rows"));
+            AR_TRY(ar_check_range(a.v, (B1 * a.qkv_stride + kvd) * 4, k, "v rows"));
+        }
+        AR_TRY(ar_check_range(a.q_norm, qd * 4, k, "q norm gain"));
+        AR_TRY(ar_check_range(a.k_norm, kvd * 4, k, "k norm gain"));
+        AR_TRY(ar_check_range(a.kcache, cache, k, "key cache"));
+        AR_TRY(ar_check_range(a.vcache, cache, k, "value cache"));
+        AR_TRY(ar_check_range(a.pos, 4, k, "position"));
+        AR_TRY(ar_check_range(a.rope_tab, (size_t)a.max_seq * (hd / 2) * sizeof(float2), k, "RoPE table"));
+        if (a.max_splits > 1) {
+            AR_TRY(ar_check_range(a.part_o, attention_partial_floats(a.batch, a.heads, a.max_splits, a.head_dim) * 4,
+                                  k, "split partials"));
+            AR_TRY(ar_check_range(a.part_ml, (size_t)a.batch * a.heads * a.max_splits * 2 * 4, k, "split maxima / sums"));
+        }
+        AR_TRY(ar_check_range(a.out, (B1 * a.out_stride + qd) * 4, k, "output"));
+        AR_TRY(ar_check_range(a.out_hi, (B1 * a.out_stride + qd) * 2, k, "output hi plane"));
+        AR_TRY(ar_check_range(a.out_lo, (B1 * a.out_stride + qd) * 2, k, "output lo plane"));
+    }
     if (a.head_dim == 128) return a.kv16 ? pick_g<128, true>(a, stream) : pick_g<128, false>(a, stream);
     if (a.head_dim == 64) return a.kv16 ? pick_g<64, true>(a, stream) : pick_g<64, false>(a, stream);
     ar_set_error("attention: head_dim %d not supported (64, 128)", a.head_dim);

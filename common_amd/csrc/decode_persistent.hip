@@ -999,6 +999,24 @@ int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t st) {
     AR_CHECK_ARG(a.vocab >= kPB, "persistent decode: vocabulary %d below %d rows", a.vocab, kPB);
     AR_CHECK_ARG(a.max_seq > 0, "persistent decode: empty cache");
     AR_CHECK_ARG(a.layer_count <= kMaxLayers, "persistent decode: %d layers exceed %d", a.layer_count, kMaxLayers);
+    if (ar_check_ptrs_enabled()) {
+        const char* k = "persistent decode";
+        const size_t wb = a.wdtype == AR_DTYPE_BF16 ? 2 : 4, D = a.dim, L = a.layer_count;
+        const size_t cache = L * a.kv_heads * (size_t)a.max_seq * a.head_dim * 4;
+        AR_TRY(ar_check_range(a.layers, L * decode_persistent_layer_bytes(), k, "layer table"));
+        AR_TRY(ar_check_range(a.x, D * 4, k, "residual row"));
+        AR_TRY(ar_check_range(a.kcache, cache, k, "key cache"));
+        AR_TRY(ar_check_range(a.vcache, cache, k, "value cache"));
+        AR_TRY(ar_check_range(a.rope_tab, (size_t)a.max_seq * (a.head_dim / 2) * sizeof(float2), k, "RoPE table"));
+        AR_TRY(ar_check_range(a.state, 4 * sizeof(int), k, "loop state"));
+        AR_TRY(ar_check_range(a.ll, decode_persistent_ll_words(a.wdtype, a.dim, a.hidden_dim, a.heads, a.kv_heads,
+                                                               a.head_dim) * 8, k, "exchange words"));
+        AR_TRY(ar_check_range(a.err, sizeof(int), k, "error flag"));
+        AR_TRY(ar_check_range(a.final_norm, D * 4, k, "final norm gain"));
+        AR_TRY(ar_check_range(a.lm_head, (size_t)a.vocab * D * wb, k, "head"));
+        AR_TRY(ar_check_range(a.logits, (size_t)a.vocab * 4, k, "logits"));
+        AR_TRY(ar_check_range(a.keys, (size_t)kArgmaxSlots * 8, k, "argmax keys"));
+    }
 #define AR_X(DT, TW, D, FF, HH, KK, HDD, SM)                                                                          \
     if (a.wdtype == DT && a.dim == D && a.hidden_dim == FF && a.heads == HH && a.kv_heads == KK && a.head_dim == HDD) \
         return launch_t<TW, D, FF, HH, KK, HDD, SM>(a, st);

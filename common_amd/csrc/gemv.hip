@@ -19,6 +19,24 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
     } else {
         AR_CHECK_ARG(a.y && a.y_stride >= a.rows, "GEMV: null output or short stride");
     }
+    if (ar_check_ptrs_enabled()) {  // extents the kernels read and write
+        const char* k = "GEMV";
+        const size_t wb = a.wdtype == AR_DTYPE_BF16 ? 2 : 4, R = a.rows, Cn = a.cols, B1 = a.batch - 1;
+        AR_TRY(ar_check_range(a.w, R * Cn * wb, k, "weights"));
+        AR_TRY(ar_check_range(a.w2, R * Cn * wb, k, "up weights"));
+        AR_TRY(ar_check_range(a.x, (B1 * a.x_stride + Cn) * 4, k, "input"));
+        AR_TRY(ar_check_range(a.norm_w, Cn * 4, k, "norm gain"));
+        AR_TRY(ar_check_range(a.bias, R * 4, k, "bias"));
+        AR_TRY(ar_check_range(a.y, (B1 * a.y_stride + R) * 4, k, "output"));
+        AR_TRY(ar_check_range(a.keys, (B1 + 1) * kArgmaxSlots * 8, k, "argmax keys"));
+        AR_TRY(ar_check_range(a.x_hi, (B1 * a.x_stride + Cn) * 2, k, "input hi plane"));
+        AR_TRY(ar_check_range(a.x_lo, (B1 * a.x_stride + Cn) * 2, k, "input lo plane"));
+        AR_TRY(ar_check_range(a.y_hi, (B1 * a.y_stride + R) * 2, k, "output hi plane"));
+        AR_TRY(ar_check_range(a.y_lo, (B1 * a.y_stride + R) * 2, k, "output lo plane"));
+        AR_TRY(ar_check_range(a.y_gain, R * 4, k, "output plane gain"));
+        AR_TRY(ar_check_range(a.kpart, (size_t)a.kpart_floats * 4, k, "k-split partials"));
+        AR_TRY(ar_check_range(a.kcount, (size_t)a.kcount_n * 4, k, "k-split counters"));
+    }
     gemv::Params p;
     p.w = a.w; p.w2 = a.w2; p.rows = a.rows; p.cols = a.cols; p.batch = a.batch;
     p.x = a.x; p.x_stride = a.x_stride; p.norm_w = a.norm_w; p.eps = a.eps; p.bias = a.bias;

@@ -165,6 +165,18 @@ int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* to
     AR_CHECK_ARG(table && tokens && keys && state && x && dim > 0, "step begin: bad arguments");
     AR_CHECK_ARG(!x_hi == !x_lo, "step begin: operand planes come in hi/lo pairs");
     AR_CHECK_ARG(batch >= 1 && batch <= 8, "step begin: batch %d outside 1..8", batch);
+    if (ar_check_ptrs_enabled()) {
+        const char* k = "step begin";
+        const size_t wb = wdtype == AR_DTYPE_BF16 ? 2 : 4, B1 = batch - 1;
+        AR_TRY(ar_check_range(table, (size_t)vocab * dim * wb, k, "embedding table"));
+        AR_TRY(ar_check_range(tokens, (size_t)batch * token_stride * 4, k, "token rows"));
+        AR_TRY(ar_check_range(keys, (size_t)batch * kArgmaxSlots * 8, k, "argmax keys"));
+        AR_TRY(ar_check_range(state, 3 * sizeof(int), k, "loop state"));
+        AR_TRY(ar_check_range(x, (B1 * x_stride + dim) * 4, k, "residual rows"));
+        AR_TRY(ar_check_range(x_hi, (B1 * x_stride + dim) * 2, k, "hi plane"));
+        AR_TRY(ar_check_range(x_lo, (B1 * x_stride + dim) * 2, k, "lo plane"));
+        AR_TRY(ar_check_range(x_gain, (size_t)dim * 4, k, "plane gain"));
+    }
     if (wdtype == AR_DTYPE_BF16)
         hipLaunchKernelGGL(step_begin_kernel<uint16_t>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)table, dim,
                            vocab, tokens, token_stride, keys, state, batch, x, x_stride, x_hi, x_lo, x_gain);

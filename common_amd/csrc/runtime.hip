@@ -50,6 +50,46 @@ void ar_log(const char* fmt, ...) {
 
 void ar_clear_error() { g_last_error[0] = '\0'; }
 
+// AR_HIP_CHECK_PTRS=1 (read once): before the launches of the decode path, every device pointer
+// argument is checked, with the extent its kernel reads or writes, against the HIP allocation that
+// holds it (hipMemGetAddressRange); a pointer outside any allocation, or an extent past the end of
+// its allocation, refuses the launch with AR_HIP_ERR_INVALID.  A debugging aid, off by default.
+namespace {
+std::atomic<unsigned long long> g_ptr_checks{0};
+}
+
+bool ar_check_ptrs_enabled() {
+    static const bool on = [] {
+        const char* v = getenv("AR_HIP_CHECK_PTRS");
+        return v && *v && strcmp(v, "0") != 0 && strcmp(v, "false") != 0;
+    }();
+    return on;
+}
+
+int ar_check_range(const void* p, size_t bytes, const char* kernel, const char* what) {
+    if (!ar_check_ptrs_enabled() || !p || !bytes) return AR_HIP_OK;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    const hipError_t e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
+    g_ptr_checks.fetch_add(1, std::memory_order_relaxed);
+    if (e != hipSuccess || !base) {
+        ar_set_error("%s: %s %p is not inside a device allocation (%s)", kernel, what, p, hipGetErrorString(e));
+        return AR_HIP_ERR_INVALID;
+    }
+    const uintptr_t b = reinterpret_cast<uintptr_t>(base), a = reinterpret_cast<uintptr_t>(p);
+    if (a < b || a + bytes > b + size) {
+        ar_set_error("%s: %s [%p, +%zu) leaves its allocation [%p, +%zu)", kernel, what, p, bytes, base, size);
+        return AR_HIP_ERR_INVALID;
+    }
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_pointer_checks(unsigned long long* checked) {
+    AR_CHECK_ARG(checked, "null argument");
+    *checked = ar_check_ptrs_enabled() ? g_ptr_checks.load(std::memory_order_relaxed) : 0ull;
+    return AR_HIP_OK;
+}
+
 extern "C" const char* ar_hip_last_error(void) { return g_last_error; }
 
 extern "C" const char* ar_hip_version(void) { return "ar-hip 0.1 gfx950"; }

@@ -93,6 +93,7 @@ _SIGS = {
     "ar_hip_qwen3_persistent": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_persistent_recomputed": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_persistent_wait_limit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint]),
+    "ar_hip_pointer_checks": (ctypes.c_int, [ctypes.POINTER(ctypes.c_ulonglong)]),
     "ar_hip_qwen3_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "ar_hip_qwen3_prefill_by_steps": (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
     "ar_hip_gemm_bf16": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4),

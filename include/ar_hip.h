@@ -304,6 +304,15 @@ int ar_hip_qwen3_persistent_recomputed(ar_qwen3 *m, int *steps);
  * device. */
 int ar_hip_qwen3_persistent_wait_limit(ar_qwen3 *m, unsigned polls);
 
+/* Debug pointer check.  With AR_HIP_CHECK_PTRS=1 in the environment (read once per process), the
+ * decode-path launches (step begin, GEMVs, attention + split combine, persistent decode step) first
+ * check every device pointer argument, with the extent its kernel reads or writes, against the HIP
+ * allocation holding it (hipMemGetAddressRange), and refuse the launch with AR_HIP_ERR_INVALID when
+ * a range leaves its allocation.  *checked receives the number of ranges checked so far in the
+ * process (0 while the flag is off).  No counterpart in the reference (its generated C has no
+ * error channel); a diagnostic only. */
+int ar_hip_pointer_checks(unsigned long long *checked);
+
 #ifdef __cplusplus
 }
 #endif
