@@ -263,7 +263,8 @@ def c2_section(args):
     return {"workload": "C2: decode-step GQA attention op, 16Q/8KV heads, hd 128, cache 0..4095 + new row at 4096, fp32",
             "us_per_call": round(us, 2), "kv_bytes": kv_bytes, "GBs": round(gbs, 1),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "note": "wall time per C-ABI call, including the op's q/k/v staging copies and position upload"}
+            "note": "wall time per C-ABI call (host-side argument checks, one attention launch and its split "
+                    "combine launch, no copies)"}
 
 
 TRAFFIC_STEPS = 8
