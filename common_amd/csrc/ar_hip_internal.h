@@ -157,7 +157,23 @@ struct GemvLaunch {
     int kpart_floats = 0;
     unsigned* kcount = nullptr;
     int kcount_n = 0;
+    // fragment-ordered copies of w / w2 (launch_frag_copy; batch <= 8, rows % 16 == 0, store / residual /
+    // SwiGLU epilogue, operand planes given): the GEMV reads these instead, over an even split of the
+    // fragments (gemv_frag.hip), with kpart / kcount (gemv_frag_part_floats, one counter per 16-row tile)
+    // as the workspace of tiles shared by wavefronts.  ss_in [cols/16][16]: per-16-row sums of squares
+    // of x, published by x's producer (needed with norm_w); ss_out [rows/16][16]: the same of the
+    // residual epilogue's output, or null
+    const uint16_t* w_frag = nullptr;
+    const uint16_t* w2_frag = nullptr;
+    const float* ss_in = nullptr;
+    float* ss_out = nullptr;
 };
+
+// fragment order of a bf16 matrix for the GEMV above: 16 x 32 blocks, each 64 lanes x 8 values
+size_t gemv_frag_elems(int rows, int cols);
+size_t gemv_frag_part_floats(int rows, int cus, int nmat);
+bool gemv_frag_fits(int rows, int cols, int batch, int cus);
+int launch_frag_copy(const uint16_t* w, uint16_t* out, int rows, int cols, hipStream_t st);
 
 // Splits v into bf16 operand planes: hi = bf16(v) (round to nearest even), lo = bf16(v - hi), so
 // hi + lo keeps 16 significant bits of v.
@@ -423,11 +439,13 @@ int attention_max_splits(int max_seq, int kv_heads, int batch, bool kv16);
 // position}.  Position p = next: the token fed is the prompt token tokens[b][p] while p is inside
 // the prompt, else the greedy choice decoded from keys[b] (the previous step's logits), which is
 // also stored at tokens[b][p]; keys are then cleared, x[b] = E[token], current = p, next = p+1.
-// x_hi / x_lo (optional): bf16 planes of x_gain * x (bf16_planes) for the first GEMV's MFMA path.
+// x_hi / x_lo (optional): bf16 planes of x_gain * x (bf16_planes) for the first GEMV's MFMA path;
+// ss_out (optional, [dim/16][16]): sums of squares of each 16 consecutive entries of x[b] (column b),
+// for the fragment-ordered GEMV's RMSNorm.
 // AutoregressiveModel.next + the embedding copy (engine/ml/.../AutoregressiveModel.java:295-308,430).
 int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* tokens, int token_stride,
                       unsigned long long* keys, int* state, int batch, float* x, int x_stride,
-                      uint16_t* x_hi, uint16_t* x_lo, const float* x_gain, hipStream_t stream);
+                      uint16_t* x_hi, uint16_t* x_lo, const float* x_gain, float* ss_out, hipStream_t stream);
 int launch_rmsnorm(const float* x, const float* w, float* y, int rows, int n, float eps,
                    hipStream_t stream);
 int launch_rope(float* x, int heads, int hd, int pos, double theta, int rows, int row_stride,

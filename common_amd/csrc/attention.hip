@@ -34,7 +34,8 @@
 namespace {
 
 constexpr int kThreads = 256;   // threads of the split (multi-block) form
-constexpr int kMaxTile = 256;   // rows per split in that form (fp32 cache)
+constexpr int kMaxTile = 348;   // rows per split in that form (fp32 cache; C5, 8 x 8 KV heads x 8256
+                                // rows: 24 splits of 344 rows 106.8 us/layer vs 33 of 251 rows 110.6)
 constexpr int kMaxTile16 = 1040; // fp16 cache: the per-row work (fp16 -> fp32 conversions) makes
                                  // longer splits pay (C5, 8 x 8 KV heads x 8256 rows: 8 splits of
                                  // 1032 rows 5.55 ms/step vs 33 of 251 rows 6.32)
@@ -99,9 +100,10 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(AttnParams p) {
     constexpr int NGR = NT / 16;     // 16-lane row groups
     constexpr int NWV = NT / 64;     // wavefronts
     // rows per group per chunk: RU0, chosen from the longest split (a chunk of NGR * RU rows covers
-    // it; 16-row splits take one row per group, no clamped duplicate loads); at most 2 for G >= 8
-    // (registers: G query fragments)
-    constexpr int RU = (G >= 8 && RU0 > 2) ? 2 : RU0;
+    // it; 16-row splits take one row per group, no clamped duplicate loads); at most 2 for G >= 8,
+    // and for G >= 4 with fp32 rows (registers: G query fragments; the G = 4 fp32 instance holds 192
+    // VGPRs at RU 4, two wavefronts per SIMD, and 136 at RU 2, three)
+    constexpr int RU = ((G >= 8 || (G >= 4 && !KV16)) && RU0 > 2) ? 2 : RU0;
     __shared__ __attribute__((aligned(16))) float q_s[G][HD];
     __shared__ __attribute__((aligned(16))) float k_new[HD];
     __shared__ __attribute__((aligned(16))) float v_new[HD];

@@ -36,6 +36,10 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
         AR_TRY(ar_check_range(a.y_gain, R * 4, k, "output plane gain"));
         AR_TRY(ar_check_range(a.kpart, (size_t)a.kpart_floats * 4, k, "k-split partials"));
         AR_TRY(ar_check_range(a.kcount, (size_t)a.kcount_n * 4, k, "k-split counters"));
+        AR_TRY(ar_check_range(a.w_frag, gemv_frag_elems(a.rows, a.cols) * 2, k, "fragment-ordered weights"));
+        AR_TRY(ar_check_range(a.w2_frag, gemv_frag_elems(a.rows, a.cols) * 2, k, "fragment-ordered up weights"));
+        AR_TRY(ar_check_range(a.ss_in, (size_t)((Cn + 15) / 16) * 16 * 4, k, "input sums of squares"));
+        AR_TRY(ar_check_range(a.ss_out, (size_t)((R + 15) / 16) * 16 * 4, k, "output sums of squares"));
     }
     gemv::Params p;
     p.w = a.w; p.w2 = a.w2; p.rows = a.rows; p.cols = a.cols; p.batch = a.batch;
@@ -43,11 +47,17 @@ int launch_gemv(const GemvLaunch& a, hipStream_t stream) {
     p.y = a.y; p.y_stride = a.y_stride; p.keys = a.keys;
     p.x_hi = a.x_hi; p.x_lo = a.x_lo; p.y_hi = a.y_hi; p.y_lo = a.y_lo; p.y_gain = a.y_gain;
     p.kpart = a.kpart; p.kpart_floats = a.kpart_floats; p.kcount = a.kcount; p.kcount_n = a.kcount_n;
+    p.wf = a.w_frag; p.wf2 = a.w2_frag; p.ss_in = a.ss_in; p.ss_out = a.ss_out;
     AR_CHECK_ARG(!a.kpart == !a.kcount, "GEMV: k-split workspace needs both partials and counters");
     const bool mfma = a.batch >= 3 && a.wdtype == AR_DTYPE_BF16 && a.cols % 32 == 0;
     AR_CHECK_ARG(mfma || (!a.x_hi && !a.y_hi), "GEMV: operand planes need the MFMA path (batch >= 3, bf16, cols %% 32)");
     AR_CHECK_ARG(!a.x_hi == !a.x_lo && !a.y_hi == !a.y_lo, "GEMV: operand planes come in hi/lo pairs");
     AR_CHECK_ARG(!a.y_hi || a.epilogue != GEMV_EPI_ARGMAX, "GEMV: no output planes for the argmax epilogue");
+    if (a.w_frag) {
+        AR_CHECK_ARG(a.wdtype == AR_DTYPE_BF16, "GEMV: fragment-ordered weights are bf16");
+        return gemv_launch_frag(p, a.epilogue, stream);
+    }
+    AR_CHECK_ARG(!a.ss_in && !a.ss_out, "GEMV: per-tile sums of squares need the fragment-ordered form");
     if (mfma) return gemv_launch_mfma(p, a.epilogue, stream);
     if (a.batch >= 3) return gemv_launch_batched(p, a.wdtype, a.epilogue, stream);
     if (a.epilogue == GEMV_EPI_ARGMAX && gemv_argmax_fits(a.cols, a.batch, a.wdtype) && a.x_stride % 4 == 0)

@@ -49,6 +49,10 @@ struct Params {
     int kpart_floats;
     unsigned* kcount;
     int kcount_n;
+    const uint16_t* wf;        // fragment-ordered copies of w / w2 (GemvLaunch), or null
+    const uint16_t* wf2;
+    const float* ss_in;        // per-16-row sums of squares of x / of the residual output (GemvLaunch)
+    float* ss_out;
 };
 
 template <typename WT>
@@ -487,3 +491,5 @@ bool gemv_argmax_fits(int cols, int batch, int wdtype);
 int gemv_launch_argmax(const gemv::Params& p, int wdtype, hipStream_t st);
 // bf16 weights, batches of 3..16, cols % 32 == 0 (gemv_mfma.hip): 16-row tiles on the MFMA units.
 int gemv_launch_mfma(const gemv::Params& p, int epi, hipStream_t st);
+// Fragment-ordered bf16 weights, batches of 1..8, store / residual / SwiGLU (gemv_frag.hip).
+int gemv_launch_frag(const gemv::Params& p, int epi, hipStream_t st);

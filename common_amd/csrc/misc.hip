@@ -21,7 +21,7 @@ template <typename WT>
 __global__ __launch_bounds__(1024) void step_begin_kernel(const WT* table, int dim, int vocab, int* tokens,
                                                          int token_stride, unsigned long long* keys, int* state,
                                                          int batch, float* x, int x_stride, uint16_t* x_hi,
-                                                         uint16_t* x_lo, const float* x_gain) {
+                                                         uint16_t* x_lo, const float* x_gain, float* ss_out) {
     __shared__ int tok_s[8];
     __shared__ unsigned long long red[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -54,12 +54,24 @@ __global__ __launch_bounds__(1024) void step_begin_kernel(const WT* table, int d
     for (int i = tid; i < batch * kArgmaxSlots; i += blockDim.x) keys[i] = 0ull;
     for (int b = 0; b < batch; b++) {
         const WT* row = table + (size_t)tok_s[b] * dim;
-        for (int i = tid; i < dim; i += blockDim.x) {
-            float v;
-            if constexpr (sizeof(WT) == 2) v = __uint_as_float((unsigned)row[i] << 16);
-            else v = row[i];
-            x[(size_t)b * x_stride + i] = v;
-            if (x_hi) bf16_planes(x_gain ? v * x_gain[i] : v, x_hi + (size_t)b * x_stride + i, x_lo + (size_t)b * x_stride + i);
+        // every lane takes part in each pass (16-lane groups hold 16 consecutive entries: the
+        // per-16-row sums of squares for the fragment-ordered GEMVs' RMSNorm)
+        for (int i0 = 0; i0 < dim; i0 += blockDim.x) {
+            const int i = i0 + tid;
+            float v = 0.f;
+            if (i < dim) {
+                if constexpr (sizeof(WT) == 2) v = __uint_as_float((unsigned)row[i] << 16);
+                else v = row[i];
+                x[(size_t)b * x_stride + i] = v;
+                if (x_hi)
+                    bf16_planes(x_gain ? v * x_gain[i] : v, x_hi + (size_t)b * x_stride + i, x_lo + (size_t)b * x_stride + i);
+            }
+            if (ss_out) {
+                float s2 = v * v;
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) s2 += __shfl_xor(s2, off, 64);
+                if ((tid & 15) == 0 && i < dim) ss_out[(size_t)(i / 16) * 16 + b] = s2;
+            }
         }
     }
     if (tid == 0) {
@@ -161,8 +173,9 @@ int grid_for(size_t n, int threads, int cap = 4096) {
 
 int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* tokens, int token_stride,
                       unsigned long long* keys, int* state, int batch, float* x, int x_stride, uint16_t* x_hi,
-                      uint16_t* x_lo, const float* x_gain, hipStream_t stream) {
+                      uint16_t* x_lo, const float* x_gain, float* ss_out, hipStream_t stream) {
     AR_CHECK_ARG(table && tokens && keys && state && x && dim > 0, "step begin: bad arguments");
+    AR_CHECK_ARG(!ss_out || dim % 16 == 0, "step begin: sums of squares need dim %% 16 == 0");
     AR_CHECK_ARG(!x_hi == !x_lo, "step begin: operand planes come in hi/lo pairs");
     AR_CHECK_ARG(batch >= 1 && batch <= 8, "step begin: batch %d outside 1..8", batch);
     if (ar_check_ptrs_enabled()) {
@@ -176,13 +189,14 @@ int launch_step_begin(const void* table, int wdtype, int dim, int vocab, int* to
         AR_TRY(ar_check_range(x_hi, (B1 * x_stride + dim) * 2, k, "hi plane"));
         AR_TRY(ar_check_range(x_lo, (B1 * x_stride + dim) * 2, k, "lo plane"));
         AR_TRY(ar_check_range(x_gain, (size_t)dim * 4, k, "plane gain"));
+        AR_TRY(ar_check_range(ss_out, (size_t)(dim / 16) * 16 * 4, k, "sums of squares"));
     }
     if (wdtype == AR_DTYPE_BF16)
         hipLaunchKernelGGL(step_begin_kernel<uint16_t>, dim3(1), dim3(1024), 0, stream, (const uint16_t*)table, dim,
-                           vocab, tokens, token_stride, keys, state, batch, x, x_stride, x_hi, x_lo, x_gain);
+                           vocab, tokens, token_stride, keys, state, batch, x, x_stride, x_hi, x_lo, x_gain, ss_out);
     else
         hipLaunchKernelGGL(step_begin_kernel<float>, dim3(1), dim3(1024), 0, stream, (const float*)table, dim, vocab,
-                           tokens, token_stride, keys, state, batch, x, x_stride, x_hi, x_lo, x_gain);
+                           tokens, token_stride, keys, state, batch, x, x_stride, x_hi, x_lo, x_gain, ss_out);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

@@ -40,6 +40,12 @@ struct Layer {
     float* q_norm = nullptr;
     float* k_norm = nullptr;
     float* bqkv = nullptr;
+    // fragment-ordered copies of wqkv, wo, w1, w3, w2 for the batched decode GEMVs (gemv_frag.hip)
+    uint16_t* fqkv = nullptr;
+    uint16_t* fo = nullptr;
+    uint16_t* f1 = nullptr;
+    uint16_t* f3 = nullptr;
+    uint16_t* f2 = nullptr;
 };
 
 }  // namespace
@@ -80,6 +86,14 @@ struct ar_qwen3 {
     float* gv_part = nullptr;
     int gv_part_floats = 0;
     unsigned* gv_count = nullptr;
+    int gv_count_n = 0;
+    // batches of 3..8 with bf16 weights: the layers' projections also in MFMA fragment order (one
+    // buffer, made at finalize), read by the QKV / O / gate-up / down GEMVs of the decode step
+    // unless switched off (ar_hip_qwen3_use_fragment_gemv); gv_ss [dim/16][16]: per-16-row sums of
+    // squares of the residual stream, published by its producers for the RMSNorm of the next GEMV
+    uint16_t* gv_frag = nullptr;
+    float* gv_ss = nullptr;
+    bool frag_on = true;
     unsigned long long* am_keys = nullptr;  // [B][kArgmaxSlots] greedy-token keys
     // token selection: greedy unless a sampling temperature is set (AR_SAMPLE_*); one
     // java.util.Random state per sequence, the sampler's workspace allocated on first use
@@ -161,7 +175,8 @@ void release(ar_qwen3* m) {
         hipEventDestroy(e.second);
     }
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->kcache, m->vcache, m->part_o,
-                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->am_keys, m->smp_rng,
+                    m->part_ml, m->pl_x, m->pl_attn, m->pl_act, m->gv_part, m->gv_count, m->gv_frag, m->gv_ss,
+                    m->am_keys, m->smp_rng,
                     m->smp_rng_saved, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16,
                     m->pf_flag, m->pk_layers, m->pk_err};
@@ -223,6 +238,21 @@ StepPlanes step_planes(const ar_qwen3* m) {
     return pl;
 }
 
+// The batched decode GEMVs read the fragment-ordered weight copies (gemv_frag.hip).
+bool frag_active(const ar_qwen3* m) { return m->gv_frag != nullptr && m->frag_on; }
+
+// Points a QKV / O / gate-up / down launch at the fragment-ordered copies and the shared workspace.
+void use_frag(const ar_qwen3* m, GemvLaunch& g, const uint16_t* w, const uint16_t* w2, bool norm_in, bool ss_out) {
+    g.w_frag = w;
+    g.w2_frag = w2;
+    g.ss_in = norm_in ? m->gv_ss : nullptr;
+    g.ss_out = ss_out ? m->gv_ss : nullptr;
+    g.kpart = m->gv_part;
+    g.kpart_floats = m->gv_part_floats;
+    g.kcount = m->gv_count;
+    g.kcount_n = m->gv_count_n;
+}
+
 // One kernel class (AR_KT_*) of the decode step for layer l (the logits class ignores l), launched
 // exactly as the step launches it.
 int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store_logits) {
@@ -237,6 +267,7 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
             g.w = L.wqkv; g.rows = m->qkv_dim; g.cols = dim; g.x = m->x; g.x_stride = dim; g.norm_w = L.attn_norm;
             g.bias = L.bqkv; g.y = m->qkv; g.y_stride = m->qkv_dim; g.epilogue = GEMV_EPI_STORE;
             g.x_hi = pl.xh; g.x_lo = pl.xl;
+            if (frag_active(m)) use_frag(m, g, L.fqkv, nullptr, true, false);
             return launch_gemv(g, st);
         }
         case AR_KT_ATTENTION: {
@@ -262,6 +293,7 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
             o.x_hi = pl.ah; o.x_lo = pl.al; o.y_hi = pl.xh; o.y_lo = pl.xl; o.y_gain = L.ffn_norm;
             o.kpart = m->gv_part; o.kpart_floats = m->gv_part_floats; o.kcount = m->gv_count;
             o.kcount_n = m->gv_count ? (dim + 15) / 16 : 0;
+            if (frag_active(m)) use_frag(m, o, L.fo, nullptr, false, true);
             return launch_gemv(o, st);
         }
         case AR_KT_GATE_UP: {  // gate/up with the pre-FFN RMSNorm and SwiGLU fused (FeedForwardFeatures.java:147-155)
@@ -271,6 +303,7 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
             u.cols = dim; u.x = m->x; u.x_stride = dim; u.norm_w = L.ffn_norm; u.y = m->act; u.y_stride = F;
             u.epilogue = GEMV_EPI_SWIGLU;
             u.x_hi = pl.xh; u.x_lo = pl.xl; u.y_hi = pl.hh; u.y_lo = pl.hl;
+            if (frag_active(m)) use_frag(m, u, L.f1, L.f3, true, false);
             return launch_gemv(u, st);
         }
         case AR_KT_DOWN: {  // down projection + residual (FeedForwardFeatures.java:156; AttentionFeatures.java:1705)
@@ -282,6 +315,7 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
             d.y_gain = l + 1 < c.layer_count ? m->layers[l + 1].attn_norm : m->final_norm;
             d.kpart = m->gv_part; d.kpart_floats = m->gv_part_floats; d.kcount = m->gv_count;
             d.kcount_n = m->gv_count ? (dim + 15) / 16 : 0;
+            if (frag_active(m)) use_frag(m, d, L.f2, nullptr, false, true);
             return launch_gemv(d, st);
         }
         case AR_KT_LOGITS: {  // final RMSNorm + tied logits + greedy token (Qwen3.java:401-405)
@@ -343,7 +377,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     if (persistent_active(m)) {
         const StepPlanes pl = step_planes(m);
         AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys,
-                                 m->state, B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, st));
+                                 m->state, B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, nullptr, st));
         DecodePersistentLaunch d;
         d.layers = m->pk_layers; d.layer_count = c.layer_count; d.wdtype = c.weight_dtype; d.dim = dim;
         d.hidden_dim = c.hidden_dim;
@@ -370,7 +404,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     }
     const StepPlanes pl = step_planes(m);
     AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys, m->state,
-                             B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, st));
+                             B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, frag_active(m) ? m->gv_ss : nullptr,
+                             st));
     for (int l = 0; l < c.layer_count; l++) {
         for (int which : {AR_KT_QKV, AR_KT_ATTENTION, AR_KT_O, AR_KT_GATE_UP, AR_KT_DOWN}) AR_TRY(timed_class(which, l));
     }
@@ -558,9 +593,33 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
         ALLOC(pl_x, (size_t)2 * B * d * 2);
         ALLOC(pl_attn, (size_t)2 * B * m->q_dim * 2);
         ALLOC(pl_act, (size_t)2 * B * F * 2);
-        m->gv_part_floats = ((d + 15) / 16) * 4 * 256;  // up to 4 k-slices of every tile
-        ALLOC(gv_part, (size_t)m->gv_part_floats * 4);
-        ALLOC(gv_count, (size_t)((d + 15) / 16) * 4);
+        size_t part = (size_t)((d + 15) / 16) * 4 * 256;  // up to 4 k-slices of every tile
+        int counters = (d + 15) / 16;
+        const int cus = ar_device_cus(m->ctx->stream);
+        const bool frag = B <= 8 && gemv_frag_fits(m->qkv_dim, d, (int)B, cus) && gemv_frag_fits(d, m->q_dim, (int)B, cus) &&
+                          gemv_frag_fits(F, d, (int)B, cus) && gemv_frag_fits(d, F, (int)B, cus) && d % 16 == 0;
+        if (frag) {
+            const size_t per_layer = gemv_frag_elems(m->qkv_dim, d) + gemv_frag_elems(d, m->q_dim) +
+                                     2 * gemv_frag_elems(F, d) + gemv_frag_elems(d, F);
+            ALLOC(gv_frag, per_layer * c.layer_count * 2);
+            ALLOC(gv_ss, (size_t)(d / 16) * 16 * 4);
+            part = std::max({part, gemv_frag_part_floats(m->qkv_dim, cus, 1), gemv_frag_part_floats(d, cus, 1),
+                             gemv_frag_part_floats(F, cus, 2)});
+            counters = std::max({counters, m->qkv_dim / 16, (int)(F / 16)});
+            uint16_t* f = m->gv_frag;
+            for (int l = 0; l < c.layer_count; l++) {
+                Layer& L = m->layers[l];
+                L.fqkv = f; f += gemv_frag_elems(m->qkv_dim, d);
+                L.fo = f; f += gemv_frag_elems(d, m->q_dim);
+                L.f1 = f; f += gemv_frag_elems(F, d);
+                L.f3 = f; f += gemv_frag_elems(F, d);
+                L.f2 = f; f += gemv_frag_elems(d, F);
+            }
+        }
+        m->gv_part_floats = (int)part;
+        m->gv_count_n = counters;
+        ALLOC(gv_part, part * 4);
+        ALLOC(gv_count, (size_t)counters * 4);
     }
     ALLOC(am_keys, B * kArgmaxSlots * 8);
     ALLOC(smp_rng, B * 8);
@@ -768,6 +827,19 @@ extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
     }
     AR_TRY(invalidate_graphs(m));
     AR_TRY(setup_persistent(m));
+    if (m->gv_frag) {  // fragment-ordered copies of the layers' projections
+        const ar_qwen3_cfg& c = m->cfg;
+        const int d = c.dim, F = c.hidden_dim;
+        hipStream_t st = m->ctx->stream;
+        for (const Layer& L : m->layers) {
+            AR_TRY(launch_frag_copy((const uint16_t*)L.wqkv, L.fqkv, m->qkv_dim, d, st));
+            AR_TRY(launch_frag_copy((const uint16_t*)L.wo, L.fo, d, m->q_dim, st));
+            AR_TRY(launch_frag_copy((const uint16_t*)L.w1, L.f1, F, d, st));
+            AR_TRY(launch_frag_copy((const uint16_t*)L.w3, L.f3, F, d, st));
+            AR_TRY(launch_frag_copy((const uint16_t*)L.w2, L.f2, d, F, st));
+        }
+        AR_HIP_TRY(hipStreamSynchronize(st));
+    }
     m->finalized = true;
     return ar_hip_qwen3_reset(m);
 }
@@ -1022,6 +1094,20 @@ extern "C" int ar_hip_qwen3_set_sampling(ar_qwen3* m, int mode, double temperatu
     m->smp_mode = mode;
     m->smp_temperature = temperature;
     m->smp_top_p = top_p;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_use_fragment_gemv(ar_qwen3* m, int enable) {
+    AR_CHECK_ARG(m, "null model");
+    AR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    if (m->frag_on != (enable != 0)) AR_TRY(invalidate_graphs(m));  // the captured step holds either form
+    m->frag_on = enable != 0;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_fragment_gemv(ar_qwen3* m, int* active) {
+    AR_CHECK_ARG(m && active, "null argument");
+    *active = frag_active(m) ? 1 : 0;
     return AR_HIP_OK;
 }
 

@@ -89,6 +89,8 @@ _SIGS = {
     "ar_hip_qwen3_kernel_time": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), _c_int_p]),
     "ar_hip_qwen3_kernel_loop": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "ar_hip_qwen3_use_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "ar_hip_qwen3_use_fragment_gemv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "ar_hip_qwen3_fragment_gemv": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_use_persistent": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_persistent": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_persistent_recomputed": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),

@@ -107,6 +107,19 @@ class AutoregressiveModel:
     def use_graph(self, enable: bool):
         hw.check(hw.lib().ar_hip_qwen3_use_graph(self.handle, int(enable)))
 
+    def use_fragment_gemv(self, enable: bool):
+        """Batches of 3..8 with bf16 weights: the decode step's QKV, O, gate/up and down GEMVs read
+        copies of those matrices in MFMA fragment order made at finalize (default on), split evenly
+        over every wavefront, or (False) the row-major weights."""
+        hw.check(hw.lib().ar_hip_qwen3_use_fragment_gemv(self.handle, int(enable)))
+
+    @property
+    def fragment_gemv(self) -> bool:
+        """Whether the decode steps use the fragment-ordered GEMVs."""
+        a = ctypes.c_int()
+        hw.check(hw.lib().ar_hip_qwen3_fragment_gemv(self.handle, ctypes.byref(a)))
+        return bool(a.value)
+
     def use_persistent(self, enable: bool):
         """Run the layers of each decode step as one persistent launch when the model qualifies
         (default on) or as separate launches.  It qualifies at batch 1 with an fp32 KV cache on the
