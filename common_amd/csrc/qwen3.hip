@@ -40,8 +40,7 @@ struct Layer {
     float* q_norm = nullptr;
     float* k_norm = nullptr;
     float* bqkv = nullptr;
-    // fragment-ordered copies of wqkv, wo, w1, w3, w2 for the batched decode GEMVs (gemv_frag.hip)
-    uint16_t* fqkv = nullptr;
+    // fragment-ordered copies of wo, w1, w3, w2 for the batched decode GEMVs (gemv_frag.hip)
     uint16_t* fo = nullptr;
     uint16_t* f1 = nullptr;
     uint16_t* f3 = nullptr;
@@ -87,10 +86,10 @@ struct ar_qwen3 {
     int gv_part_floats = 0;
     unsigned* gv_count = nullptr;
     int gv_count_n = 0;
-    // batches of 3..8 with bf16 weights: the layers' projections also in MFMA fragment order (one
-    // buffer, made at finalize), read by the QKV / O / gate-up / down GEMVs of the decode step
-    // unless switched off (ar_hip_qwen3_use_fragment_gemv); gv_ss [dim/16][16]: per-16-row sums of
-    // squares of the residual stream, published by its producers for the RMSNorm of the next GEMV
+    // batches of 3..8 with bf16 weights: the layers' O, gate/up and down matrices also in MFMA
+    // fragment order (one buffer, made at finalize), read by those GEMVs of the decode step unless
+    // switched off (ar_hip_qwen3_use_fragment_gemv); gv_ss [dim/16][16]: per-16-row sums of squares
+    // of the residual stream after the O projection, published by it for the gate/up RMSNorm
     uint16_t* gv_frag = nullptr;
     float* gv_ss = nullptr;
     bool frag_on = true;
@@ -241,7 +240,7 @@ StepPlanes step_planes(const ar_qwen3* m) {
 // The batched decode GEMVs read the fragment-ordered weight copies (gemv_frag.hip).
 bool frag_active(const ar_qwen3* m) { return m->gv_frag != nullptr && m->frag_on; }
 
-// Points a QKV / O / gate-up / down launch at the fragment-ordered copies and the shared workspace.
+// Points an O / gate-up / down launch at the fragment-ordered copies and the shared workspace.
 void use_frag(const ar_qwen3* m, GemvLaunch& g, const uint16_t* w, const uint16_t* w2, bool norm_in, bool ss_out) {
     g.w_frag = w;
     g.w2_frag = w2;
@@ -267,7 +266,8 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
             g.w = L.wqkv; g.rows = m->qkv_dim; g.cols = dim; g.x = m->x; g.x_stride = dim; g.norm_w = L.attn_norm;
             g.bias = L.bqkv; g.y = m->qkv; g.y_stride = m->qkv_dim; g.epilogue = GEMV_EPI_STORE;
             g.x_hi = pl.xh; g.x_lo = pl.xl;
-            if (frag_active(m)) use_frag(m, g, L.fqkv, nullptr, true, false);
+            // (QKV stays on the row-major MFMA GEMV: its planes-in-registers persistent form measured
+            // 16.2 us per C5 layer in the step against 17.8 for the fragment-ordered form)
             return launch_gemv(g, st);
         }
         case AR_KT_ATTENTION: {
@@ -315,7 +315,7 @@ int launch_class(ar_qwen3* m, int which, int l, const StepPlanes& pl, bool store
             d.y_gain = l + 1 < c.layer_count ? m->layers[l + 1].attn_norm : m->final_norm;
             d.kpart = m->gv_part; d.kpart_floats = m->gv_part_floats; d.kcount = m->gv_count;
             d.kcount_n = m->gv_count ? (dim + 15) / 16 : 0;
-            if (frag_active(m)) use_frag(m, d, L.f2, nullptr, false, true);
+            if (frag_active(m)) use_frag(m, d, L.f2, nullptr, false, false);
             return launch_gemv(d, st);
         }
         case AR_KT_LOGITS: {  // final RMSNorm + tied logits + greedy token (Qwen3.java:401-405)
@@ -404,8 +404,7 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
     }
     const StepPlanes pl = step_planes(m);
     AR_TRY(launch_step_begin(m->embed, c.weight_dtype, dim, c.vocab_size, m->tokens, m->S + 1, m->am_keys, m->state,
-                             B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, frag_active(m) ? m->gv_ss : nullptr,
-                             st));
+                             B, m->x, dim, pl.xh, pl.xl, m->layers[0].attn_norm, nullptr, st));
     for (int l = 0; l < c.layer_count; l++) {
         for (int which : {AR_KT_QKV, AR_KT_ATTENTION, AR_KT_O, AR_KT_GATE_UP, AR_KT_DOWN}) AR_TRY(timed_class(which, l));
     }
@@ -596,20 +595,17 @@ extern "C" int ar_hip_qwen3_create(ar_hip_ctx* ctx, const ar_qwen3_cfg* cfg, ar_
         size_t part = (size_t)((d + 15) / 16) * 4 * 256;  // up to 4 k-slices of every tile
         int counters = (d + 15) / 16;
         const int cus = ar_device_cus(m->ctx->stream);
-        const bool frag = B <= 8 && gemv_frag_fits(m->qkv_dim, d, (int)B, cus) && gemv_frag_fits(d, m->q_dim, (int)B, cus) &&
-                          gemv_frag_fits(F, d, (int)B, cus) && gemv_frag_fits(d, F, (int)B, cus) && d % 16 == 0;
+        const bool frag = B <= 8 && gemv_frag_fits(d, m->q_dim, (int)B, cus) && gemv_frag_fits(F, d, (int)B, cus) &&
+                          gemv_frag_fits(d, F, (int)B, cus) && d % 16 == 0;
         if (frag) {
-            const size_t per_layer = gemv_frag_elems(m->qkv_dim, d) + gemv_frag_elems(d, m->q_dim) +
-                                     2 * gemv_frag_elems(F, d) + gemv_frag_elems(d, F);
+            const size_t per_layer = gemv_frag_elems(d, m->q_dim) + 2 * gemv_frag_elems(F, d) + gemv_frag_elems(d, F);
             ALLOC(gv_frag, per_layer * c.layer_count * 2);
             ALLOC(gv_ss, (size_t)(d / 16) * 16 * 4);
-            part = std::max({part, gemv_frag_part_floats(m->qkv_dim, cus, 1), gemv_frag_part_floats(d, cus, 1),
-                             gemv_frag_part_floats(F, cus, 2)});
-            counters = std::max({counters, m->qkv_dim / 16, (int)(F / 16)});
+            part = std::max({part, gemv_frag_part_floats(d, cus, 1), gemv_frag_part_floats(F, cus, 2)});
+            counters = std::max({counters, (int)(F / 16)});
             uint16_t* f = m->gv_frag;
             for (int l = 0; l < c.layer_count; l++) {
                 Layer& L = m->layers[l];
-                L.fqkv = f; f += gemv_frag_elems(m->qkv_dim, d);
                 L.fo = f; f += gemv_frag_elems(d, m->q_dim);
                 L.f1 = f; f += gemv_frag_elems(F, d);
                 L.f3 = f; f += gemv_frag_elems(F, d);
@@ -832,7 +828,6 @@ extern "C" int ar_hip_qwen3_finalize(ar_qwen3* m) {
         const int d = c.dim, F = c.hidden_dim;
         hipStream_t st = m->ctx->stream;
         for (const Layer& L : m->layers) {
-            AR_TRY(launch_frag_copy((const uint16_t*)L.wqkv, L.fqkv, m->qkv_dim, d, st));
             AR_TRY(launch_frag_copy((const uint16_t*)L.wo, L.fo, d, m->q_dim, st));
             AR_TRY(launch_frag_copy((const uint16_t*)L.w1, L.f1, F, d, st));
             AR_TRY(launch_frag_copy((const uint16_t*)L.w3, L.f3, F, d, st));

@@ -108,9 +108,9 @@ class AutoregressiveModel:
         hw.check(hw.lib().ar_hip_qwen3_use_graph(self.handle, int(enable)))
 
     def use_fragment_gemv(self, enable: bool):
-        """Batches of 3..8 with bf16 weights: the decode step's QKV, O, gate/up and down GEMVs read
-        copies of those matrices in MFMA fragment order made at finalize (default on), split evenly
-        over every wavefront, or (False) the row-major weights."""
+        """Batches of 3..8 with bf16 weights: the decode step's O, gate/up and down GEMVs read copies
+        of those matrices in MFMA fragment order made at finalize (default on), split evenly over
+        every wavefront, or (False) the row-major weights."""
         hw.check(hw.lib().ar_hip_qwen3_use_fragment_gemv(self.handle, int(enable)))
 
     @property

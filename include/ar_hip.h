@@ -279,13 +279,14 @@ int ar_hip_qwen3_kernel_loop(ar_qwen3 *m, int which, int reps, double *us_per_la
 /* Use a captured HIP graph per decode step (1, default) or plain launches (0). */
 int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
 /* Fragment-ordered decode GEMVs.  For batches of 3..8 with bf16 weights (and dims that split into
- * 16 x 32 fragments, at least 4 per CU), finalize also stores each layer's QKV, O, gate/up and down
- * matrices in MFMA fragment order (16 x 32 blocks of 1 KB; as many bytes again as those weights), and
- * the decode step's four projections read that copy, split evenly over every wavefront of the GPU,
- * instead of the row-major weights; the residual-stream producers then also publish per-16-row sums
- * of squares for the next RMSNorm.  No counterpart in the reference (a weight layout of this
- * backend); results match the row-major GEMVs within float rounding.  enable 1 (default) or 0;
- * ar_hip_qwen3_fragment_gemv reports whether the steps use it. */
+ * 16 x 32 fragments, at least one per wavefront of a two-wavefront-per-CU grid), finalize also stores
+ * each layer's O, gate/up and down matrices in MFMA fragment order (16 x 32 blocks of 1 KB; as many
+ * bytes again as those weights), and those projections of the decode step read that copy, split
+ * evenly over every wavefront of the GPU, instead of the row-major weights; the O projection then
+ * also publishes per-16-row sums of squares of the residual stream for the gate/up RMSNorm.  No
+ * counterpart in the reference (a weight layout of this backend); results match the row-major
+ * GEMVs within float rounding.  enable 1 (default) or 0; ar_hip_qwen3_fragment_gemv reports whether
+ * the steps use it. */
 int ar_hip_qwen3_use_fragment_gemv(ar_qwen3 *m, int enable);
 int ar_hip_qwen3_fragment_gemv(ar_qwen3 *m, int *active);
 /* Persistent decode step.  For batch 1 with an fp32 KV cache, on the instantiated shapes

@@ -1,16 +1,16 @@
 """GPU parity of the fragment-ordered batched decode GEMVs (gemv_frag.hip), through the C-ABI.
 
-With 3..8 sequences and bf16 weights the decode step's QKV, O, gate/up and down projections read
-copies of the matrices in MFMA fragment order, split evenly over every wavefront, and the RMSNorm
-of QKV and gate/up takes its sums of squares from the per-16-row partials that the residual
-stream's producers publish.  Checked here:
+With 3..8 sequences and bf16 weights the decode step's O, gate/up and down projections read
+copies of the matrices in MFMA fragment order, split evenly over every wavefront, and the gate/up
+RMSNorm takes its sums of squares from the per-16-row partials that the O projection publishes.
+Checked here:
 
 * the C5 layer shape (d 2560, 32 Q / 8 KV heads, F 9728), batch 8: the same greedy decode with the
   fragment GEMVs and with the row-major MFMA GEMVs (ar_hip_qwen3_use_fragment_gemv(m, 0)) agree
   within float rounding (logits 1e-5 relative, every token equal), over a 24-token prompt fed one
   token per step and 16 generated tokens;
 * the Qwen3-0.6B layer shape with bf16 weights at batch 3 (sequences 3..7 of the MFMA columns
-  unused, tiles shared by up to 5 wavefronts) against the FP32 oracle run on the same bf16-rounded
+  unused, most tiles shared by several wavefronts) against the FP32 oracle run on the same bf16-rounded
   weights: logits within 2e-2 and the greedy tokens equal where the reference's top-2 margin is
   above that tolerance (the bar of the other bf16 workload tests).
 """
