@@ -24,7 +24,8 @@
 //   P4 gate/up  h = (W3 . xn) * silu(W1 . xn), xn = rmsnorm(x_mid) * ffn_norm
 //   P5 down     x' = x_mid + W2 . h          (the last layer also stores x' in the model's x)
 // then once: P6 final RMSNorm, logits (stored when asked), greedy-token keys.
-// The block grid is fixed (one block per CU); the rows of every GEMV divide evenly over it.
+// The block grid is fixed (one block per CU); each GEMV's rows divide evenly over all of it or, for
+// dims that do not split 256 ways into whole wavefront rows, over its first blocks (pick_rq, pick_ro).
 #include <cstdint>
 
 #include "ar_hip_internal.h"
@@ -243,21 +244,43 @@ __device__ inline float block_sum(float v, float* red, int lane, int wave) {
     return t;
 }
 
+// Row distribution of the GEMV stages over the kPB blocks.  QKV: RQ rows per block (a multiple of the
+// wavefront count, all rows of a block in one head), the smallest such that QKVD / RQ blocks cover
+// the rows.  O / down: RO rows per block, each split over WPR = kPW / RO wavefronts, the smallest RO
+// for which DIM / RO blocks cover the rows and the O / down input widths split into whole 64-lane
+// chunks per wavefront.  Blocks past QKVD / RQ (DIM / RO) have no rows in that stage.
+constexpr int pick_rq(int qkvd, int hd) {
+    for (int rq = kPW; rq <= 64; rq += kPW)
+        if (qkvd % rq == 0 && qkvd / rq <= kPB && hd % rq == 0) return rq;
+    return 0;
+}
+constexpr int pick_ro(int dim, int qd, int f, int cw) {
+    for (int ro = 1; ro <= kPW; ro *= 2) {
+        const int wpr = kPW / ro;
+        if (dim % ro == 0 && dim / ro <= kPB && qd % (wpr * cw) == 0 && f % (wpr * cw) == 0) return ro;
+    }
+    return 0;
+}
+
 template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
 __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     using WR = WRow<TW>;
     typedef typename WR::raw wraw;
     constexpr int CW = 64 * WR::V;  // columns per 16-byte load of a wavefront
     constexpr int QD = H * HD, KVD = KV * HD, QKVD = QD + 2 * KVD, G = H / KV, FD = HD / 2;
-    // P1: RPWq rows per wavefront, NCq CW-column chunks per row
-    constexpr int RQ = QKVD / kPB, RPWq = RQ / kPW, NCq = DIM / CW;
-    // P3 / P5: RO (= RD) rows per block, each split over WPR wavefronts
-    constexpr int RO = DIM / kPB, WPR = kPW / RO, NCo = QD / (WPR * CW), NCd = F / (WPR * CW);
+    // P1: RQ rows per block on the first NQB blocks, RPWq per wavefront, NCq CW-column chunks per row
+    constexpr int RQ = pick_rq(QKVD, HD), NQB = RQ ? QKVD / RQ : 1, RPWq = RQ / kPW, NCq = DIM / CW;
+    // P3 / P5: RO (= RD) rows per block on the first NOB blocks, each split over WPR wavefronts
+    constexpr int RO = pick_ro(DIM, QD, F, CW), NOB = RO ? DIM / RO : 1, WPR = RO ? kPW / RO : 1;
+    constexpr int NCo = QD / (WPR * CW), NCd = F / (WPR * CW);
     // P4: RG gate/up row pairs per block; wavefronts 0..kPW/2-1 take gate rows, the rest up rows
     constexpr int RG = F / kPB, RPWg = 2 * RG / kPW, NCg = DIM / CW;
-    static_assert(QKVD % kPB == 0 && RQ % kPW == 0 && RPWq >= 1, "QKV rows must split over the waves");
-    static_assert(DIM % CW == 0 && DIM % kPB == 0 && RO >= 1 && kPW % RO == 0, "dim must split over the waves");
-    static_assert(QD % (WPR * CW) == 0 && F % (WPR * CW) == 0, "O / down columns must split over the waves");
+    // inputs of DIM / QD / F values: this many per thread of the block
+    constexpr int NXD = (DIM + kPT - 1) / kPT, NXA = (QD + kPT - 1) / kPT;
+    static_assert(RQ > 0 && RPWq >= 1, "QKV rows must split over the blocks' waves");
+    // (constant true when every block has rows in the stage)
+    const bool has_q = NQB >= kPB || (int)blockIdx.x < NQB, has_o = NOB >= kPB || (int)blockIdx.x < NOB;
+    static_assert(DIM % CW == 0 && RO > 0, "dim must split over the blocks' waves");
     static_assert(F % kPB == 0 && (2 * RG) % kPW == 0 && RG % RPWg == 0 && 2 * RG <= 64, "gate/up rows");
     static_assert(HD == 128 || HD == 64, "head size");
     constexpr int XMAX = QD > F ? (QD > DIM ? QD : DIM) : (F > DIM ? F : DIM);
@@ -271,7 +294,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     constexpr int OFF_SS = OFF_H + F;
     constexpr int PAR_WORDS = OFF_SS + NSQ + NSK;
     static_assert(QD % RQ == 0 && KVD % RQ == 0 && HD % RQ == 0, "a QKV block's rows lie in one head");
-    static_assert(KV * SMAX <= kPB - H && QD % kPT == 0, "attention and merge blocks must not overlap");
+    static_assert(KV * SMAX <= kPB - H, "attention and merge blocks must not overlap");
 
     __shared__ __attribute__((aligned(16))) float xr[DIM];    // layer input x_l
     __shared__ __attribute__((aligned(16))) float xmr[DIM];   // x_mid (after the O residual)
@@ -320,6 +343,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     constexpr bool kQkvAfterDown = sizeof(TW) == 4;
     wraw wq[RPWq][NCq];
     auto load_wq = [&](const void* W, int wave, int lane) {
+        if (!has_q) return;  // no QKV rows in this block
         const int r0 = b * RQ + wave * RPWq;
 #pragma unroll
         for (int i = 0; i < RPWq; i++)
@@ -342,7 +366,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         {
         STAGE_IDS();
         {
-            constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+            constexpr int NX = NXD;
             // the gains are loaded before the wait, so the wait's completion covers them
             float gv[NX];
 #pragma unroll
@@ -374,6 +398,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             float ssq = 0.f;
 #pragma unroll
             for (int i = 0; i < RPWq; i++) {
+                if (!has_q) break;
                 float a = 0.f;
 #pragma unroll
                 for (int c = 0; c < NCq; c++) a = WR::dot(wq[i][c], &xin[c * CW + lane * WR::V], a);
@@ -628,7 +653,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         // issue_o_gu(wave, lane, i0, i1): the O rows (when i0 == 0) and gate/up rows i0 .. i1-1 of the wavefront
         auto issue_o_gu = [&](int wave, int lane, int i0, int i1) {
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
-            if (i0 == 0) {
+            if (i0 == 0 && has_o) {
 #pragma unroll
                 for (int c = 0; c < NCo; c++)
                     wo[c] = WR::load(Ly.wo, (size_t)row * QD + col0 + c * CW + lane * WR::V);
@@ -715,24 +740,27 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // merge blocks issued both before their merge).
             if (b < kPB - H) issue_o_gu(wave, lane, 0, RPWg);
             else if (kMergeEarlyRows < RPWg) issue_o_gu(wave, lane, kMergeEarlyRows, RPWg);
-            constexpr int NA = QD / kPT;
+            constexpr int NA = NXA;
             int idx[NA];
 #pragma unroll
-            for (int j = 0; j < NA; j++) idx[j] = OFF_A + tid + j * kPT;
+            for (int j = 0; j < NA; j++) idx[j] = has_o && (QD % kPT == 0 || tid + j * kPT < QD) ? OFF_A + tid + j * kPT : -1;
             float av[NA];
             ll_wait<NA>(cur, idx, av, ep, dead, p.err, p.spin_limit);
             PK_MARK(l, 7);
 #pragma unroll
-            for (int j = 0; j < NA; j++) xin[tid + j * kPT] = av[j];
+            for (int j = 0; j < NA; j++)
+                if (QD % kPT == 0 || tid + j * kPT < QD) xin[tid + j * kPT] = av[j];
             lds_barrier();
             PK_MARK(l, 21);
             float a = 0.f;
+            if (has_o) {
 #pragma unroll
-            for (int c = 0; c < NCo; c++) a = WR::dot(wo[c], &xin[col0 + c * CW + lane * WR::V], a);
+                for (int c = 0; c < NCo; c++) a = WR::dot(wo[c], &xin[col0 + c * CW + lane * WR::V], a);
+            }
             a = gemv::dpp_sum_lane63(a);
             if (lane == 63) rows_s[wave] = a;
             lds_barrier();
-            if (tid < RO) {
+            if (tid < RO && has_o) {
                 float sum = 0.f;
 #pragma unroll
                 for (int k = 0; k < WPR; k++) sum += rows_s[tid * WPR + k];
@@ -747,7 +775,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         {
             STAGE_IDS();
             if (!kQkvAfterDown && l + 1 < p.L) load_wq(lay_s[l + 1].wqkv, wave, lane);
-            constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+            constexpr int NX = NXD;
             float gv[NX];
 #pragma unroll
             for (int j = 0; j < NX; j++) gv[j] = tid + j * kPT < DIM ? gld(Ly.ffn_norm, tid + j * kPT) : 0.f;
@@ -793,13 +821,15 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             STAGE_IDS();
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (F / WPR);
             wraw wd[NCd];
+            if (has_o) {
 #pragma unroll
-            for (int c = 0; c < NCd; c++)
-                wd[c] = WR::load(Ly.w2, (size_t)row * F + col0 + c * CW + lane * WR::V);
+                for (int c = 0; c < NCd; c++)
+                    wd[c] = WR::load(Ly.w2, (size_t)row * F + col0 + c * CW + lane * WR::V);
+            }
             constexpr int NH = F / kPT > 0 ? (F + kPT - 1) / kPT : 1;
             int idx[NH];
 #pragma unroll
-            for (int j = 0; j < NH; j++) idx[j] = tid + j * kPT < F ? OFF_H + tid + j * kPT : -1;
+            for (int j = 0; j < NH; j++) idx[j] = has_o && tid + j * kPT < F ? OFF_H + tid + j * kPT : -1;
             float hv[NH];
             ll_wait<NH>(cur, idx, hv, ep, dead, p.err, p.spin_limit);
             PK_MARK(l, 11);
@@ -809,12 +839,14 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             lds_barrier();
             PK_MARK(l, 23);
             float a = 0.f;
+            if (has_o) {
 #pragma unroll
-            for (int c = 0; c < NCd; c++) a = WR::dot(wd[c], &xin[col0 + c * CW + lane * WR::V], a);
+                for (int c = 0; c < NCd; c++) a = WR::dot(wd[c], &xin[col0 + c * CW + lane * WR::V], a);
+            }
             a = gemv::dpp_sum_lane63(a);
             if (lane == 63) rows_s[wave] = a;
             lds_barrier();
-            if (tid < RO) {
+            if (tid < RO && has_o) {
                 float sum = 0.f;
 #pragma unroll
                 for (int k = 0; k < WPR; k++) sum += rows_s[tid * WPR + k];
@@ -850,7 +882,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         };
         const int first = gw * RB;
         if (first < r1) load_batch(wa, first);
-        constexpr int NX = DIM / kPT > 0 ? DIM / kPT : 1;
+        constexpr int NX = NXD;
         float gv[NX];
 #pragma unroll
         for (int j = 0; j < NX; j++) gv[j] = tid + j * kPT < DIM ? gld(p.final_norm, tid + j * kPT) : 0.f;
@@ -915,7 +947,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
 template <int DIM, int F, int H, int KV, int HD, int SMAX>
 constexpr size_t ll_words() {
     constexpr int QD = H * HD, KVD = KV * HD, G = H / KV;
-    constexpr int RQ = (QD + 2 * KVD) / kPB;
+    constexpr int RQ = pick_rq(QD + 2 * KVD, HD);
     return 2 * (size_t)(2 * DIM + QD + 2 * KVD + KV * SMAX * G * (HD + 2) + QD + F + (QD + KVD) / RQ);
 }
 
@@ -954,10 +986,13 @@ int fits_t(int* blocks_per_cu) {
 
 // The instantiated shapes: (weight type, dim, FFN, heads, KV heads, head size, attention splits per KV
 // head).  Qwen3-0.6B with fp32 weights (contexts of a few hundred rows: 8 splits), Qwen3-1.7B with bf16
-// weights (2K-row contexts: 28 splits of ~80 rows, 224 attention blocks).
+// weights (2K-row contexts: 28 splits of ~80 rows, 224 attention blocks), and the llama2.c stories110M
+// shape with fp32 weights (12 heads of 64, no QK-norm gains, 1K-row contexts: 16 splits of <= 64 rows,
+// 192 attention blocks; QKV rows on 144 blocks, O / down rows on 96).
 #define AR_PERSISTENT_SHAPES(X)                         \
     X(AR_DTYPE_F32, float, 1024, 3072, 16, 8, 128, 8)  \
-    X(AR_DTYPE_BF16, uint16_t, 2048, 6144, 16, 8, 128, 28)
+    X(AR_DTYPE_BF16, uint16_t, 2048, 6144, 16, 8, 128, 28) \
+    X(AR_DTYPE_F32, float, 768, 2048, 12, 12, 64, 16)
 
 }  // namespace
 

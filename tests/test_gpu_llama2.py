@@ -230,3 +230,56 @@ def test_llama2_unsupported_shapes(ctx, tmp_path):
     write_checkpoint(tmp_path / "model.bin", cfg, make_weights(cfg))
     with pytest.raises(hw.HardwareException, match="head size"):
         Llama2(tmp_path / "model.bin", None, ctx)
+
+
+def test_llama2_stories_shape_persistent_vs_oracle_and_multi_launch(ctx, tmp_path):
+    """The persistent decode step at the llama2.c stories110M layer shape (d 768, 12 heads of 64 =
+    KV heads, F 2048, fp32, no QK-norm gains; 2 layers and a 1000-word tied head here): QKV rows on
+    144 of the 256 blocks, O / down rows on 96, 12 x 16 attention blocks.  A short prompt fed one
+    token per step against the FP64 oracle (tokens exact, logits 1e-4); then a 600-token prompt
+    through the batched fp32 prefill and 12 persistent steps (16 splits of 38-39 rows) against the
+    same steps as separate launches (logits 1e-5, tokens equal) and against the oracle's prompt pass."""
+    cfg = Llama2Config(768, 2048, 2, 12, 12, 1000, 1024, True, 64)
+    w = make_weights(cfg, seed=5)
+    write_checkpoint(tmp_path / "model.bin", cfg, w)
+    prompt = [BOS, 17, 230, 5, 99, 301]
+    ref = oracle_model(cfg, w)
+    ref_fed, ref_logits = ref.generate(prompt, 20)
+    rng = np.random.default_rng(6)
+    long = [BOS] + [int(t) for t in rng.integers(3, cfg.vocab_size, 599)]
+    lref_fed, lref_logits = oracle_model(cfg, w, precision="fp32").generate_prefilled(long, 12)
+    with Llama2(tmp_path / "model.bin", None, ctx) as m:
+        am = m.model
+        assert am.persistent, "the stories110M shape should run the persistent decode kernel"
+        fed, logits = gpu_generate(m, prompt, 20)
+        assert compare_tokens(fed, ref_fed, ref_logits, len(prompt)) == len(ref_fed)
+        assert rel_err(logits, np.asarray(ref_logits)) <= 1e-4
+        runs = {}
+        for persistent in (True, False):
+            am.use_persistent(persistent)
+            assert am.persistent == persistent
+            am.reset()
+            am.set_prompt(long)
+            lp = am.prefill(return_logits=True)
+            toks, lgs = [], []
+            for _ in range(12):
+                t, lg = am.next(return_logits=True)
+                toks.append(int(t[0]))
+                lgs.append(lg[0])
+            runs[persistent] = (lp[0], toks, np.stack(lgs))
+        am.use_persistent(True)
+    (lp_p, toks_p, lgs_p), (lp_m, toks_m, lgs_m) = runs[True], runs[False]
+    assert toks_p == toks_m, (toks_p, toks_m)
+    assert rel_err(lgs_p, lgs_m) <= 1e-5, rel_err(lgs_p, lgs_m)
+    assert rel_err(lp_p, lref_logits[0]) <= 1e-4
+    n_eq = len(toks_p)
+    for s in range(len(toks_p)):  # token s was chosen from lref_logits[s] (the prompt's last row for s = 0)
+        if toks_p[s] != lref_fed[s]:
+            top2 = np.sort(lref_logits[s])[-2:]
+            assert (top2[1] - top2[0]) / max(abs(top2[1]), 1e-30) < NEAR_TIE, (s, toks_p[s], lref_fed[s])
+            n_eq = s
+            break
+    for s in range(n_eq):
+        assert rel_err(lgs_p[s], lref_logits[s + 1]) <= 1e-4, (s, rel_err(lgs_p[s], lref_logits[s + 1]))
+    print(f"[llama2] stories shape: persistent == separate launches over 12 steps at 600-611 rows, "
+          f"{n_eq} of 12 decisions equal to the oracle", flush=True)
