@@ -396,8 +396,8 @@ __host__ __device__ inline void attn_split_plan(int n, int max_splits, int* nspl
 // Attention partials + (when the context is split) the combine kernel.
 int launch_attention_decode(const AttnLaunch& a, hipStream_t stream);
 
-// Persistent decode step (decode_persistent.hip): every layer of a batch-1 fp32 decode step in one
-// cooperative launch of one block per CU.  `layers` is a device table of layer_count entries written
+// Persistent decode step (decode_persistent.hip): every layer of a batch-1 decode step in one launch
+// of one block per CU.  `layers` is a device table of layer_count entries written
 // by decode_persistent_layer_entry; `ll` holds decode_persistent_ll_words() zeroed words at first
 // use; state[0] is the position and state[3] the exchange epoch base, which every launch advances.
 struct DecodePersistentLaunch {
@@ -406,8 +406,9 @@ struct DecodePersistentLaunch {
     int wdtype = AR_DTYPE_F32;  // projection / head weights: AR_DTYPE_F32 or AR_DTYPE_BF16
     int dim = 0, hidden_dim = 0, heads = 0, kv_heads = 0, head_dim = 0;
     float* x = nullptr;        // [dim] the step's input and, after the launch, its output
-    float* kcache = nullptr;   // [L][KV][S][HD] fp32
-    float* vcache = nullptr;
+    void* kcache = nullptr;    // [L][KV][S][HD], fp32 or (kv16) fp16
+    void* vcache = nullptr;
+    bool kv16 = false;
     int max_seq = 0;
     const float2* rope_tab = nullptr;
     int* state = nullptr;
@@ -428,7 +429,7 @@ size_t decode_persistent_ll_words(int wdtype, int dim, int F, int heads, int kv_
 int decode_persistent_layer_entry(void* dst, const void* wqkv, const void* wo, const void* w1, const void* w3,
                                   const void* w2, const float* attn_norm, const float* ffn_norm, const float* q_norm,
                                   const float* k_norm, const float* bqkv);
-bool decode_persistent_supported(int wdtype, int dim, int F, int heads, int kv_heads, int hd);
+bool decode_persistent_supported(int wdtype, int dim, int F, int heads, int kv_heads, int hd, bool kv16);
 int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t stream);
 size_t attention_partial_floats(int batch, int heads, int max_splits, int hd);
 // Splits for a cache of max_seq rows: about one block per CU, rows per split <= 256 (1040 for an

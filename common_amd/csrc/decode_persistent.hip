@@ -82,8 +82,8 @@ struct PParams {
     const PLayer* layers;
     int L;
     float* x;          // [dim]: the step's input (embedding row) and, after the last layer, its output
-    float* kcache;     // [L][KV][S][HD]
-    float* vcache;
+    void* kcache;      // [L][KV][S][HD], fp32 or fp16 (the KT instantiation)
+    void* vcache;
     int S;
     const float2* rope_tab;  // [S][HD/2] (cos, sin)
     int* state;        // [0] position, [3] epoch base (advanced by L at the end of every launch)
@@ -262,10 +262,14 @@ constexpr int pick_ro(int dim, int qd, int f, int cw) {
     return 0;
 }
 
-template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
+template <typename TW, typename KT, int DIM, int F, int H, int KV, int HD, int SMAX>
 __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     using WR = WRow<TW>;
     typedef typename WR::raw wraw;
+    // fp16 cache: rows are widened as they are read; the step's new k / v row is rounded to fp16
+    // before it is used, so every step sees exactly the values the cache holds
+    constexpr bool kv16 = sizeof(KT) == 2;
+    static_assert(sizeof(KT) == 4 || sizeof(KT) == 2, "fp32 or fp16 cache");
     constexpr int CW = 64 * WR::V;  // columns per 16-byte load of a wavefront
     constexpr int QD = H * HD, KVD = KV * HD, QKVD = QD + 2 * KVD, G = H / KV, FD = HD / 2;
     // P1: RQ rows per block on the first NQB blocks, RPWq per wavefront, NCq CW-column chunks per row
@@ -442,21 +446,26 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             const int g = b / nsplit, s = b - g * nsplit;
             const int t0 = s * tile, t1 = min(t0 + tile, n);
             const size_t head_base = ((size_t)l * KV + g) * (size_t)p.S * HD;
-            float* kc = p.kcache + head_base;
-            float* vc = p.vcache + head_base;
+            KT* kc = reinterpret_cast<KT*>(p.kcache) + head_base;
+            KT* vc = reinterpret_cast<KT*>(p.vcache) + head_base;
             // row j of chunk c of this wavefront (uniform over the wavefront)
             auto row_of = [&](int c, int j) { return t0 + c * (kPW * RW) + wave + kPW * j; };
             float kr[RW][DPL], vr[RW][DPL];
-            auto load_rows = [&](float (&dst)[RW][DPL], const float* src, int c) {
+            auto load_rows = [&](float (&dst)[RW][DPL], const KT* src, int c) {
 #pragma unroll
                 for (int j = 0; j < RW; j++) {
-                    const float* r = src + (size_t)min(row_of(c, j), t1 - 1) * HD + lane * DPL;
-                    if constexpr (DPL == 2) {
+                    const KT* r = src + (size_t)min(row_of(c, j), t1 - 1) * HD + lane * DPL;
+                    if constexpr (kv16 && DPL == 2) {
+                        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                        const h2 v = *reinterpret_cast<const h2*>(r);
+                        dst[j][0] = (float)v.x;
+                        dst[j][1] = (float)v.y;
+                    } else if constexpr (DPL == 2) {
                         const float2 v = *reinterpret_cast<const float2*>(r);
                         dst[j][0] = v.x;
                         dst[j][1] = v.y;
                     } else {
-                        dst[j][0] = r[0];
+                        dst[j][0] = (float)r[0];
                     }
                 }
             };
@@ -511,7 +520,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 sk = gemv::dpp_sum_lane63(sk);
                 if (lane == 63) red2[wave] = make_float2(sq, sk);
             }
-            if (tid >= T_V && tid < T_S) v_new[tid - T_V] = qv[0];
+            if (tid >= T_V && tid < T_S) v_new[tid - T_V] = kv16 ? (float)(KT)qv[0] : qv[0];
             lds_barrier();
             PK_MARK(l, 16);
             const bool has_pos = pos >= t0 && pos < t1;
@@ -538,15 +547,16 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                     q_s[rj][rf] = o1;
                     q_s[rj][rf + FD] = o2;
                 } else {
-                    k_new[rf] = o1;
-                    k_new[rf + FD] = o2;
+                    const KT k1 = (KT)o1, k2 = (KT)o2;
+                    k_new[rf] = (float)k1;
+                    k_new[rf + FD] = (float)k2;
                     if (has_pos) {
-                        kc[(size_t)pos * HD + rf] = o1;
-                        kc[(size_t)pos * HD + rf + FD] = o2;
+                        kc[(size_t)pos * HD + rf] = k1;
+                        kc[(size_t)pos * HD + rf + FD] = k2;
                     }
                 }
             } else if (tid < T_S && has_pos) {
-                vc[(size_t)pos * HD + (tid - T_V)] = qv[0];
+                vc[(size_t)pos * HD + (tid - T_V)] = (KT)qv[0];
             }
             lds_barrier();
             PK_MARK(l, 17);
@@ -951,7 +961,7 @@ constexpr size_t ll_words() {
     return 2 * (size_t)(2 * DIM + QD + 2 * KVD + KV * SMAX * G * (HD + 2) + QD + F + (QD + KVD) / RQ);
 }
 
-template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
+template <typename TW, typename KT, int DIM, int F, int H, int KV, int HD, int SMAX>
 int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     PParams p;
     p.layers = reinterpret_cast<const PLayer*>(a.layers);
@@ -960,7 +970,7 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     p.state = a.state; p.ll = a.ll; p.err = a.err; p.eps = a.eps; p.per_head = a.per_head_norm;
     p.spin_limit = a.wait_limit ? a.wait_limit : kSpinLimit;
     p.final_norm = a.final_norm; p.lm_head = a.lm_head; p.vocab = a.vocab; p.logits = a.logits; p.keys = a.keys;
-    auto kern = decode_persistent_kernel<TW, DIM, F, H, KV, HD, SMAX>;  // (its LDS attribute is set by fits_t)
+    auto kern = decode_persistent_kernel<TW, KT, DIM, F, H, KV, HD, SMAX>;  // (its LDS attribute is set by fits_t)
     // A plain launch (a cooperative one measured ~20 us longer per step): every block must be resident
     // at once, which decode_persistent_supported checks (one 512-thread block per CU, kPB CUs) and
     // which holds while nothing else runs on the device; if some block were not, the others' waits
@@ -970,9 +980,9 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     return AR_HIP_OK;
 }
 
-template <typename TW, int DIM, int F, int H, int KV, int HD, int SMAX>
+template <typename TW, typename KT, int DIM, int F, int H, int KV, int HD, int SMAX>
 int fits_t(int* blocks_per_cu) {
-    auto kern = decode_persistent_kernel<TW, DIM, F, H, KV, HD, SMAX>;
+    auto kern = decode_persistent_kernel<TW, KT, DIM, F, H, KV, HD, SMAX>;
     // no private (scratch) memory: the dispatcher may hold back waves that need scratch beyond the
     // runtime's scratch allocation, and every block of this kernel must be resident at once
     hipFuncAttributes fa;
@@ -984,8 +994,8 @@ int fits_t(int* blocks_per_cu) {
     return 1;
 }
 
-// The instantiated shapes: (weight type, dim, FFN, heads, KV heads, head size, attention splits per KV
-// head).  Qwen3-0.6B with fp32 weights (contexts of a few hundred rows: 8 splits), Qwen3-1.7B with bf16
+// The instantiated shapes, each with an fp32 and an fp16 KV cache: (weight type, dim, FFN, heads, KV
+// heads, head size, attention splits per KV head).  Qwen3-0.6B with fp32 weights (contexts of a few hundred rows: 8 splits), Qwen3-1.7B with bf16
 // weights (2K-row contexts: 28 splits of ~80 rows, 224 attention blocks), and the llama2.c stories110M
 // shape with fp32 weights (12 heads of 64, no QK-norm gains, 1K-row contexts: 16 splits of <= 64 rows,
 // 192 attention blocks; QKV rows on 144 blocks, O / down rows on 96).
@@ -1014,14 +1024,15 @@ int decode_persistent_layer_entry(void* dst, const void* wqkv, const void* wo, c
     return AR_HIP_OK;
 }
 
-bool decode_persistent_supported(int wdtype, int dim, int F, int heads, int kv_heads, int hd) {
+bool decode_persistent_supported(int wdtype, int dim, int F, int heads, int kv_heads, int hd, bool kv16) {
     if (decode_persistent_ll_words(wdtype, dim, F, heads, kv_heads, hd) == 0) return false;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
     int ok = 0;
-#define AR_X(DT, TW, D, FF, HH, KK, HDD, SM) \
-    if (wdtype == DT && dim == D && F == FF && heads == HH && kv_heads == KK && hd == HDD) ok = fits_t<TW, D, FF, HH, KK, HDD, SM>(&per_cu);
+#define AR_X(DT, TW, D, FF, HH, KK, HDD, SM)                                                              \
+    if (wdtype == DT && dim == D && F == FF && heads == HH && kv_heads == KK && hd == HDD)                \
+        ok = kv16 ? fits_t<TW, _Float16, D, FF, HH, KK, HDD, SM>(&per_cu) : fits_t<TW, float, D, FF, HH, KK, HDD, SM>(&per_cu);
     AR_PERSISTENT_SHAPES(AR_X)
 #undef AR_X
     return ok && per_cu >= 1 && (long long)per_cu * cus >= kPB;
@@ -1037,7 +1048,7 @@ int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t st) {
     if (ar_check_ptrs_enabled()) {
         const char* k = "persistent decode";
         const size_t wb = a.wdtype == AR_DTYPE_BF16 ? 2 : 4, D = a.dim, L = a.layer_count;
-        const size_t cache = L * a.kv_heads * (size_t)a.max_seq * a.head_dim * 4;
+        const size_t cache = L * a.kv_heads * (size_t)a.max_seq * a.head_dim * (a.kv16 ? 2 : 4);
         AR_TRY(ar_check_range(a.layers, L * decode_persistent_layer_bytes(), k, "layer table"));
         AR_TRY(ar_check_range(a.x, D * 4, k, "residual row"));
         AR_TRY(ar_check_range(a.kcache, cache, k, "key cache"));
@@ -1054,7 +1065,7 @@ int launch_decode_persistent(const DecodePersistentLaunch& a, hipStream_t st) {
     }
 #define AR_X(DT, TW, D, FF, HH, KK, HDD, SM)                                                                          \
     if (a.wdtype == DT && a.dim == D && a.hidden_dim == FF && a.heads == HH && a.kv_heads == KK && a.head_dim == HDD) \
-        return launch_t<TW, D, FF, HH, KK, HDD, SM>(a, st);
+        return a.kv16 ? launch_t<TW, _Float16, D, FF, HH, KK, HDD, SM>(a, st) : launch_t<TW, float, D, FF, HH, KK, HDD, SM>(a, st);
     AR_PERSISTENT_SHAPES(AR_X)
 #undef AR_X
     ar_set_error("persistent decode: weight type %d, dim %d, hidden %d, heads %d/%d, head size %d has no instantiation",

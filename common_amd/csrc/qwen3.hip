@@ -139,7 +139,7 @@ struct ar_qwen3 {
     bool pf_w16_in_range = true;  // host copy of pf_flag[1] after the fp16 copies were made
     int pf_by_steps = 0;          // prefill calls that went through the decode step
 
-    // persistent decode step (batch 1, fp32 or bf16 weights, fp32 cache): every layer, the final RMSNorm, the
+    // persistent decode step (batch 1, fp32 or bf16 weights, fp32 or fp16 cache): every layer, the final RMSNorm, the
     // logits and the greedy keys in one launch (decode_persistent.hip) after the step-begin kernel
     bool pk_ok = false;          // shape, dtypes and device qualify; buffers below allocated
     bool pk_on = true;           // ar_hip_qwen3_use_persistent
@@ -382,7 +382,8 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         d.layers = m->pk_layers; d.layer_count = c.layer_count; d.wdtype = c.weight_dtype; d.dim = dim;
         d.hidden_dim = c.hidden_dim;
         d.heads = c.head_count; d.kv_heads = c.kv_head_count; d.head_dim = c.head_size; d.x = m->x;
-        d.kcache = (float*)m->kcache; d.vcache = (float*)m->vcache; d.max_seq = m->S; d.rope_tab = m->rope_tab;
+        d.kcache = m->kcache; d.vcache = m->vcache; d.kv16 = c.kv_dtype == AR_DTYPE_F16; d.max_seq = m->S;
+        d.rope_tab = m->rope_tab;
         d.state = m->state; d.ll = m->pk_ll; d.err = m->pk_err; d.wait_limit = m->pk_wait_limit;
         d.eps = (float)c.epsilon;
         d.per_head_norm = c.qk_norm_mode == AR_QK_NORM_PER_HEAD;
@@ -706,8 +707,9 @@ extern "C" int ar_hip_qwen3_set_weight(ar_qwen3* m, const char* key, const void*
 static int setup_persistent(ar_qwen3* m) {
     const ar_qwen3_cfg& c = m->cfg;
     m->pk_ok = false;
-    if (m->B != 1 || c.kv_dtype == AR_DTYPE_F16) return AR_HIP_OK;
-    if (!decode_persistent_supported(c.weight_dtype, c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size))
+    if (m->B != 1) return AR_HIP_OK;
+    if (!decode_persistent_supported(c.weight_dtype, c.dim, c.hidden_dim, c.head_count, c.kv_head_count, c.head_size,
+                                     c.kv_dtype == AR_DTYPE_F16))
         return AR_HIP_OK;
     const size_t eb = decode_persistent_layer_bytes();
     if (!m->pk_ll) {

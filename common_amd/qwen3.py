@@ -122,8 +122,8 @@ class AutoregressiveModel:
 
     def use_persistent(self, enable: bool):
         """Run the layers of each decode step as one persistent launch when the model qualifies
-        (default on) or as separate launches.  It qualifies at batch 1 with an fp32 KV cache on the
-        three instantiated shapes: d1024/F3072, 16/8 heads of 128, fp32 weights (Qwen3-0.6B),
+        (default on) or as separate launches.  It qualifies at batch 1 with an fp32 or fp16 KV cache
+        on the three instantiated shapes: d1024/F3072, 16/8 heads of 128, fp32 weights (Qwen3-0.6B),
         d2048/F6144, 16/8 heads of 128, bf16 weights (Qwen3-1.7B) and d768/F2048, 12/12 heads of 64,
         fp32 weights (llama2.c stories110M).  A call whose persistent launch
         timed out (blocks not resident together) is recomputed as separate launches and switches

@@ -289,7 +289,7 @@ int ar_hip_qwen3_use_graph(ar_qwen3 *m, int enable);
  * the steps use it. */
 int ar_hip_qwen3_use_fragment_gemv(ar_qwen3 *m, int enable);
 int ar_hip_qwen3_fragment_gemv(ar_qwen3 *m, int *active);
-/* Persistent decode step.  For batch 1 with an fp32 KV cache, on the instantiated shapes
+/* Persistent decode step.  For batch 1 with an fp32 or fp16 KV cache, on the instantiated shapes
  *   dim 1024 / FFN 3072 / 16 Q, 8 KV heads / head size 128 with fp32 weights (Qwen3-0.6B),
  *   dim 2048 / FFN 6144 / 16 Q, 8 KV heads / head size 128 with bf16 weights (Qwen3-1.7B), and
  *   dim 768 / FFN 2048 / 12 Q = KV heads / head size 64 with fp32 weights (llama2.c stories110M),

@@ -529,3 +529,56 @@ def test_persistent_models_side_by_side_and_after_release(ctx):
         check(1, *gpu_generate(m1, prompts[1], 8))
     finally:
         m1.close()
+
+
+@pytest.mark.parametrize("shape", ["c3", "c4"])
+def test_persistent_fp16_kv_cache_matches_multi_launch_and_oracle(ctx, shape):
+    """The persistent decode kernel with an fp16 KV cache (rows widened as they are read, the step's
+    new k / v row rounded to fp16 before it is used): the Qwen3-0.6B layer shape with fp32 weights
+    and the Qwen3-1.7B layer shape with bf16 weights, 2 layers, batch 1.  A 300-token prompt through
+    the batched prefill (which writes the fp16 cache), then 16 greedy steps (10 attention splits per
+    KV head for the 1.7B instance, the 8-split cap for the 0.6B one) in the persistent kernel and as
+    separate launches: tokens equal and logits within 1e-4 (the two forms compute the new k row in
+    fp32 in different orders, so now and then one element rounds to the neighbouring fp16 value, one
+    fp16 ulp = 4.9e-4 relative, which moves the logits by ~1e-5; with the fp32 cache the forms agree
+    to 1e-5); against the FP32 oracle (fp32 cache) the bf16 north-star bar, 2e-2, as for the other
+    fp16-cache tests."""
+    base = C.C3_0_6B if shape == "c3" else C.C4_1_7B
+    cfg = dataclasses.replace(base, layer_count=2, vocab_size=4096, shared_weights=False, seq_len=336, max_batch=1,
+                              kv_dtype=C.DTYPE_F16)
+    sd = synthetic.state_dict(cfg, seed=41)
+    prompt = synthetic.prompt_ids(300, cfg.vocab_size, seed=42)
+    runs = {}
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        assert am.persistent, "the fp16 cache should run the persistent decode kernel"
+        for persistent in (True, False):
+            am.use_persistent(persistent)
+            assert am.persistent == persistent
+            am.reset()
+            am.set_prompt(prompt)
+            lp = am.prefill(return_logits=True)
+            toks, lgs = [], []
+            for _ in range(16):
+                t, lg = am.next(return_logits=True)
+                toks.append(int(t[0]))
+                lgs.append(lg[0])
+            runs[persistent] = (lp[0], toks, np.stack(lgs))
+        am.use_persistent(True)
+    (lp_p, toks_p, lgs_p), (_, toks_m, lgs_m) = runs[True], runs[False]
+    assert toks_p == toks_m, (toks_p, toks_m)
+    assert rel_err(lgs_p, lgs_m) <= 1e-4, rel_err(lgs_p, lgs_m)
+    ref = oracle.OracleQwen3(cfg, sd, precision="fp32")
+    fed, rl = ref.generate_prefilled(prompt, 16)
+    ref.close()
+    assert rel_err(lp_p, rl[0]) <= 2e-2
+    n_eq = 16
+    for s in range(16):  # token s was chosen from rl[s]
+        if toks_p[s] != fed[s]:
+            top = np.sort(rl[s])[-2:]
+            assert (top[1] - top[0]) / abs(top[1]) < 2e-2, (s, toks_p[s], fed[s])
+            n_eq = s
+            break
+        assert rel_err(lgs_p[s], rl[s + 1]) <= 2e-2, (s, rel_err(lgs_p[s], rl[s + 1]))
+    print(f"{shape} fp16 cache: persistent vs separate launches {rel_err(lgs_p, lgs_m):.1e} over 16 steps, "
+          f"{n_eq} of 16 decisions equal to the FP32 oracle", flush=True)
