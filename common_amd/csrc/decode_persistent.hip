@@ -660,6 +660,13 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         // O rows and gate/up rows of this block (held from their issue to the O and gate/up stages)
         wraw wo[NCo];
         wraw wg[RPWg][NCg];
+        // With fp32 weights the blocks that run neither attention nor a merge also issue their down
+        // rows behind the gate/up rows, so the down stage's poll has nothing queued ahead of it on
+        // those CUs (C3 0.5612-0.5644 -> 0.5575-0.5616 ms per step over three runs); the attention
+        // blocks doing the same (0.585) or every block (0.586) delays the attention chain instead.
+        // (bf16 at d 2048 has no register room for them.)
+        wraw wd[NCd];
+        const bool early_d = sizeof(TW) == 4 && has_o && b >= KV * nsplit && b < kPB - H;
         // issue_o_gu(wave, lane, i0, i1): the O rows (when i0 == 0) and gate/up rows i0 .. i1-1 of the wavefront
         auto issue_o_gu = [&](int wave, int lane, int i0, int i1) {
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
@@ -671,8 +678,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // The blocks that are not busy with attention hold the gate/up rows back kGateUpDelay
             // after their QKV stage: issued at once they queue in HBM ahead of the attention's cache
             // rows and exchanges.  Measured at C3 (ms per step) with the current schedule: at once
-            // 0.569, after 0.5 / 1 / 1.5 / 2 / 2.5 us 0.571 / 0.569 / 0.560 / 0.564 / 0.576; the down
-            // rows issued here as well (blocks without attention or merge): 0.580 vs 0.576.
+            // 0.569, after 0.5 / 1 / 1.5 / 2 / 2.5 us 0.571 / 0.569 / 0.560 / 0.564 / 0.576.
             if (b >= KV * nsplit && i0 == 0)
                 while (wall_clock64() < t_p1 + kGateUpDelay<TW>) __builtin_amdgcn_s_sleep(4);
             const bool up = wave >= kPW / 2;
@@ -683,6 +689,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 if (i >= i0 && i < i1)
 #pragma unroll
                     for (int c = 0; c < NCg; c++) wg[i][c] = WR::load(W, (size_t)(r0 + i) * DIM + c * CW + lane * WR::V);
+            if (early_d && i1 == RPWg) {
+                const int rowd = b * RO + wave / WPR, cold = (wave % WPR) * (F / WPR);
+#pragma unroll
+                for (int c = 0; c < NCd; c++) wd[c] = WR::load(Ly.w2, (size_t)rowd * F + cold + c * CW + lane * WR::V);
+            }
         };
 
         // ================= P2b: merge the splits of each query head ==================
@@ -830,8 +841,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         {
             STAGE_IDS();
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (F / WPR);
-            wraw wd[NCd];
-            if (has_o) {
+            if (has_o && !early_d) {
 #pragma unroll
                 for (int c = 0; c < NCd; c++)
                     wd[c] = WR::load(Ly.w2, (size_t)row * F + col0 + c * CW + lane * WR::V);
