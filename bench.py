@@ -754,10 +754,17 @@ def main():
     warm = am.run(args.warmup) if args.warmup else np.zeros((1, 0), np.int32)
 
     # ---- timed region ----------------------------------------------------------------
+    # The persistent kernel is timed over these same steps: each launch's dispatch records a start /
+    # stop event pair (hipExtLaunchKernel), which adds no packet or wait to the stream.
+    if am.persistent:
+        am.kernel_timing(q.KT_LAYERS)
     model.ctx.synchronize()
     t1 = time.perf_counter()
     toks = am.run(args.steps)  # enqueues K steps, synchronises once at the end
     t2 = time.perf_counter()
+    if am.persistent:
+        ms_k, n_k = am.kernel_time()
+        am.kernel_timing(q.KT_NONE)
     elapsed = t2 - t1
     tok_s = args.steps / elapsed
     ms = 1000.0 * elapsed / args.steps
@@ -771,17 +778,13 @@ def main():
     persistent = am.persistent
     kernels = {}
     roofline = None
-    # ---- the persistent kernel: HIP events on the model's stream before and after each launch ----
-    # (eager steps while the probe is on; one launch per step covers the 28 layers, the final norm,
-    # the logits and the greedy keys, so its algorithmic bytes are the step's)
+    # ---- the persistent kernel over the timed steps (events recorded by each launch's dispatch) ----
+    # (one launch per step covers the 28 layers, the final norm, the logits and the greedy keys, so
+    # its algorithmic bytes are the step's)
     probe_pos0 = pos0 + args.steps
     if persistent:
-        am.kernel_timing(q.KT_LAYERS)
-        am.run(args.probe_steps)
-        ms_k, n_k = am.kernel_time()
-        am.kernel_timing(q.KT_NONE)
         avg_us = 1000.0 * ms_k / max(n_k, 1)
-        b = float(np.mean([c3_class_bytes(cfg, "decode_persistent", p) for p in range(probe_pos0, probe_pos0 + n_k)]))
+        b = float(np.mean([c3_class_bytes(cfg, "decode_persistent", p) for p in range(pos0, pos0 + n_k)]))
         gbs = b / avg_us / 1e3
         tr = traffic.get("decode_persistent", {})
         kernels["decode_persistent"] = {"avg_us": round(avg_us, 3), "launches": n_k, "bytes_per_launch": round(b),
@@ -792,11 +795,10 @@ def main():
                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": tr.get("hbm_bytes_per_launch"),
                     "traffic_source": "profiles/c3_decode_traffic.md" if tr else None, "bytes_per_launch": round(b),
                     "avg_launch_us": round(avg_us, 3), "launches_timed": n_k,
-                    "timing": "HIP events on the model's stream before and after each launch, eager steps",
+                    "timing": "HIP events recorded by each launch's own dispatch (hipExtLaunchKernel) over the timed steps",
                     "share_of_step": round(avg_us / (1000.0 * ms), 4)}
         log(f"[bench] persistent decode kernel: {avg_us:.1f} us/launch = {gbs:.0f} GB/s "
             f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak), {100 * avg_us / (1000.0 * ms):.1f}% of the step")
-        probe_pos0 += n_k
         am.use_persistent(False)  # the comparison below runs the step as separate launches
 
     # ---- the step as separate launches: its tok/s, and each kernel class timed ---------------

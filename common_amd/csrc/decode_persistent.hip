@@ -984,8 +984,9 @@ int launch_t(const DecodePersistentLaunch& a, hipStream_t st) {
     // A plain launch (a cooperative one measured ~20 us longer per step): every block must be resident
     // at once, which decode_persistent_supported checks (one 512-thread block per CU, kPB CUs) and
     // which holds while nothing else runs on the device; if some block were not, the others' waits
-    // time out, the error flag is set and the launch still completes.
-    hipLaunchKernelGGL(kern, dim3(kPB), dim3(kPT), kPadLds, st, p);
+    // time out, the error flag is set and the launch still completes.  (ar_launch: while a timing
+    // hook is installed the dispatch itself records the start / stop events.)
+    ar_launch(kern, dim3(kPB), dim3(kPT), kPadLds, st, p);
     AR_LAUNCH_CHECK();
     return AR_HIP_OK;
 }

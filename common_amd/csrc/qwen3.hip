@@ -390,12 +390,9 @@ int enqueue_step(ar_qwen3* m, bool store_logits) {
         const bool sampling = !sample_is_greedy(m->smp_mode, m->smp_temperature);
         d.final_norm = m->final_norm; d.lm_head = m->lm_head; d.vocab = c.vocab_size;
         d.logits = (store_logits || sampling) ? m->logits : nullptr; d.keys = m->am_keys;
-        if (m->timed == AR_KT_LAYERS) {  // events on the stream around the launch
+        if (m->timed == AR_KT_LAYERS) {  // the launch's dispatch records the start / stop events
             AR_TRY(timed_begin(AR_KT_LAYERS));
-            g_launch_timing = nullptr;
-            AR_HIP_TRY(hipEventRecord(timing.start, st));
             AR_TRY(launch_decode_persistent(d, st));
-            AR_HIP_TRY(hipEventRecord(timing.stop, st));
             AR_TRY(timed_end(AR_KT_LAYERS));
         } else {
             AR_TRY(launch_decode_persistent(d, st));
