@@ -400,13 +400,21 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             PK_MARK(l, 15);
             const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
             float ssq = 0.f;
+            float av[RPWq];
+#pragma unroll
+            for (int i = 0; i < RPWq; i++) {
+                float a = 0.f;
+                if (has_q) {
+#pragma unroll
+                    for (int c = 0; c < NCq; c++) a = WR::dot(wq[i][c], &xin[c * CW + lane * WR::V], a);
+                }
+                av[i] = a;
+            }
+            gemv::dpp_sum_lane63_n(av);
 #pragma unroll
             for (int i = 0; i < RPWq; i++) {
                 if (!has_q) break;
-                float a = 0.f;
-#pragma unroll
-                for (int c = 0; c < NCq; c++) a = WR::dot(wq[i][c], &xin[c * CW + lane * WR::V], a);
-                a = gemv::dpp_sum_lane63(a) * rn;
+                const float a = av[i] * rn;
                 if (lane == 63) {
                     const int row = b * RQ + wave * RPWq + i;
                     const float v = Ly.bqkv ? a + gld(Ly.bqkv, row) : a;
@@ -516,8 +524,10 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             } else {
                 const bool isq = tid >= T_S && tid - T_S < NSQ;
                 float sq = isq ? qv[0] : 0.f, sk = (tid >= T_S && !isq) ? qv[0] : 0.f;
-                sq = gemv::dpp_sum_lane63(sq);
-                sk = gemv::dpp_sum_lane63(sk);
+                float sqk[2] = {sq, sk};
+                gemv::dpp_sum_lane63_n(sqk);
+                sq = sqk[0];
+                sk = sqk[1];
                 if (lane == 63) red2[wave] = make_float2(sq, sk);
             }
             if (tid >= T_V && tid < T_S) v_new[tid - T_V] = kv16 ? (float)(KT)qv[0] : qv[0];
@@ -587,16 +597,27 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                             }
                 }
                 float sc[G][RW];  // (uniform over the wavefront)
+                {
+                    // the G x RW dot products' wavefront sums, interleaved step by step
+                    float dd[G * RW];
 #pragma unroll
-                for (int j = 0; j < RW; j++) {
-                    const bool valid = row_of(c, j) < t1;
+                    for (int j = 0; j < RW; j++)
 #pragma unroll
-                    for (int gg = 0; gg < G; gg++) {
-                        float d = 0.f;
+                        for (int gg = 0; gg < G; gg++) {
+                            float d = 0.f;
 #pragma unroll
-                        for (int e = 0; e < DPL; e++) d = fmaf(qf[gg][e], kr[j][e], d);
-                        d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gemv::dpp_sum_lane63(d)), 63));
-                        sc[gg][j] = valid ? d : -INFINITY;
+                            for (int e = 0; e < DPL; e++) d = fmaf(qf[gg][e], kr[j][e], d);
+                            dd[j * G + gg] = d;
+                        }
+                    gemv::dpp_sum_lane63_n(dd);
+#pragma unroll
+                    for (int j = 0; j < RW; j++) {
+                        const bool valid = row_of(c, j) < t1;
+#pragma unroll
+                        for (int gg = 0; gg < G; gg++) {
+                            const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dd[j * G + gg]), 63));
+                            sc[gg][j] = valid ? d : -INFINITY;
+                        }
                     }
                 }
                 if (c + 1 < nch) load_rows(kr, kc, c + 1);
@@ -819,14 +840,18 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             const float tot = block_sum(ss, red, lane, wave);
             PK_MARK(l, 22);
             const float rn = 1.0f / sqrtf(tot / (float)DIM + p.eps);
+            float av[RPWg];
 #pragma unroll
             for (int i = 0; i < RPWg; i++) {
                 float a = 0.f;
 #pragma unroll
                 for (int c = 0; c < NCg; c++) a = WR::dot(wg[i][c], &xin[c * CW + lane * WR::V], a);
-                a = gemv::dpp_sum_lane63(a) * rn;
-                if (lane == 63) rows_s[wave * RPWg + i] = a;
+                av[i] = a;
             }
+            gemv::dpp_sum_lane63_n(av);
+#pragma unroll
+            for (int i = 0; i < RPWg; i++)
+                if (lane == 63) rows_s[wave * RPWg + i] = av[i] * rn;
             lds_barrier();
             if (tid < RG) {
                 const float gt = rows_s[tid], u = rows_s[RG + tid];
@@ -933,12 +958,18 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
         unsigned long long best = 0ull;  // (lane 63)
         auto use_batch = [&](const wraw (&w)[RB][NCl], int rbase) {
+            float av[RB];
 #pragma unroll
             for (int i = 0; i < RB; i++) {
                 float a = 0.f;
 #pragma unroll
                 for (int c = 0; c < NCl; c++) a = WR::dot(w[i][c], xq[c], a);
-                a = gemv::dpp_sum_lane63(a) * rn;
+                av[i] = a;
+            }
+            gemv::dpp_sum_lane63_n(av);
+#pragma unroll
+            for (int i = 0; i < RB; i++) {
+                const float a = av[i] * rn;
                 const int r = rbase + i;
                 if (lane == 63 && r < r1) {
                     if (p.logits) p.logits[r] = a;

@@ -105,6 +105,24 @@ __device__ inline float dpp_sum_lane63(float v) {
     v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
     return v;
 }
+// N independent sums, step by step across all N: each DPP step waits two cycles for the previous
+// write of its operand, so N chains written one after the other stall on every step, while steps
+// interleaved over N values fill those cycles (each sum is added in the same order as above).
+template <int N>
+__device__ inline void dpp_sum_lane63_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = dpp_add<0xB1, 0xF>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = dpp_add<0x4E, 0xF>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = dpp_add<0x114, 0xF>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = dpp_add<0x118, 0xF>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = dpp_add<0x142, 0xA>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = dpp_add<0x143, 0xC>(v[i]);
+}
 
 __device__ inline bool better(float v1, int i1, float v2, int i2) {
     return v1 > v2 || (v1 == v2 && i1 < i2);
