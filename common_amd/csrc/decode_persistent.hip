@@ -315,6 +315,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     __shared__ float red_m[kPW][G], red_l[kPW][G];
     __shared__ __attribute__((aligned(16))) float mrg_o[SMAX][HD];  // split merge
     __shared__ float2 mrg_ml[SMAX];
+    __shared__ float mrg_w[SMAX];
     __shared__ int dead_s;
     // the layer table, read from LDS: a global load of it inside the loop would make the wavefront
     // wait for every weight load it has in flight
@@ -754,19 +755,24 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             }
             lds_barrier();
             PK_MARK(l, 20);
-            if (tid < HD) {
+            // the split weights once per block, one split per thread (each thread of the HD lanes
+            // computing all of them took ~2.7 us at 28 splits); splits past nsplit have max -inf and
+            // zero partials, so their weight is 0 and they add exact zeros below
+            if (tid < SMAX) {
                 float M = -INFINITY;
 #pragma unroll
-                for (int s = 0; s < SMAX; s++)
-                    if (s < nsplit) M = fmaxf(M, mrg_ml[s].x);
+                for (int s = 0; s < SMAX; s++) M = fmaxf(M, mrg_ml[s].x);
+                mrg_w[tid] = expf(mrg_ml[tid].x - M);
+            }
+            lds_barrier();
+            if (tid < HD) {
                 float Ls = 0.f, o = 0.f;
 #pragma unroll
-                for (int s = 0; s < SMAX; s++)
-                    if (s < nsplit) {
-                        const float w = expf(mrg_ml[s].x - M);
-                        Ls = fmaf(mrg_ml[s].y, w, Ls);
-                        o = fmaf(mrg_o[s][tid], w, o);
-                    }
+                for (int s = 0; s < SMAX; s++) {
+                    const float w = mrg_w[s];
+                    Ls = fmaf(mrg_ml[s].y, w, Ls);
+                    o = fmaf(mrg_o[s][tid], w, o);
+                }
                 ll_put(cur + OFF_A + h * HD + tid, ep, o / Ls);
             }
             PK_MARK(l, 6);
