@@ -315,7 +315,9 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     __shared__ float red_m[kPW][G], red_l[kPW][G];
     __shared__ __attribute__((aligned(16))) float mrg_o[SMAX][HD];  // split merge
     __shared__ float2 mrg_ml[SMAX];
-    __shared__ float mrg_w[SMAX];
+    constexpr int SMAX4 = (SMAX + 3) / 4 * 4;
+    __shared__ __attribute__((aligned(16))) float mrg_w[SMAX4];  // split weights and sums, 16-byte reads
+    __shared__ __attribute__((aligned(16))) float mrg_l[SMAX4];
     __shared__ int dead_s;
     // the layer table, read from LDS: a global load of it inside the loop would make the wavefront
     // wait for every weight load it has in flight
@@ -762,20 +764,31 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // the split weights once per block, one split per thread (each thread of the HD lanes
             // computing all of them took ~2.7 us at 28 splits); splits past nsplit have max -inf and
             // zero partials, so their weight is 0 and they add exact zeros below
-            if (tid < SMAX) {
+            if (tid < SMAX4) {
                 float M = -INFINITY;
 #pragma unroll
                 for (int s = 0; s < SMAX; s++) M = fmaxf(M, mrg_ml[s].x);
-                mrg_w[tid] = expf(mrg_ml[tid].x - M);
+                mrg_w[tid] = tid < SMAX ? expf(mrg_ml[tid].x - M) : 0.f;
+                mrg_l[tid] = tid < SMAX ? mrg_ml[tid].y : 0.f;
             }
             lds_barrier();
             if (tid < HD) {
+                // four weights and sums per LDS read (the bf16 instance has no registers to spare for
+                // loads issued ahead, so every read would be a round trip of its own)
                 float Ls = 0.f, o = 0.f;
 #pragma unroll
-                for (int s = 0; s < SMAX; s++) {
-                    const float w = mrg_w[s];
-                    Ls = fmaf(mrg_ml[s].y, w, Ls);
-                    o = fmaf(mrg_o[s][tid], w, o);
+                for (int s4 = 0; s4 < SMAX4 / 4; s4++) {
+                    const float4 w4 = *reinterpret_cast<const float4*>(&mrg_w[4 * s4]);
+                    const float4 l4 = *reinterpret_cast<const float4*>(&mrg_l[4 * s4]);
+                    const float w[4] = {w4.x, w4.y, w4.z, w4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int s = 4 * s4 + k;
+                        if (s < SMAX) {
+                            Ls = fmaf(lv[k], w[k], Ls);
+                            o = fmaf(mrg_o[s][tid], w[k], o);
+                        }
+                    }
                 }
                 ll_put(cur + OFF_A + h * HD + tid, ep, o / Ls);
             }
