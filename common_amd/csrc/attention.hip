@@ -35,7 +35,8 @@ namespace {
 
 constexpr int kThreads = 256;   // threads of the split (multi-block) form
 constexpr int kMaxTile = 348;   // rows per split in that form (fp32 cache; C5, 8 x 8 KV heads x 8256
-                                // rows: 24 splits of 344 rows 106.8 us/layer vs 33 of 251 rows 110.6)
+                                // rows: 24 splits of 344 rows 106.8 us/layer vs 33 of 251 rows 110.6,
+                                // 20 of 413 rows 109.7, 16 of 516 rows 118.3)
 constexpr int kMaxTile16 = 1040; // fp16 cache: the per-row work (fp16 -> fp32 conversions) makes
                                  // longer splits pay (C5, 8 x 8 KV heads x 8256 rows: 8 splits of
                                  // 1032 rows 5.55 ms/step vs 33 of 251 rows 6.32)
