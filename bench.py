@@ -346,6 +346,33 @@ TRACE_MARKS = ["layer start", "QKV input (thread 0)", "QKV stored", "attention i
 TRACE_STEPS = 24
 
 
+def profile_tree(args):
+    """The C3 model's decode step as a profile tree (common_amd.profile): the prompt through the batched
+    prefill, 5 warm-up steps, then PROFILE_STEPS steps per kernel class (the persistent launch, then
+    each class of the step as separate launches), written as the XML document the reference's
+    OperationProfileNode.load reads and printed as an indented summary and one JSON line."""
+    from common_amd import config as C
+    from common_amd import profile as prof
+    from common_amd import synthetic
+    from common_amd.qwen3 import Qwen3
+
+    cfg = C.C3_0_6B
+    prompt = synthetic.prompt_ids(C.C3_PROMPT, cfg.vocab_size, seed=args.seed)
+    model = Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=args.seed))
+    am = model.model
+    am.reset()
+    am.set_prompt(prompt)
+    am.prefill()
+    am.run(5)
+    tree = prof.decode_profile(am, PROFILE_STEPS, name="C3 decode")
+    prof.save(tree, args.profile_tree)
+    log(prof.summary(tree))
+    print(json.dumps({"profile_tree": {"xml": args.profile_tree, "tree": tree}}), flush=True)
+
+
+PROFILE_STEPS = 16
+
+
 def stage_trace(args):
     """Per-stage timeline of the persistent decode kernel at C3 (or C4 with --stage-trace c4): needs the
     diagnostic build (python -m common_amd.build --trace, loaded with AR_HIP_LIB=common_amd/lib/trace/
@@ -674,6 +701,9 @@ def main():
                     help="summarise the two counter passes' CSV output directories per decode class and exit")
     ap.add_argument("--stage-trace", choices=("c3", "c4"),
                     help="per-stage timeline of the persistent decode kernel (needs the trace build) and exit")
+    ap.add_argument("--profile-tree", metavar="XML",
+                    help="time 16 C3 decode steps per kernel class, print the profile tree and write it to XML in "
+                         "the reference's OperationProfileNode format, and exit")
     ap.add_argument("--prefill-probe", choices=("c3", "c4"),
                     help="only run that workload's prompt through the batched prefill (a warm call and "
                          "PREFILL_PROBE_RUNS more, no decode step) for rocprofv3 counter passes, and exit")
@@ -693,6 +723,9 @@ def main():
         return
     if args.stage_trace:
         stage_trace(args)
+        return
+    if args.profile_tree:
+        profile_tree(args)
         return
     sections = {x.strip() for x in args.sections.split(",") if x.strip()}
     if "c3" not in sections:  # profiling aid: only the named extra sections, one JSON line of them

@@ -354,6 +354,30 @@ JNIEXPORT jint JNICALL HIP_CLASS(qwen3MaxBatch)(JNIEnv *env, jclass c, jlong m) 
 
 JNIEXPORT jint JNICALL HIP_CLASS(qwen3VocabSize)(JNIEnv *env, jclass c, jlong m) { return QM(m)->vocab; }
 
+JNIEXPORT void JNICALL HIP_CLASS(qwen3KernelTiming)(JNIEnv *env, jclass c, jlong m, jint which) {
+    failed(env, ar_hip_qwen3_kernel_timing(QM(m)->m, which));
+}
+
+JNIEXPORT jdoubleArray JNICALL HIP_CLASS(qwen3KernelTime)(JNIEnv *env, jclass c, jlong m) {
+    double ms = 0.0;
+    int launches = 0;
+    if (failed(env, ar_hip_qwen3_kernel_time(QM(m)->m, &ms, &launches))) return NULL;
+    const jdouble v[2] = {ms, (jdouble)launches};
+    jdoubleArray out = (*env)->NewDoubleArray(env, 2);
+    if (out) (*env)->SetDoubleArrayRegion(env, out, 0, 2, v);
+    return out;
+}
+
+JNIEXPORT void JNICALL HIP_CLASS(qwen3UsePersistent)(JNIEnv *env, jclass c, jlong m, jboolean enable) {
+    failed(env, ar_hip_qwen3_use_persistent(QM(m)->m, enable ? 1 : 0));
+}
+
+JNIEXPORT jboolean JNICALL HIP_CLASS(qwen3Persistent)(JNIEnv *env, jclass c, jlong m) {
+    int active = 0;
+    if (failed(env, ar_hip_qwen3_persistent(QM(m)->m, &active))) return JNI_FALSE;
+    return active ? JNI_TRUE : JNI_FALSE;
+}
+
 JNIEXPORT void JNICALL HIP_CLASS(qwen3Destroy)(JNIEnv *env, jclass c, jlong m) {
     jqwen3 *h = QM(m);
     if (!h) return;

@@ -27,6 +27,9 @@ final class HIP {
 	static final int QK_NORM_PER_HEAD = 1;
 	static final int SAMPLE_MODEL = 0;
 	static final int SAMPLE_TOKEN = 1;
+	// kernel classes of the decode step (AR_KT_* of include/ar_hip.h)
+	static final int KT_NONE = 0, KT_LOGITS = 1, KT_GATE_UP = 2, KT_QKV = 3, KT_ATTENTION = 4, KT_DOWN = 5, KT_O = 6,
+			KT_LAYERS = 7;
 
 	/* ---- data / compute context and memory (DataContext, ComputeContext, MemoryProvider) ---- */
 	static native int deviceCount();                                   // ar_hip_device_count
@@ -79,6 +82,10 @@ final class HIP {
 	static native int qwen3MaxBatch(long model);                                 // kept by the shim
 	static native int qwen3VocabSize(long model);                                // kept by the shim
 	static native void qwen3Destroy(long model);                                 // ar_hip_qwen3_destroy
+	static native void qwen3KernelTiming(long model, int which);                 // ar_hip_qwen3_kernel_timing
+	static native double[] qwen3KernelTime(long model);                          // ar_hip_qwen3_kernel_time: {ms, launches}
+	static native void qwen3UsePersistent(long model, boolean enable);           // ar_hip_qwen3_use_persistent
+	static native boolean qwen3Persistent(long model);                           // ar_hip_qwen3_persistent
 
 	/* ---- protobuf weights (StateDictionary) ---- */
 	static native long stateDictOpen(String weightsDirectory);                   // ar_hip_state_dict_open

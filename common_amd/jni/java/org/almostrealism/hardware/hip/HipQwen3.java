@@ -16,6 +16,13 @@
  */
 package org.almostrealism.hardware.hip;
 
+import io.almostrealism.profile.OperationProfileNode;
+
+import java.util.ArrayList;
+import java.util.HashMap;
+import java.util.List;
+import java.util.Map;
+
 public class HipQwen3 implements AutoCloseable {
 	private final HipDataContext context;
 	private long model;
@@ -137,6 +144,61 @@ public class HipQwen3 implements AutoCloseable {
 
 	/** The whole prompt at once; leaves the model where prompt-length calls of next() would. */
 	public void prefill() { HIP.qwen3Prefill(handle(), null); }
+
+	// the separate-launch step's classes in step order, and their node names (common_amd/profile.py
+	// builds the same tree from Python)
+	private static final int[] STEP_CLASSES = {HIP.KT_QKV, HIP.KT_ATTENTION, HIP.KT_O, HIP.KT_GATE_UP, HIP.KT_DOWN,
+			HIP.KT_LOGITS};
+	private static final String[] STEP_NAMES = {"rmsnorm + dense qkv", "qk-norm + rope + attention",
+			"dense o + residual", "rmsnorm + dense gate/up + swiglu", "dense down + residual",
+			"rmsnorm + logits + indexOfMax"};
+
+	/**
+	 * The decode step as a profile tree in the reference's format (io.almostrealism.profile
+	 * .OperationProfileNode, base/code/src/main/java/io/almostrealism/profile/OperationProfileNode.java:
+	 * 188-460, which Qwen3.java:189-190 installs on the compiled model): steps decode steps timed per
+	 * kernel class, each node's metric holding the class's summed seconds and launch count.  Under the
+	 * root, the persistent launch (when the model runs it) and the step as separate launches, one node
+	 * per class.  The model advances steps x 7 positions (x 6 without the persistent launch); save()
+	 * writes the tree as the reference's XML.
+	 */
+	public OperationProfileNode profile(int steps) {
+		if (steps < 1) throw new IllegalArgumentException("steps must be >= 1");
+		List<OperationProfileNode> children = new ArrayList<>();
+		boolean persistent = HIP.qwen3Persistent(handle());
+		try {
+			if (persistent) {
+				children.add(timed(HIP.KT_LAYERS, "decode_persistent (layers + final norm + logits + argmax keys)",
+						steps));
+				HIP.qwen3UsePersistent(handle(), false);
+			}
+			List<OperationProfileNode> classes = new ArrayList<>();
+			for (int i = 0; i < STEP_CLASSES.length; i++) classes.add(timed(STEP_CLASSES[i], STEP_NAMES[i], steps));
+			OperationProfileNode separate = new OperationProfileNode("separate launches per stage");
+			separate.setChildren(classes);
+			children.add(separate);
+		} finally {
+			if (persistent) HIP.qwen3UsePersistent(handle(), true);
+		}
+		OperationProfileNode root = new OperationProfileNode("decode: " + steps + " steps per class");
+		root.setChildren(children);
+		return root;
+	}
+
+	private OperationProfileNode timed(int which, String name, int steps) {
+		double[] t;
+		HIP.qwen3KernelTiming(handle(), which);
+		try {
+			HIP.qwen3Run(handle(), steps);
+			t = HIP.qwen3KernelTime(handle());
+		} finally {
+			HIP.qwen3KernelTiming(handle(), HIP.KT_NONE);
+		}
+		OperationProfileNode n = new OperationProfileNode(name);
+		n.setMetricEntries(new HashMap<>(Map.of(name, t[0] / 1000.0)));
+		n.setMetricCounts(new HashMap<>(Map.of(name, (int) t[1])));
+		return n;
+	}
 
 	@Override
 	public void close() {
