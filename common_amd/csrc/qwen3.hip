@@ -1001,7 +1001,7 @@ extern "C" int ar_hip_qwen3_kernel_loop(ar_qwen3* m, int which, int reps, double
         AR_HIP_TRY(hipEventCreate(&e0));
         hipError_t e = hipEventCreate(&e1);
         int rc = AR_HIP_OK;
-        for (int i = 0; i < 2 && rc == AR_HIP_OK; i++)  // (round 0 warms the launch path)
+        for (int i = 0; i < 2 && rc == AR_HIP_OK; i++)  // (pass 0 warms the launch path)
             rc = launch_class(m, which, 0, pl, false);
         if (e == hipSuccess && rc == AR_HIP_OK) e = hipEventRecord(e0, st);
         for (int i = 0; i < reps && e == hipSuccess && rc == AR_HIP_OK; i++)
