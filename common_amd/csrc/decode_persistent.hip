@@ -59,7 +59,7 @@ constexpr int kPT = 512;           // threads per block
 constexpr int kPW = kPT / 64;      // wavefronts per block
 constexpr int kRowsPerSplit = 32;  // cache rows per split before another split is opened
 constexpr unsigned kSpinLimit = 1u << 18;  // default polls before a wait is abandoned (~0.3 s)
-constexpr int kPadLds = 64 * 1024;         // dynamic LDS that keeps a second block off each CU
+constexpr int kPadLds = 64 * 1024;         // dynamic LDS: keeps a second block off each CU, holds copied down rows
 constexpr int kMaxLayers = 64;             // layer table held in LDS
 // gate/up hold-back of the blocks without attention, wall-clock ticks (10 ns): see the O stage
 template <typename TW>
@@ -107,6 +107,7 @@ struct PParams {
 // address folds back into a generic load); the host pass compiles these bodies without running them.
 // The 16-byte weight loads are nontemporal: every weight byte is read once per step, and streaming
 // them past the caches' normal retention measured C3 0.608 -> 0.594 and C4 1.005 -> 0.975 ms per step.
+typedef __attribute__((address_space(3))) void pk_lds_void;
 typedef const __attribute__((address_space(1))) float gfloat;
 __device__ inline float4 gld4(const float* base, size_t off) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -323,6 +324,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     // wait for every weight load it has in flight
     __shared__ PLayer lay_s[kMaxLayers];
 
+    extern __shared__ __attribute__((aligned(1024))) unsigned char dyn_lds[];  // kPadLds bytes
     const int tid0 = threadIdx.x, b = blockIdx.x;
     int* dead = &dead_s;
     if (tid0 == 0) dead_s = 0;
@@ -850,6 +852,19 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             float xv[NX];
             ll_wait<NX>(cur, idx, xv, ep, dead, p.err, p.spin_limit);
             PK_MARK(l, 9);
+            // Where attention blocks hold most of the down rows (llama2.c stories110M: 192 attention
+            // blocks, down rows on the first 96), the blocks that did not take theirs early copy them
+            // into LDS (direct global-to-LDS loads, no registers) once the gate/up input is here, so they
+            // stream during the gate/up stage: 5,443 -> 5,561 tok/s; at C3, whose free blocks hold them
+            // in registers, the same copies by the attention and merge blocks cost 0.560 -> 0.571 ms.
+            constexpr bool kDownDma = sizeof(TW) == 4 && kPW * NCd * 1024 <= kPadLds && KV * SMAX >= NOB;
+            if (kDownDma && has_o && !early_d) {
+                const int rowd = b * RO + wave / WPR, cold = (wave % WPR) * (F / WPR);
+#pragma unroll
+                for (int c = 0; c < NCd; c++)
+                    __builtin_amdgcn_global_load_lds((const void*)((const float*)Ly.w2 + (size_t)rowd * F + cold + c * CW + lane * 4),
+                                                     (pk_lds_void*)(dyn_lds + (wave * NCd + c) * 1024), 16, 0, 0);
+            }
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < NX; j++) {
@@ -889,7 +904,8 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         {
             STAGE_IDS();
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (F / WPR);
-            if (has_o && !early_d) {
+            constexpr bool kDownDma = sizeof(TW) == 4 && kPW * NCd * 1024 <= kPadLds && KV * SMAX >= NOB;
+            if (has_o && !early_d && !kDownDma) {
 #pragma unroll
                 for (int c = 0; c < NCd; c++)
                     wd[c] = WR::load(Ly.w2, (size_t)row * F + col0 + c * CW + lane * WR::V);
@@ -901,6 +917,12 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             float hv[NH];
             ll_wait<NH>(cur, idx, hv, ep, dead, p.err, p.spin_limit);
             PK_MARK(l, 11);
+            if (kDownDma && has_o && !early_d) {
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's copies have landed
+#pragma unroll
+                for (int c = 0; c < NCd; c++)
+                    wd[c] = *reinterpret_cast<const wraw*>(dyn_lds + (wave * NCd + c) * 1024 + lane * 16);
+            }
 #pragma unroll
             for (int j = 0; j < NH; j++)
                 if (tid + j * kPT < F) xin[tid + j * kPT] = hv[j];
