@@ -278,6 +278,9 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
     // P3 / P5: RO (= RD) rows per block on the first NOB blocks, each split over WPR wavefronts
     constexpr int RO = pick_ro(DIM, QD, F, CW), NOB = RO ? DIM / RO : 1, WPR = RO ? kPW / RO : 1;
     constexpr int NCo = QD / (WPR * CW), NCd = F / (WPR * CW);
+    // down-row chunks per wavefront copied into the dynamic LDS after the gate/up input (see P4)
+    constexpr bool kDownDma = sizeof(TW) == 4 && kPW * NCd * 1024 <= kPadLds && KV * SMAX >= NOB;
+    constexpr int kDmaChunks = kDownDma ? NCd : 0;
     // P4: RG gate/up row pairs per block; wavefronts 0..kPW/2-1 take gate rows, the rest up rows
     constexpr int RG = F / kPB, RPWg = 2 * RG / kPW, NCg = DIM / CW;
     // inputs of DIM / QD / F values: this many per thread of the block
@@ -856,14 +859,15 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // blocks, down rows on the first 96), the blocks that did not take theirs early copy them
             // into LDS (direct global-to-LDS loads, no registers) once the gate/up input is here, so they
             // stream during the gate/up stage: 5,443 -> 5,561 tok/s; at C3, whose free blocks hold them
-            // in registers, the same copies by the attention and merge blocks cost 0.560 -> 0.571 ms.
-            constexpr bool kDownDma = sizeof(TW) == 4 && kPW * NCd * 1024 <= kPadLds && KV * SMAX >= NOB;
-            if (kDownDma && has_o && !early_d) {
+            // in registers, the same copies by the attention and merge blocks cost 0.560 -> 0.571 ms, and
+            // at C4 (bf16: 8 of 12 chunks fit) copying part of them cost 0.872 -> 0.885 ms.
+            if (kDmaChunks > 0 && has_o && !early_d) {
                 const int rowd = b * RO + wave / WPR, cold = (wave % WPR) * (F / WPR);
+                const char* src = reinterpret_cast<const char*>(Ly.w2) + ((size_t)rowd * F + cold) * sizeof(TW) + lane * 16;
 #pragma unroll
-                for (int c = 0; c < NCd; c++)
-                    __builtin_amdgcn_global_load_lds((const void*)((const float*)Ly.w2 + (size_t)rowd * F + cold + c * CW + lane * 4),
-                                                     (pk_lds_void*)(dyn_lds + (wave * NCd + c) * 1024), 16, 0, 0);
+                for (int c = 0; c < kDmaChunks; c++)
+                    __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)c * CW * sizeof(TW)),
+                                                     (pk_lds_void*)(dyn_lds + (wave * kDmaChunks + c) * 1024), 16, 0, 0);
             }
             float ss = 0.f;
 #pragma unroll
@@ -904,10 +908,9 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         {
             STAGE_IDS();
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (F / WPR);
-            constexpr bool kDownDma = sizeof(TW) == 4 && kPW * NCd * 1024 <= kPadLds && KV * SMAX >= NOB;
-            if (has_o && !early_d && !kDownDma) {
+            if (has_o && !early_d) {  // (the chunks past the copied ones)
 #pragma unroll
-                for (int c = 0; c < NCd; c++)
+                for (int c = kDmaChunks; c < NCd; c++)
                     wd[c] = WR::load(Ly.w2, (size_t)row * F + col0 + c * CW + lane * WR::V);
             }
             constexpr int NH = F / kPT > 0 ? (F + kPT - 1) / kPT : 1;
@@ -917,11 +920,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             float hv[NH];
             ll_wait<NH>(cur, idx, hv, ep, dead, p.err, p.spin_limit);
             PK_MARK(l, 11);
-            if (kDownDma && has_o && !early_d) {
+            if (kDmaChunks > 0 && has_o && !early_d) {
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's copies have landed
 #pragma unroll
-                for (int c = 0; c < NCd; c++)
-                    wd[c] = *reinterpret_cast<const wraw*>(dyn_lds + (wave * NCd + c) * 1024 + lane * 16);
+                for (int c = 0; c < kDmaChunks; c++)
+                    wd[c] = *reinterpret_cast<const wraw*>(dyn_lds + (wave * kDmaChunks + c) * 1024 + lane * 16);
             }
 #pragma unroll
             for (int j = 0; j < NH; j++)
