@@ -700,10 +700,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         // (bf16 at d 2048 has no register room for them.)
         wraw wd[NCd];
         const bool early_d = sizeof(TW) == 4 && has_o && b >= KV * nsplit && b < kPB - H;
-        // issue_o_gu(wave, lane, i0, i1): the O rows (when i0 == 0) and gate/up rows i0 .. i1-1 of the wavefront
-        auto issue_o_gu = [&](int wave, int lane, int i0, int i1) {
+        // issue_o_gu(wave, lane, i0, i1, with_o): the O rows (when with_o and i0 == 0) and gate/up rows
+        // i0 .. i1-1 of the wavefront
+        auto issue_o_gu = [&](int wave, int lane, int i0, int i1, bool with_o = true) {
             const int row = b * RO + wave / WPR, col0 = (wave % WPR) * (QD / WPR);
-            if (i0 == 0 && has_o) {
+            if (with_o && i0 == 0 && has_o) {
 #pragma unroll
                 for (int c = 0; c < NCo; c++)
                     wo[c] = WR::load(Ly.wo, (size_t)row * QD + col0 + c * CW + lane * WR::V);
@@ -712,7 +713,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // after their QKV stage: issued at once they queue in HBM ahead of the attention's cache
             // rows and exchanges.  Measured at C3 (ms per step) with the current schedule: at once
             // 0.569, after 0.5 / 1 / 1.5 / 2 / 2.5 us 0.571 / 0.569 / 0.560 / 0.564 / 0.576.
-            if (b >= KV * nsplit && i0 == 0)
+            if (b >= KV * nsplit && i0 == 0 && with_o)
                 while (wall_clock64() < t_p1 + kGateUpDelay<TW>) __builtin_amdgcn_s_sleep(4);
             const bool up = wave >= kPW / 2;
             const int r0 = b * RG + (up ? wave - kPW / 2 : wave) * RPWg;
@@ -808,7 +809,17 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // The gate/up rows (the largest stage, 24 MB at C3) are issued with the O rows, so they
             // stream while the attention chain runs instead of at the start of their own stage (the
             // merge blocks issued both before their merge).
-            if (b < kPB - H) issue_o_gu(wave, lane, 0, RPWg);
+            // Where the attention blocks are a minority of the O-row holders (fp32 weights; C3: 64 of
+            // 256), they come to the O stage last, and their O input poll queued behind all their gate/up
+            // rows; they now issue one gate/up row per wavefront before the poll and the rest after
+            // their O stores (C3 0.5602-0.5610 -> 0.5500-0.5505 ms per step; two before the poll
+            // 0.5524-0.5531; with their down rows behind the late ones 0.576; at the stories110M
+            // shape, 192 attention blocks of 256, it cost 0.1797 -> 0.1805 ms, so that shape keeps
+            // the one issue).  The bf16 instance has no register room for the split (it spills).
+            constexpr bool kAttLateGu = sizeof(TW) == 4 && KV * SMAX < NOB && RPWg > 1;
+            constexpr int kAttEarlyRows = kAttLateGu ? 1 : RPWg;
+            const bool att_late = kAttLateGu && b < KV * nsplit;
+            if (b < kPB - H) issue_o_gu(wave, lane, 0, att_late ? kAttEarlyRows : RPWg);
             else if (kMergeEarlyRows < RPWg) issue_o_gu(wave, lane, kMergeEarlyRows, RPWg);
             constexpr int NA = NXA;
             int idx[NA];
@@ -837,6 +848,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 const int r = b * RO + tid;
                 ll_put(cur + OFF_XM + r, ep, xr[r] + sum);
             }
+            if (att_late) issue_o_gu(wave, lane, kAttEarlyRows, RPWg, false);
             PK_MARK(l, 8);
         }
 
