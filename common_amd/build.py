@@ -70,7 +70,8 @@ def build_hip(jobs: int = 8, trace: bool = False):
         objs = list(ex.map(compile_one, srcs))
         objs += list(ex.map(compile_host, sorted(glob.glob(os.path.join(CSRC, "*.cpp")))))
     out = os.path.join(lib_dir, "libar_hip.so")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", *objs])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", *objs, "-L/opt/rocm/lib",
+          "-lrocblas"])
     os.replace(out + ".tmp", out)
     return out
 

@@ -73,6 +73,8 @@ struct ar_hip_ctx {
     // device address of this device's copy of the allocation-free attention entry point's scratch
     // array (ops.hip), looked up once by ar_hip_init
     float* noalloc_scratch = nullptr;
+    // rocBLAS handle of the prefill products on rocBLAS (gemm_blas.hip), created by their first call
+    void* blas = nullptr;
 };
 
 // Looks up the device addresses the operator entry points need on ctx's device (called by
@@ -285,6 +287,11 @@ struct GemmLaunch {
     int* range_flag = nullptr;  // set when an fp16 SwiGLU output value overflows (f16_range_check)
 };
 int launch_gemm(const GemmLaunch& a, hipStream_t stream);
+// The same products on rocBLAS (gemm_blas.hip; fp16 operands, ksplit 1, no bias): store / residual
+// epilogues as beta 0 / 1 on fp32 C; SwiGLU as one fp16 product of 2N outputs into `gu` (at least
+// M x 2N values) and a SwiGLU pass into O with the fp16 range check.
+int launch_gemm_blas(ar_hip_ctx* ctx, const GemmLaunch& a, uint16_t* gu, size_t gu_elems, hipStream_t stream);
+void gemm_blas_release(ar_hip_ctx* ctx);
 
 // fp32 prefill GEMM on MFMA (gemm_f32.hip): C[M x N] = A[M x K] . W[N x K]^T, all fp32.  Epilogues as
 // GemmLaunch (SwiGLU writes fp32 C).  N % 64 == 0, K % (32 * ksplit) == 0.

@@ -138,6 +138,9 @@ struct ar_qwen3 {
     int* pf_flag = nullptr;
     bool pf_w16_in_range = true;  // host copy of pf_flag[1] after the fp16 copies were made
     int pf_by_steps = 0;          // prefill calls that went through the decode step
+    int pf_gemm = AR_PREFILL_GEMM_ROCBLAS;  // ar_hip_qwen3_prefill_gemm: products of the fp16 prefill
+    uint16_t* pf_gu = nullptr;    // [R][2F] fp16 gate/up rows of the rocBLAS path
+    size_t pf_gu_elems = 0;
 
     // persistent decode step (batch 1, fp32 or bf16 weights, fp32 or fp16 cache): every layer, the final RMSNorm, the
     // logits and the greedy keys in one launch (decode_persistent.hip) after the step-begin kernel
@@ -178,7 +181,7 @@ void release(ar_qwen3* m) {
                     m->am_keys, m->smp_rng,
                     m->smp_rng_saved, m->smp_work, m->rope_tab, m->tokens, m->state, m->staging,
                     m->pf_x, m->pf_h, m->pf_qkv, m->pf_q, m->pf_act, m->pf_part, m->pf_w16, m->pf_k16, m->pf_vt16,
-                    m->pf_flag, m->pk_layers, m->pk_err};
+                    m->pf_flag, m->pf_gu, m->pk_layers, m->pk_err};
     for (void* b : bufs)
         if (b) ar_ctx_free(m->ctx, b);
     if (m->pk_ll) {  // (uncached: back to the process-wide free list once no launch uses it)
@@ -1113,6 +1116,20 @@ extern "C" int ar_hip_qwen3_use_persistent(ar_qwen3* m, int enable) {
     return AR_HIP_OK;
 }
 
+extern "C" int ar_hip_qwen3_prefill_gemm(ar_qwen3* m, int backend) {
+    AR_CHECK_ARG(m, "null model");
+    AR_CHECK_ARG(backend == AR_PREFILL_GEMM_OWN || backend == AR_PREFILL_GEMM_ROCBLAS,
+                 "prefill GEMM backend %d is not AR_PREFILL_GEMM_OWN or AR_PREFILL_GEMM_ROCBLAS", backend);
+    m->pf_gemm = backend;
+    return AR_HIP_OK;
+}
+
+extern "C" int ar_hip_qwen3_prefill_gemm_backend(ar_qwen3* m, int* backend) {
+    AR_CHECK_ARG(m && backend, "null argument");
+    *backend = m->pf_gemm;
+    return AR_HIP_OK;
+}
+
 extern "C" int ar_hip_qwen3_persistent(ar_qwen3* m, int* active) {
     AR_CHECK_ARG(m && active, "null argument");
     *active = persistent_active(m) ? 1 : 0;
@@ -1345,7 +1362,21 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
     const size_t per_layer16 = (size_t)m->qkv_dim * dd + dd * qd + 3 * FF * dd;
     AR_TRY(launch_embed_rows(m->embed, c.weight_dtype, d, m->tokens, m->S + 1, T, (int)R, m->pf_x, st));
     const size_t layer_cache = (size_t)B * c.kv_head_count * m->S * c.head_size;
-    const int so = prefill_ksplit(m, R, d, qd), sd = prefill_ksplit(m, R, d, F);
+    // rocBLAS products: O and down add into the residual rows in place (beta 1), so no k-slices;
+    // gate/up go through the stacked-weight product and a SwiGLU pass; a QKV projection with a bias
+    // stays on gemm.hip's kernel (bias in its epilogue)
+    const bool blas = m->pf_gemm == AR_PREFILL_GEMM_ROCBLAS;
+    if (blas && m->pf_gu_elems < R * 2 * FF) {
+        if (m->pf_gu) AR_TRY(ar_ctx_free(m->ctx, m->pf_gu));
+        m->pf_gu = nullptr;
+        m->pf_gu_elems = 0;
+        AR_TRY(ar_ctx_alloc(m->ctx, R * 2 * FF * 2, (void**)&m->pf_gu));
+        m->pf_gu_elems = R * 2 * FF;
+    }
+    auto gemm = [&](const GemmLaunch& g) {
+        return blas && !g.bias ? launch_gemm_blas(m->ctx, g, m->pf_gu, m->pf_gu_elems, st) : launch_gemm(g, st);
+    };
+    const int so = blas ? 1 : prefill_ksplit(m, R, d, qd), sd = blas ? 1 : prefill_ksplit(m, R, d, F);
     if ((so > 1 || sd > 1) && m->pf_part_rows < R) {
         if (m->pf_part) AR_TRY(ar_ctx_free(m->ctx, m->pf_part));
         m->pf_part = nullptr;
@@ -1368,7 +1399,7 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         GemmLaunch g;
         g.A = m->pf_h; g.lda = d; g.W = wqkv16; g.ldw = d; g.M = (int)R; g.N = m->qkv_dim; g.K = d;
         g.bias = L.bqkv; g.C = m->pf_qkv; g.ldc = m->qkv_dim; g.epilogue = GEMV_EPI_STORE; g.f16 = true;
-        AR_TRY(launch_gemm(g, st));
+        AR_TRY(gemm(g));
         PrefillPrep pp;
         pp.qkv = m->pf_qkv; pp.qkv_stride = m->qkv_dim; pp.q_norm = L.q_norm; pp.k_norm = L.k_norm;
         pp.eps = (float)c.epsilon; pp.per_head = c.qk_norm_mode == AR_QK_NORM_PER_HEAD; pp.rope_tab = m->rope_tab;
@@ -1386,14 +1417,14 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
         if (so > 1) {  // k-slices into pf_part, added into pf_x by the next row RMSNorm
             o.C = m->pf_part; o.epilogue = GEMV_EPI_STORE; o.ksplit = so;
         }
-        AR_TRY(launch_gemm(o, st));
+        AR_TRY(gemm(o));
         AR_TRY(launch_fold_rmsnorm_rows_f16(m->pf_x, m->pf_part, so > 1 ? so : 0, L.ffn_norm, m->pf_h, (int)R, d,
                                             (float)c.epsilon, rf, st));
         GemmLaunch u;
         u.A = m->pf_h; u.lda = d; u.W = w1_16; u.W2 = w3_16; u.ldw = d; u.M = (int)R;
         u.N = F; u.K = d; u.O = m->pf_act; u.ldo = F; u.epilogue = GEMV_EPI_SWIGLU; u.f16 = true;
         u.range_flag = rf;
-        AR_TRY(launch_gemm(u, st));
+        AR_TRY(gemm(u));
         GemmLaunch dn;
         dn.A = m->pf_act; dn.lda = F; dn.W = w2_16; dn.ldw = F; dn.M = (int)R; dn.N = d; dn.K = F;
         dn.C = m->pf_x; dn.ldc = d; dn.epilogue = GEMV_EPI_RESIDUAL; dn.f16 = true;
@@ -1401,7 +1432,7 @@ extern "C" int ar_hip_qwen3_prefill(ar_qwen3* m, float* logits_out) {
             dn.C = m->pf_part; dn.epilogue = GEMV_EPI_STORE; dn.ksplit = sd;
             pending = sd;
         }
-        AR_TRY(launch_gemm(dn, st));
+        AR_TRY(gemm(dn));
     }
     // A value stored as an fp16 MFMA operand left the fp16 range (outlier activations of a real
     // checkpoint): the batched pass is discarded and the prompt goes through the decode step, whose

@@ -154,6 +154,7 @@ extern "C" int ar_hip_destroy(ar_hip_ctx* ctx) {
     ar_ops_release(ctx);
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
+    gemm_blas_release(ctx);
     for (auto& kv : ctx->device_allocs) hipFree(kv.first);
     for (auto& kv : ctx->host_allocs) hipHostFree(kv.first);
     hipStreamDestroy(ctx->stream);

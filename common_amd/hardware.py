@@ -92,6 +92,8 @@ _SIGS = {
     "ar_hip_qwen3_use_fragment_gemv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "ar_hip_qwen3_fragment_gemv": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_use_persistent": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "ar_hip_qwen3_prefill_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "ar_hip_qwen3_prefill_gemm_backend": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_persistent": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_persistent_recomputed": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]),
     "ar_hip_qwen3_persistent_wait_limit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint]),

@@ -18,6 +18,8 @@ from . import hardware as hw
 from .config import DTYPE_BF16, Qwen3Config
 
 KT_NONE, KT_LOGITS, KT_GATE_UP, KT_QKV, KT_ATTENTION, KT_DOWN, KT_O, KT_LAYERS = range(8)
+# ar_hip_qwen3_prefill_gemm backends: the library's MFMA kernels, or rocBLAS gemm_ex
+PREFILL_GEMM_OWN, PREFILL_GEMM_ROCBLAS = 0, 1
 
 
 class _Cfg(ctypes.Structure):
@@ -149,6 +151,18 @@ class AutoregressiveModel:
         a = ctypes.c_int()
         hw.check(hw.lib().ar_hip_qwen3_persistent(self.handle, ctypes.byref(a)))
         return bool(a.value)
+
+    @property
+    def prefill_gemm(self) -> int:
+        """Which kernels run the bf16 prefill's projections: PREFILL_GEMM_ROCBLAS (default) or
+        PREFILL_GEMM_OWN (the library's fused MFMA kernels)."""
+        a = ctypes.c_int()
+        hw.check(hw.lib().ar_hip_qwen3_prefill_gemm_backend(self.handle, ctypes.byref(a)))
+        return a.value
+
+    @prefill_gemm.setter
+    def prefill_gemm(self, backend: int):
+        hw.check(hw.lib().ar_hip_qwen3_prefill_gemm(self.handle, int(backend)))
 
     def kernel_timing(self, which: int):
         hw.check(hw.lib().ar_hip_qwen3_kernel_timing(self.handle, which))

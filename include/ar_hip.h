@@ -238,6 +238,18 @@ int ar_hip_qwen3_prefill(ar_qwen3 *m, float *logits_out);
 /* Number of ar_hip_qwen3_prefill calls on this model that went through the decode step (fp32
  * weights, or a value outside the fp16 range on the bf16 path). */
 int ar_hip_qwen3_prefill_by_steps(ar_qwen3 *m, int *count);
+/* Which kernels run the bf16 path's prefill products (the QKV, O, gate/up and down projections of
+ * every prompt row).  No counterpart in the reference (its prompt goes through the decode step, see
+ * above); a throughput option only.  AR_PREFILL_GEMM_ROCBLAS (default): rocBLAS gemm_ex on the fp16
+ * operands with fp32 accumulation, the residual adds as beta = 1 on the fp32 rows, gate/up as one
+ * fp16 product over the stacked gate and up rows and a SwiGLU pass (a QKV projection with a bias
+ * stays on the library's kernel).  AR_PREFILL_GEMM_OWN: the library's MFMA kernels (gemm.hip, the
+ * epilogues fused, O and down split over k where that fills more CUs).  Both round to the same
+ * fp16 operands; results agree within float rounding.  Rejects other values (AR_HIP_ERR_INVALID). */
+#define AR_PREFILL_GEMM_OWN 0
+#define AR_PREFILL_GEMM_ROCBLAS 1
+int ar_hip_qwen3_prefill_gemm(ar_qwen3 *m, int backend);
+int ar_hip_qwen3_prefill_gemm_backend(ar_qwen3 *m, int *backend);
 /* Token selection of next / run / prefill.  Default: AR_SAMPLE_MODEL at temperature 0, i.e. greedy,
  * as a new AutoregressiveModel starts.  AR_SAMPLE_MODEL with another temperature is
  * AutoregressiveModel.setTemperature (AutoregressiveModel.java:258-260) with the sample function of

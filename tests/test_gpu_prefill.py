@@ -4,7 +4,9 @@ GEMM: against float64 products of the same bf16-rounded operands (fp32 accumulat
 relative; the SwiGLU epilogue rounds its output to bf16, 8e-3).  Prefill: a batched prompt must
 leave the model where sequential next() calls would (north-star bf16 tolerance 2e-2 on logits,
 since prefill feeds bf16 activations to the MFMA units), checked against the GPU decode path and
-against the FP64 oracle on the same bf16-rounded weights.
+against the FP64 oracle on the same bf16-rounded weights.  The bf16 prefill tests run on both
+product backends (ar_hip_qwen3_prefill_gemm): rocBLAS gemm_ex (the default) and the library's own
+fused MFMA kernels.
 """
 import dataclasses
 
@@ -15,11 +17,13 @@ import oracle
 from common_amd import config as C
 from common_amd import hardware as hw
 from common_amd import synthetic
+from common_amd import qwen3 as q
 from common_amd.qwen3 import Qwen3
 from conftest import rel_err
 
 pytestmark = pytest.mark.gpu
 BF16_TOL = 2e-2
+BACKENDS = [pytest.param(q.PREFILL_GEMM_ROCBLAS, id="rocblas"), pytest.param(q.PREFILL_GEMM_OWN, id="own")]
 
 
 def bf16(a):
@@ -138,8 +142,9 @@ def _bf16_cfg(base, **kw):
     return dataclasses.replace(base, weight_dtype=C.DTYPE_BF16, **kw)
 
 
+@pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("per_head,batch", [(False, 1), (True, 2)])
-def test_prefill_matches_sequential_decode_and_oracle(ctx, per_head, batch):
+def test_prefill_matches_sequential_decode_and_oracle(ctx, per_head, batch, backend):
     cfg = _bf16_cfg(C.C1_TINY, seq_len=200, max_batch=batch,
                     qk_norm_mode=C.QK_NORM_PER_HEAD if per_head else C.QK_NORM_WHOLE)
     sd = synthetic.state_dict(cfg, seed=5)
@@ -147,6 +152,8 @@ def test_prefill_matches_sequential_decode_and_oracle(ctx, per_head, batch):
     prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=20 + b) for b in range(batch)]
     with Qwen3(cfg, sd, ctx) as m:
         am = m.model
+        am.prefill_gemm = backend
+        assert am.prefill_gemm == backend
         am.reset()
         for b, p in enumerate(prompts):
             am.set_prompt(p, seq=b)
@@ -253,13 +260,15 @@ def test_prefill_fp32_c3_prompt_vs_oracle(ctx):
         assert rel_err(lgs[s], rl[s + 1]) <= 1e-4, (s, rel_err(lgs[s], rl[s + 1]))
 
 
-def test_prefill_c4_shape_matches_sequential_decode(ctx):
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_prefill_c4_shape_matches_sequential_decode(ctx, backend):
     """Qwen3-1.7B shape, bf16 weights, prefill 2048 tokens vs the decode step."""
     cfg = dataclasses.replace(C.C4_1_7B, seq_len=C.C4_PROMPT + 8)
     T = C.C4_PROMPT
     prompt = synthetic.prompt_ids(T, cfg.vocab_size, seed=4)
     with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=4), ctx) as m:
         am = m.model
+        am.prefill_gemm = backend
         am.reset()
         am.set_prompt(prompt)
         lp = am.prefill(return_logits=True)
@@ -299,7 +308,8 @@ def test_prefill_gqa4_batch8_matches_oracle(ctx):
             assert after_prefill[b, s] == rf[T + s], (b, s)
 
 
-def test_prefill_c5_shape_batch8_matches_sequential_decode(ctx):
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_prefill_c5_shape_batch8_matches_sequential_decode(ctx, backend):
     """Qwen3-4B layer shape (d2560, 32Q/8KV, hd128, F9728), batch 8, two layers
     and a 512-token context: batched prefill vs the decode step fed one token at a time."""
     T = 512
@@ -307,6 +317,7 @@ def test_prefill_c5_shape_batch8_matches_sequential_decode(ctx):
     prompts = [synthetic.prompt_ids(T, cfg.vocab_size, seed=50 + b) for b in range(8)]
     with Qwen3(cfg, synthetic.iter_state_dict(cfg, seed=5), ctx) as m:
         am = m.model
+        am.prefill_gemm = backend
         am.reset()
         for b, p in enumerate(prompts):
             am.set_prompt(p, seq=b)
@@ -377,9 +388,10 @@ def test_fp16_kv_cache_c5_layer_shape_close_to_fp32_cache(ctx):
         assert rel_err(out[C.DTYPE_F16][b], out[C.DTYPE_F32][b]) <= BF16_TOL, b
 
 
-def _prefill_vs_oracle(ctx, cfg, sd, prompts, steps):
+def _prefill_vs_oracle(ctx, cfg, sd, prompts, steps, backend=q.PREFILL_GEMM_ROCBLAS):
     with Qwen3(cfg, sd, ctx) as m:
         am = m.model
+        am.prefill_gemm = backend
         am.reset()
         for b, p in enumerate(prompts):
             am.set_prompt(p, seq=b)
@@ -398,8 +410,9 @@ def _prefill_vs_oracle(ctx, cfg, sd, prompts, steps):
     return by_steps
 
 
-@pytest.mark.parametrize("where", ["ffn_norm_gain", "swiglu_output"])
-def test_prefill_fp16_overflow_takes_the_decode_step(ctx, where):
+@pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("where", ["ffn_norm_gain", "swiglu_output", "gate_value"])
+def test_prefill_fp16_overflow_takes_the_decode_step(ctx, where, backend):
     """Activations past the fp16 range (a real checkpoint's outliers): a post-attention RMSNorm gain
     of 2^17 (normalised rows ~1e5) or gate/up weights scaled by 2^11 (SwiGLU outputs ~1e6).  The
     batched pass sees the overflow and the prompt goes through the decode step: logits and tokens
@@ -408,11 +421,18 @@ def test_prefill_fp16_overflow_takes_the_decode_step(ctx, where):
     sd = synthetic.state_dict(cfg, seed=31)
     if where == "ffn_norm_gain":
         sd["model.layers.0.post_attention_layernorm.weight"] = sd["model.layers.0.post_attention_layernorm.weight"] * 2.0 ** 17
-    else:
+    elif where == "swiglu_output":
         for k in ("mlp.gate_proj.weight", "mlp.up_proj.weight"):
             sd["model.layers.1." + k] = sd["model.layers.1." + k] * 2.0 ** 11
+    else:  # gate pre-activations past the fp16 range with small up values: the rocBLAS path's fp16
+        # gate/up rows overflow although the SwiGLU outputs would fit
+        # (gate rows ~4e4 rms, up rows ~2e-2: outputs up to ~1e4)
+        sd["model.layers.1.mlp.gate_proj.weight"] = sd["model.layers.1.mlp.gate_proj.weight"] * 2.0 ** 17
+        sd["model.layers.1.mlp.up_proj.weight"] = sd["model.layers.1.mlp.up_proj.weight"] * 2.0 ** -4
     prompts = [synthetic.prompt_ids(40, cfg.vocab_size, seed=32 + b) for b in range(2)]
-    assert _prefill_vs_oracle(ctx, cfg, sd, prompts, 4) == 1
+    by_steps = _prefill_vs_oracle(ctx, cfg, sd, prompts, 4, backend)
+    # (the own kernels' fused epilogue keeps gate and up in fp32: only the SwiGLU output is checked)
+    assert by_steps == (0 if where == "gate_value" and backend == q.PREFILL_GEMM_OWN else 1)
 
 
 def test_prefill_tiny_weights_stay_on_the_batched_path(ctx):
@@ -426,3 +446,27 @@ def test_prefill_tiny_weights_stay_on_the_batched_path(ctx):
     assert np.mean(np.abs(w) < 2.0 ** -17) > 0.5
     prompts = [synthetic.prompt_ids(40, cfg.vocab_size, seed=34)]
     assert _prefill_vs_oracle(ctx, cfg, sd, prompts, 4) == 0
+
+
+def test_prefill_backends_agree_and_reject_unknown(ctx):
+    """The two product backends on one prompt (C1 shape, bf16, batch 2): logits within float
+    rounding of each other (same fp16 operands, fp32 accumulation in both; the rocBLAS path rounds
+    gate and up to fp16 before the SwiGLU), and an unknown backend is refused."""
+    cfg = _bf16_cfg(C.C1_TINY, seq_len=160, max_batch=2)
+    sd = synthetic.state_dict(cfg, seed=41)
+    prompts = [synthetic.prompt_ids(130, cfg.vocab_size, seed=42 + b) for b in range(2)]
+    out = {}
+    with Qwen3(cfg, sd, ctx) as m:
+        am = m.model
+        with pytest.raises(hw.HardwareException) as e:
+            am.prefill_gemm = 7
+        assert e.value.code == hw.AR_HIP_ERR_INVALID
+        assert am.prefill_gemm == q.PREFILL_GEMM_ROCBLAS  # the default, unchanged by the refused call
+        for backend in (q.PREFILL_GEMM_OWN, q.PREFILL_GEMM_ROCBLAS):
+            am.prefill_gemm = backend
+            am.reset()
+            for b, p in enumerate(prompts):
+                am.set_prompt(p, seq=b)
+            out[backend] = am.prefill(return_logits=True)
+            assert am.prefill_by_steps() == 0
+    assert rel_err(out[q.PREFILL_GEMM_ROCBLAS], out[q.PREFILL_GEMM_OWN]) <= 5e-3
