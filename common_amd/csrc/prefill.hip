@@ -526,7 +526,10 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
     uint16_t* const ks = reinterpret_cast<uint16_t*>(lds);              // [2][SK][KROW]
     uint16_t* const vs = ks + 2 * L::K_HALVES;                          // [2][HD][VS]
 
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, h2 = lane >> 5, lq = lane & 31;
+    // (w through readfirstlane: the compiler then treats everything derived from the wavefront index
+    // — the key slice, the query rows, the diagonal-tile test — as uniform and branches on it)
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, h2 = lane >> 5,
+              lq = lane & 31;
     const int slice = w / NG, wq = w % NG;
     // block -> (unit, query block); unit -> (pair = sequence*KV + g, head subset)
     const int units = p.pairs * p.nsub;
@@ -619,19 +622,21 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
         for (int kk = 0; kk < HD / 16; kk++)
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const halfx8*>(kt + kk * 16), qf[kk], s, 0, 0,
                                                        0);
-        float mx = -INFINITY;
+        // The causal mask only on the tiles that cross the diagonal or the prompt's end (a uniform
+        // branch); the scale c2 > 0 is applied to the maximum and inside the exponent's FMA, so the
+        // other tiles spend four vector operations and one exp2 per score.
         const bool edge = (kh + 31 > row0) || (kh + 31 >= p.T);
+        if (edge) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            float v = s[r] * c2;
-            if (edge) {
+            for (int r = 0; r < 16; r++) {
                 const int key = kh + (r >> 2) * 8 + h2 * 4 + (r & 3);
-                if (key > myq || key >= p.T) v = -INFINITY;
+                if (key > myq || key >= p.T) s[r] = -INFINITY;
             }
-            s[r] = v;
-            mx = fmaxf(mx, v);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float mx = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c2;
         if (__ballot(mx > m + 8.0f)) {
             const float m_new = fmaxf(m, mx);
             const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
@@ -647,7 +652,7 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
         float sum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const float e = __builtin_amdgcn_exp2f(s[r] - mu);
+            const float e = __builtin_amdgcn_exp2f(fmaf(s[r], c2, -mu));
             s[r] = e;
             sum += e;
         }
