@@ -133,7 +133,8 @@ def c4_section(args):
         "prefill": {"tokens": T, "ms": round(1000 * t_pre, 3), "tok_s": round(T / t_pre, 1),
                     "tflop": round(flops / 1e12, 3), "achieved_tflops": round(flops / t_pre / 1e12, 1),
                     "mfma_frac": round(flops / t_pre / 1e12 / MFMA_PEAK_TFLOPS, 4),
-                    "path": "fp16 MFMA GEMMs on exact fp16 copies of the bf16 weights + causal flash attention"},
+                    "path": "fp16 products on exact fp16 copies of the bf16 weights (rocBLAS gemm_ex, the default "
+                            "ar_hip_qwen3_prefill_gemm backend) + causal flash attention"},
         "decode": {"tokens": n_dec - warm, "tok_s": round(dec_tok_s, 2), "ms_per_token": round(1000 * t_dec / (n_dec - warm), 4),
                    "algorithmic_bytes_per_token": round(bytes_tok),
                    "hbm_frac": round(bytes_tok * dec_tok_s / 1e9 / HBM_PEAK_GBS, 4)},

@@ -378,6 +378,16 @@ JNIEXPORT jboolean JNICALL HIP_CLASS(qwen3Persistent)(JNIEnv *env, jclass c, jlo
     return active ? JNI_TRUE : JNI_FALSE;
 }
 
+JNIEXPORT void JNICALL HIP_CLASS(qwen3PrefillGemm)(JNIEnv *env, jclass c, jlong m, jint backend) {
+    failed(env, ar_hip_qwen3_prefill_gemm(QM(m)->m, backend));
+}
+
+JNIEXPORT jint JNICALL HIP_CLASS(qwen3PrefillGemmBackend)(JNIEnv *env, jclass c, jlong m) {
+    int backend = 0;
+    if (failed(env, ar_hip_qwen3_prefill_gemm_backend(QM(m)->m, &backend))) return -1;
+    return backend;
+}
+
 JNIEXPORT void JNICALL HIP_CLASS(qwen3Destroy)(JNIEnv *env, jclass c, jlong m) {
     jqwen3 *h = QM(m);
     if (!h) return;

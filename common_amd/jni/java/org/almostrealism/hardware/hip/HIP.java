@@ -30,6 +30,8 @@ final class HIP {
 	// kernel classes of the decode step (AR_KT_* of include/ar_hip.h)
 	static final int KT_NONE = 0, KT_LOGITS = 1, KT_GATE_UP = 2, KT_QKV = 3, KT_ATTENTION = 4, KT_DOWN = 5, KT_O = 6,
 			KT_LAYERS = 7;
+	// prefill product backends (AR_PREFILL_GEMM_* of include/ar_hip.h)
+	static final int PREFILL_GEMM_OWN = 0, PREFILL_GEMM_ROCBLAS = 1;
 
 	/* ---- data / compute context and memory (DataContext, ComputeContext, MemoryProvider) ---- */
 	static native int deviceCount();                                   // ar_hip_device_count
@@ -86,6 +88,8 @@ final class HIP {
 	static native double[] qwen3KernelTime(long model);                          // ar_hip_qwen3_kernel_time: {ms, launches}
 	static native void qwen3UsePersistent(long model, boolean enable);           // ar_hip_qwen3_use_persistent
 	static native boolean qwen3Persistent(long model);                           // ar_hip_qwen3_persistent
+	static native void qwen3PrefillGemm(long model, int backend);                // ar_hip_qwen3_prefill_gemm
+	static native int qwen3PrefillGemmBackend(long model);                       // ar_hip_qwen3_prefill_gemm_backend
 
 	/* ---- protobuf weights (StateDictionary) ---- */
 	static native long stateDictOpen(String weightsDirectory);                   // ar_hip_state_dict_open

@@ -145,6 +145,12 @@ public class HipQwen3 implements AutoCloseable {
 	/** The whole prompt at once; leaves the model where prompt-length calls of next() would. */
 	public void prefill() { HIP.qwen3Prefill(handle(), null); }
 
+	/** Which kernels run the bf16 prefill's projections: HIP.PREFILL_GEMM_ROCBLAS, the default, or
+	 *  HIP.PREFILL_GEMM_OWN, the library's fused MFMA kernels; results agree within float rounding. */
+	public void setPrefillGemm(int backend) { HIP.qwen3PrefillGemm(handle(), backend); }
+
+	public int getPrefillGemm() { return HIP.qwen3PrefillGemmBackend(handle()); }
+
 	// the separate-launch step's classes in step order, and their node names (common_amd/profile.py
 	// builds the same tree from Python)
 	private static final int[] STEP_CLASSES = {HIP.KT_QKV, HIP.KT_ATTENTION, HIP.KT_O, HIP.KT_GATE_UP, HIP.KT_DOWN,
