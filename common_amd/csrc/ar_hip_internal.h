@@ -248,6 +248,16 @@ __device__ inline float xor32(float v, int lane) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float((lane & 32) ? r[0] : r[1]);
 }
+// max / sum of the values held by lanes l and l ^ 32, in every lane (the swap's two results are the
+// lower and the upper half in every lane, so no lane select; the sum is lower + upper in both lanes)
+__device__ inline float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // fp32 values from 65520 up (and infinities) round to an infinite fp16.  The prefill path stores
 // its MFMA operands as fp16; every conversion checks this and marks *range_flag (when given), so the

@@ -636,7 +636,7 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
         float mx = s[0];
 #pragma unroll
         for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c2;
+        mx = max_xor32(mx) * c2;
         if (__ballot(mx > m + 8.0f)) {
             const float m_new = fmaxf(m, mx);
             const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
@@ -656,7 +656,7 @@ __global__ __launch_bounds__(512) void flash_prefill_kernel(FlashParams p) {
             s[r] = e;
             sum += e;
         }
-        l += sum + __shfl_xor(sum, 32, 64);
+        l += sum_xor32(sum);
         // O^T += V^T P^T over the 32 keys, in register order: k-step kk, slot i <-> register 8kk+i
         // <-> key kh + 16kk + 8*(i/4) + (l/32)*4 + i%4
         const uint16_t* vt0 = vs + buf * L::V_HALVES + lq * L::VS + 32 * slice + h2 * 4;
