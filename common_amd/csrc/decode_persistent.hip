@@ -712,7 +712,8 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             // The blocks that are not busy with attention hold the gate/up rows back kGateUpDelay
             // after their QKV stage: issued at once they queue in HBM ahead of the attention's cache
             // rows and exchanges.  Measured at C3 (ms per step) with the current schedule: at once
-            // 0.569, after 0.5 / 1 / 1.5 / 2 / 2.5 us 0.571 / 0.569 / 0.560 / 0.564 / 0.576.
+            // 0.569, after 0.5 / 1 / 1.5 / 2 / 2.5 us 0.571 / 0.569 / 0.560 / 0.564 / 0.576; with the
+            // attention blocks' late gate/up rows, 1 / 1.5 / 2 us 0.555 / 0.552 / 0.559.
             if (b >= KV * nsplit && i0 == 0 && with_o)
                 while (wall_clock64() < t_p1 + kGateUpDelay<TW>) __builtin_amdgcn_s_sleep(4);
             const bool up = wave >= kPW / 2;
