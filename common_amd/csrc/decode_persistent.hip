@@ -737,7 +737,11 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
         // merge, they arrive last of all and hold up every block's gate/up input (C3: 0.668 ->
         // 0.635 ms per step).  Where the rows and the merge's words do not fit in registers together
         // (bf16 at d 2048: 96 VGPRs of gate/up rows, 28 splits), they follow the merge.
-        constexpr int kMergeEarlyRows = RPWg * NCg <= 12 ? RPWg : RPWg / 3;
+        // With fp32 weights and the attention blocks a minority of the O-row holders (C3), the merge
+        // blocks keep one gate/up row per wavefront before the merge and issue the rest after their O
+        // stores, as the attention blocks do (C3 0.5512-0.5518 -> 0.5505-0.5508 ms per step).
+        constexpr bool kMergeLate = sizeof(TW) == 4 && KV * SMAX < NOB && RPWg > 1;
+        constexpr int kMergeEarlyRows = kMergeLate ? 1 : RPWg * NCg <= 12 ? RPWg : RPWg / 3;
         if (b >= kPB - H) {  // one block per query head (never an attention block)
             STAGE_IDS();
             issue_o_gu(wave, lane, 0, kMergeEarlyRows);
@@ -822,7 +826,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
             constexpr int kAttEarlyRows = kAttLateGu ? 1 : RPWg;
             const bool att_late = kAttLateGu && b < KV * nsplit;
             if (b < kPB - H) issue_o_gu(wave, lane, 0, att_late ? kAttEarlyRows : RPWg);
-            else if (kMergeEarlyRows < RPWg) issue_o_gu(wave, lane, kMergeEarlyRows, RPWg);
+            else if (kMergeEarlyRows < RPWg && !kMergeLate) issue_o_gu(wave, lane, kMergeEarlyRows, RPWg);
             constexpr int NA = NXA;
             int idx[NA];
 #pragma unroll
@@ -851,6 +855,7 @@ __global__ __launch_bounds__(kPT, 1) void decode_persistent_kernel(PParams p) {
                 ll_put(cur + OFF_XM + r, ep, xr[r] + sum);
             }
             if (att_late) issue_o_gu(wave, lane, kAttEarlyRows, RPWg, false);
+            else if (kMergeLate && b >= kPB - H) issue_o_gu(wave, lane, kMergeEarlyRows, RPWg, false);
             PK_MARK(l, 8);
         }
 
